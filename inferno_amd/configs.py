@@ -1,0 +1,146 @@
+"""The five BASELINE.json workloads as seeded synthetic GPU-resident layers.
+
+Seeds: 1000 + config index; sub-streams per tensor (x, router, bias, gate,
+up, down, shared gate/up/down) and per layer. Weights are N(0, 0.02)
+quantised on the device (inferno_synth_quantized); activations N(0, 1).
+"""
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from ._lib import BF16, F32, Q2_K, Q3_K, Q4_K, Q8_0, SCORE_SIGMOID, SCORE_SOFTMAX
+from . import ops
+
+
+@dataclass
+class Config:
+    name: str
+    index: int
+    hidden: int
+    experts: int
+    intermediate: int
+    top_k: int
+    quants: tuple              # routed kind per layer
+    score_fn: int
+    norm: bool
+    scale: float
+    bias_std: float            # 0 = no correction bias
+    shared_intermediate: int   # 0 = no shared expert
+    x_dtype: torch.dtype
+    tokens: tuple
+    zipf: float = 0.0          # >0: bias calibrated so expert load follows Zipf(s)
+    rms_eps: float = 1e-6
+    notes: str = ""
+    weight_std: float = 0.02
+
+    @property
+    def seed(self):
+        return 1000 + self.index
+
+    @property
+    def layers(self):
+        return len(self.quants)
+
+
+CONFIGS = {
+    "c1": Config("c1_q4k_h2048_e64_top8_softmax", 0, 2048, 64, 768, 8, (Q4_K,), SCORE_SOFTMAX,
+                 True, 1.0, 0.0, 0, torch.float32, (1, 16)),
+    "c2": Config("c2_glm_q2k_h6144_e256_top8_sigmoid_decode", 1, 6144, 256, 2048, 8, (Q2_K,),
+                 SCORE_SIGMOID, True, 2.5, 0.1, 2048, torch.bfloat16, (1,)),
+    "c3": Config("c3_glm_q3k_prefill_t512", 2, 6144, 256, 2048, 8, (Q3_K,), SCORE_SIGMOID, True,
+                 2.5, 0.1, 2048, torch.bfloat16, (512,)),
+    "c4": Config("c4_laguna_s_4layer_q2k_q3k_top10_softmax", 3, 4096, 128, 1536, 10,
+                 (Q2_K, Q2_K, Q3_K, Q3_K), SCORE_SOFTMAX, True, 1.0, 0.0, 1536, torch.bfloat16,
+                 (1, 32)),
+    "c5": Config("c5_glm_q2k_prefill_t4096_zipf", 4, 6144, 256, 2048, 8, (Q2_K,), SCORE_SIGMOID,
+                 True, 2.5, 0.1, 2048, torch.bfloat16, (4096,), zipf=1.1),
+}
+
+# sub-stream ids
+_X, _ROUTER, _BIAS, _GATE, _UP, _DOWN, _SG, _SU, _SD, _NORM = range(10)
+
+
+def stream_seed(cfg, layer, which, variant=0):
+    return (cfg.seed << 20) | (layer << 12) | (variant << 4) | which
+
+
+@dataclass
+class LayerTensors:
+    quant: int
+    router: torch.Tensor
+    bias: torch.Tensor
+    gate: torch.Tensor
+    up: torch.Tensor
+    down: torch.Tensor
+    shared: tuple = None
+    norm_w: torch.Tensor = None
+    layer: ops.MoELayer = field(default=None, repr=False)
+
+
+def make_input(cfg, T, variant=0, device="cuda"):
+    return ops.synth_normal(stream_seed(cfg, 0, _X, variant), 1.0, T * cfg.hidden,
+                            dtype=cfg.x_dtype, device=device).view(T, cfg.hidden)
+
+
+def build_layer(cfg, layer=0, device="cuda", max_tokens=1, bias=None):
+    H, E, I = cfg.hidden, cfg.experts, cfg.intermediate
+    q = cfg.quants[layer]
+    ws = cfg.weight_std
+    router = ops.synth_normal(stream_seed(cfg, layer, _ROUTER), ws, E * H, device=device).view(E, H)
+    if bias is None and cfg.bias_std > 0:
+        bias = ops.synth_normal(stream_seed(cfg, layer, _BIAS), cfg.bias_std, E, device=device)
+    gate = ops.synth_quantized(q, stream_seed(cfg, layer, _GATE), ws, E * I, H, device)
+    up = ops.synth_quantized(q, stream_seed(cfg, layer, _UP), ws, E * I, H, device)
+    down = ops.synth_quantized(q, stream_seed(cfg, layer, _DOWN), ws, E * H, I, device)
+    shared = None
+    Is = cfg.shared_intermediate
+    if Is:
+        shared = (ops.synth_quantized(Q8_0, stream_seed(cfg, layer, _SG), ws, Is, H, device),
+                  ops.synth_quantized(Q8_0, stream_seed(cfg, layer, _SU), ws, Is, H, device),
+                  ops.synth_quantized(Q8_0, stream_seed(cfg, layer, _SD), ws, H, Is, device))
+    norm_w = 1.0 + ops.synth_normal(stream_seed(cfg, layer, _NORM), 0.1, H, device=device)
+    lt = LayerTensors(q, router, bias, gate, up, down, shared, norm_w)
+    lt.layer = ops.MoELayer(
+        hidden=H, experts=E, intermediate=I, top_k=cfg.top_k, quant=q, down_quant=q,
+        score_fn=cfg.score_fn, norm_topk_prob=cfg.norm, routed_scaling_factor=cfg.scale,
+        router=router, router_bias=bias, gate=gate, up=up, down=down,
+        shared_intermediate=Is,
+        shared_gate=shared[0] if shared else None, shared_up=shared[1] if shared else None,
+        shared_down=shared[2] if shared else None, max_tokens=max_tokens)
+    return lt
+
+
+def zipf_bias(cfg, logits, iters=200):
+    """Correction bias that makes top-k load follow Zipf(cfg.zipf).
+
+    Target share of rank r is r^-s normalised; an expert can take at most one
+    slot per token, so targets are capped at T and the excess is spread over
+    the rest; experts whose target is below half a slot get none. The bias is
+    fitted by multiplicative updates on the host (numpy) from the device
+    logits of the actual input.
+    """
+    T, E = logits.shape
+    k = cfg.top_k
+    A = T * k
+    p = np.arange(1, E + 1, dtype=np.float64) ** (-cfg.zipf)
+    target = A * p / p.sum()
+    for _ in range(10):
+        over = target > T
+        if not over.any():
+            break
+        excess = (target[over] - T).sum()
+        target[over] = T
+        rest = ~over
+        target[rest] += excess * target[rest] / target[rest].sum()
+    target[target < 0.5] = 0.0
+    target *= A / target.sum()
+    score = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
+    bias = np.where(target > 0, 0.0, -4.0)
+    for _ in range(iters):
+        sel = score + bias
+        top = np.argpartition(-sel, k - 1, axis=1)[:, :k]
+        count = np.bincount(top.reshape(-1), minlength=E).astype(np.float64)
+        live = target > 0
+        bias[live] += 0.05 * (np.log(target[live] + 1) - np.log(count[live] + 1))
+    return bias.astype(np.float32)

@@ -1,0 +1,444 @@
+// extern "C" entry points: argument validation (mirroring the reference's
+// Err paths, e.g. crates/backend/src/metal/gguf_moe.rs:84-121 and
+// crates/backend/src/metal/moe.rs:582-623), workspace carving and kernel
+// sequencing. No function allocates device memory or synchronises.
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "quantize.hpp"
+
+namespace inferno {
+
+thread_local std::string g_last_error;
+void set_error(const std::string& msg) { g_last_error = msg; }
+void clear_error() { g_last_error.clear(); }
+
+namespace {
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
+
+// Carves aligned sub-buffers out of a caller workspace.
+struct Carver {
+  char* base;
+  size_t used = 0;
+  template <typename T>
+  T* take(size_t count) {
+    T* p = reinterpret_cast<T*>(base ? base + used : nullptr);
+    used += align_up(count * sizeof(T));
+    return p;
+  }
+};
+
+bool is_routed_quant(int q) {
+  return q == INFERNO_Q2_K || q == INFERNO_Q3_K || q == INFERNO_Q4_K;
+}
+bool is_down_quant(int q) { return is_routed_quant(q) || q == INFERNO_Q6_K; }
+
+// Bytes of one expert matrix of `rows` rows over `cols` values.
+size_t matrix_bytes(int quant, size_t rows, size_t cols) {
+  return rows * (cols / size_t(block_values(quant))) * size_t(block_bytes(quant));
+}
+
+int check_len(const char* label, size_t got, size_t experts, size_t stride) {
+  if (got != experts * stride) {
+    set_error(std::string("GGUF ") + label + " expert payload must contain " +
+              std::to_string(experts * stride) + " bytes, got " + std::to_string(got));
+    return INFERNO_ERR_SIZE;
+  }
+  return INFERNO_OK;
+}
+
+struct MoeScratch {
+  uint32_t* offsets;
+  uint32_t* sorted;
+  uint32_t* active;
+  float* h;
+  float* y;
+};
+
+MoeScratch carve_moe(Carver& c, size_t T, size_t k, size_t E, size_t H, size_t I) {
+  MoeScratch m;
+  m.offsets = c.take<uint32_t>(E + 1);
+  m.sorted = c.take<uint32_t>(T * k);
+  m.active = c.take<uint32_t>(E + 1);
+  m.h = c.take<float>(T * k * I);
+  m.y = c.take<float>(T * k * H);
+  return m;
+}
+
+int validate_moe(int quant, int down_quant, size_t gate_bytes, size_t up_bytes,
+                 size_t down_bytes, size_t T, size_t k, size_t E, size_t H, size_t I) {
+  INF_CHECK_ARG(is_routed_quant(quant), "routed gate/up experts must be Q2_K, Q3_K or Q4_K");
+  INF_CHECK_ARG(is_down_quant(down_quant), "routed down experts must be Q2_K, Q3_K, Q4_K or Q6_K");
+  if (T == 0 || k == 0 || k > E) {
+    set_error("GGUF MoE routing dimensions are invalid: tokens=" + std::to_string(T) +
+              ", top_k=" + std::to_string(k) + ", experts=" + std::to_string(E));
+    return INFERNO_ERR_INVALID;
+  }
+  INF_CHECK_ARG(E <= size_t(kMaxExperts), "at most 256 experts are supported");
+  INF_CHECK_ARG(k <= size_t(kMaxTopK), "top_k must be at most 16");
+  if (H % kKBlock || I % kKBlock || H == 0 || I == 0) {
+    set_error("GGUF MoE dimensions must use 256-wide quant blocks, got in=" + std::to_string(H) +
+              ", intermediate=" + std::to_string(I));
+    return INFERNO_ERR_INVALID;
+  }
+  INF_CHECK_ARG(T * k < (size_t(1) << 31), "too many assignments");
+  int st;
+  if ((st = check_len("gate", gate_bytes, E, matrix_bytes(quant, I, H)))) return st;
+  if ((st = check_len("up", up_bytes, E, matrix_bytes(quant, I, H)))) return st;
+  if ((st = check_len("down", down_bytes, E, matrix_bytes(down_quant, H, I)))) return st;
+  return INFERNO_OK;
+}
+
+// Routed part shared by inferno_gguf_moe and the layer: dispatch, gate/up,
+// down. Leaves per-assignment down rows (already routing-weighted) in m.y.
+int run_routed(hipStream_t s, int quant, int down_quant, const void* gate, const void* up,
+               const void* down, const void* x, int x_dtype, const uint32_t* ids,
+               const float* w, size_t T, size_t k, size_t E, size_t H, size_t I,
+               const MoeScratch& m) {
+  int st;
+  if ((st = launch_dispatch(s, ids, T, k, E, m.offsets, m.sorted, m.active))) return st;
+  if ((st = launch_gemv_gate_up_routed(s, quant, gate, up, x, x_dtype, m.offsets, m.sorted,
+                                       m.active, w, T, k, E, H, I, m.h)))
+    return st;
+  return launch_gemv_down_routed(s, down_quant, down, m.h, m.offsets, m.sorted, m.active, T, k,
+                                 E, H, I, m.y);
+}
+
+}  // namespace
+}  // namespace inferno
+
+using namespace inferno;
+
+extern "C" {
+
+const char* inferno_last_error(void) { return g_last_error.c_str(); }
+
+int inferno_block_bytes(int quant) { return block_bytes(quant); }
+int inferno_block_values(int quant) { return block_values(quant); }
+
+int inferno_stream_synchronize(void* stream) {
+  clear_error();
+  INF_HIP(hipStreamSynchronize(as_stream(stream)));
+  return INFERNO_OK;
+}
+
+int inferno_gguf_dequantize(void* stream, int quant, const void* blocks, size_t n_blocks,
+                            float* out) {
+  clear_error();
+  INF_CHECK_ARG(block_bytes(quant) > 0, "unknown quant kind");
+  INF_CHECK_ARG(n_blocks == 0 || (blocks && out), "null pointer");
+  return launch_dequant(as_stream(stream), quant, blocks, n_blocks, out);
+}
+
+int inferno_router_logits(void* stream, const void* x, int x_dtype, const float* w_router,
+                          size_t T, size_t H, size_t E, float* logits) {
+  clear_error();
+  INF_CHECK_ARG(x_dtype == INFERNO_F32 || x_dtype == INFERNO_BF16, "x dtype must be F32 or BF16");
+  INF_CHECK_ARG(H > 0 && H % 4 == 0, "hidden size must be a positive multiple of 4");
+  INF_CHECK_ARG(E > 0, "expert count must be positive");
+  INF_CHECK_ARG(T == 0 || (x && w_router && logits), "null pointer");
+  return launch_router_logits(as_stream(stream), x, x_dtype, w_router, T, H, E, logits);
+}
+
+int inferno_moe_router_topk(void* stream, const float* logits, const float* bias, size_t T,
+                            size_t E, size_t k, int score_fn, int norm_topk_prob,
+                            float routed_scaling_factor, uint32_t* expert_ids,
+                            float* expert_weights, uint32_t* token_indices) {
+  clear_error();
+  INF_CHECK_ARG(T > 0 && E > 0, "MoE router top-k requires non-zero token_count and expert_count");
+  if (k == 0 || k > size_t(kMaxTopK)) {
+    set_error("MoE router top-k supports 1..=16 selected experts, got " + std::to_string(k));
+    return INFERNO_ERR_INVALID;
+  }
+  if (k > E) {
+    set_error("MoE router top-k " + std::to_string(k) + " exceeds expert_count " +
+              std::to_string(E));
+    return INFERNO_ERR_INVALID;
+  }
+  if (E > size_t(kMaxExperts)) {
+    set_error("MoE router top-k supports at most 256 experts, got " + std::to_string(E));
+    return INFERNO_ERR_INVALID;
+  }
+  INF_CHECK_ARG(score_fn == INFERNO_SCORE_SIGMOID || score_fn == INFERNO_SCORE_SOFTMAX,
+                "score_fn must be SIGMOID or SOFTMAX");
+  INF_CHECK_ARG(std::isfinite(routed_scaling_factor), "MoE router routed scaling factor must be finite");
+  INF_CHECK_ARG(logits && expert_ids && expert_weights, "null pointer");
+  return launch_router_topk(as_stream(stream), logits, bias, T, E, k, score_fn, norm_topk_prob,
+                            routed_scaling_factor, expert_ids, expert_weights, token_indices);
+}
+
+int inferno_moe_dispatch(void* stream, const uint32_t* expert_ids, size_t T, size_t k, size_t E,
+                         uint32_t* offsets, uint32_t* sorted, uint32_t* active) {
+  clear_error();
+  INF_CHECK_ARG(E > 0 && E <= size_t(kMaxExperts), "expert_count must be in 1..=256");
+  INF_CHECK_ARG(T * k < (size_t(1) << 31), "too many assignments");
+  INF_CHECK_ARG(offsets && active && (T * k == 0 || (expert_ids && sorted)), "null pointer");
+  return launch_dispatch(as_stream(stream), expert_ids, T, k, E, offsets, sorted, active);
+}
+
+size_t inferno_gguf_moe_workspace_bytes(size_t T, size_t k, size_t E, size_t H, size_t I) {
+  Carver c{nullptr};
+  carve_moe(c, T, k, E, H, I);
+  return c.used;
+}
+
+int inferno_gguf_moe(void* stream, int quant, int down_quant, const void* gate,
+                     size_t gate_bytes, const void* up, size_t up_bytes, const void* down,
+                     size_t down_bytes, const void* x, int x_dtype, const uint32_t* expert_ids,
+                     const float* expert_weights, size_t T, size_t k, size_t E, size_t H,
+                     size_t I, float* out, void* workspace, size_t workspace_bytes) {
+  clear_error();
+  int st = validate_moe(quant, down_quant, gate_bytes, up_bytes, down_bytes, T, k, E, H, I);
+  if (st) return st;
+  INF_CHECK_ARG(x_dtype == INFERNO_F32 || x_dtype == INFERNO_BF16, "x dtype must be F32 or BF16");
+  INF_CHECK_ARG(gate && up && down && x && expert_ids && expert_weights && out && workspace,
+                "null pointer");
+  size_t need = inferno_gguf_moe_workspace_bytes(T, k, E, H, I);
+  if (workspace_bytes < need) {
+    set_error("workspace too small: need " + std::to_string(need) + " bytes");
+    return INFERNO_ERR_SIZE;
+  }
+  Carver c{static_cast<char*>(workspace)};
+  MoeScratch m = carve_moe(c, T, k, E, H, I);
+  hipStream_t s = as_stream(stream);
+  if ((st = run_routed(s, quant, down_quant, gate, up, down, x, x_dtype, expert_ids,
+                       expert_weights, T, k, E, H, I, m)))
+    return st;
+  return launch_topk_combine(s, nullptr, nullptr, m.y, nullptr, T, H, k, out);
+}
+
+int inferno_moe_expert_gate_up_swiglu(void* stream, int quant, const void* gate,
+                                      size_t gate_bytes, const void* up, size_t up_bytes,
+                                      const void* x, int x_dtype, const uint32_t* offsets,
+                                      const uint32_t* sorted, const uint32_t* active,
+                                      const float* expert_weights, size_t T, size_t k, size_t E,
+                                      size_t H, size_t I, float* h) {
+  clear_error();
+  int st = validate_moe(quant, quant, gate_bytes, up_bytes, E * matrix_bytes(quant, H, I), T, k,
+                        E, H, I);
+  if (st) return st;
+  INF_CHECK_ARG(x_dtype == INFERNO_F32 || x_dtype == INFERNO_BF16, "x dtype must be F32 or BF16");
+  INF_CHECK_ARG(gate && up && x && offsets && sorted && active && expert_weights && h,
+                "null pointer");
+  return launch_gemv_gate_up_routed(as_stream(stream), quant, gate, up, x, x_dtype, offsets,
+                                    sorted, active, expert_weights, T, k, E, H, I, h);
+}
+
+int inferno_moe_expert_down(void* stream, int down_quant, const void* down, size_t down_bytes,
+                            const float* h, const uint32_t* offsets, const uint32_t* sorted,
+                            const uint32_t* active, size_t T, size_t k, size_t E, size_t H,
+                            size_t I, float* y) {
+  clear_error();
+  int st = validate_moe(INFERNO_Q2_K, down_quant, E * matrix_bytes(INFERNO_Q2_K, I, H),
+                        E * matrix_bytes(INFERNO_Q2_K, I, H), down_bytes, T, k, E, H, I);
+  if (st) return st;
+  INF_CHECK_ARG(down && h && offsets && sorted && active && y, "null pointer");
+  return launch_gemv_down_routed(as_stream(stream), down_quant, down, h, offsets, sorted, active,
+                                 T, k, E, H, I, y);
+}
+
+int inferno_q8_0_gate_up_swiglu(void* stream, const void* gate, size_t gate_bytes, const void* up,
+                                size_t up_bytes, const void* x, int x_dtype, size_t T, size_t H,
+                                size_t Is, float* out) {
+  clear_error();
+  INF_CHECK_ARG(H % kKBlock == 0 && Is > 0 && H > 0, "Q8_0 in_features must be a multiple of 256");
+  INF_CHECK_ARG(x_dtype == INFERNO_F32 || x_dtype == INFERNO_BF16, "x dtype must be F32 or BF16");
+  int st;
+  if ((st = check_len("shared gate", gate_bytes, 1, matrix_bytes(INFERNO_Q8_0, Is, H)))) return st;
+  if ((st = check_len("shared up", up_bytes, 1, matrix_bytes(INFERNO_Q8_0, Is, H)))) return st;
+  if (T == 0) return INFERNO_OK;
+  INF_CHECK_ARG(gate && up && x && out, "null pointer");
+  return launch_gemv_gate_up_dense(as_stream(stream), INFERNO_Q8_0, gate, up, x, x_dtype, T, H,
+                                   Is, out);
+}
+
+int inferno_q8_0_matvec_add2(void* stream, const void* w, size_t w_bytes, const float* input,
+                             const float* residual_a, const float* residual_b, size_t T,
+                             size_t In, size_t O, float* out) {
+  clear_error();
+  INF_CHECK_ARG(In % kKBlock == 0 && In > 0 && O > 0, "Q8_0 in_features must be a multiple of 256");
+  int st;
+  if ((st = check_len("shared down", w_bytes, 1, matrix_bytes(INFERNO_Q8_0, O, In)))) return st;
+  if (T == 0) return INFERNO_OK;
+  INF_CHECK_ARG(w && input && out, "null pointer");
+  return launch_gemv_down_dense(as_stream(stream), INFERNO_Q8_0, w, input, nullptr, 0,
+                                residual_a, residual_b, T, In, O, out);
+}
+
+int inferno_moe_topk_combine_residual(void* stream, const float* shared, const float* residual,
+                                      const float* expert_outputs, const float* expert_weights,
+                                      size_t T, size_t H, size_t k, float* out) {
+  clear_error();
+  INF_CHECK_ARG(k > 0 && H > 0, "top_k and hidden size must be positive");
+  INF_CHECK_ARG(T == 0 || (expert_outputs && expert_weights && out), "null pointer");
+  return launch_topk_combine(as_stream(stream), shared, residual, expert_outputs, expert_weights,
+                             T, H, k, out);
+}
+
+int inferno_moe_weighted_index_add_combine(void* stream, const float* acc,
+                                           const uint32_t* token_indices,
+                                           const float* expert_outputs,
+                                           const float* expert_weights, size_t T, size_t H,
+                                           size_t A, float* out) {
+  clear_error();
+  INF_CHECK_ARG(T == 0 || (acc && out), "null pointer");
+  INF_CHECK_ARG(A == 0 || (token_indices && expert_outputs && expert_weights), "null pointer");
+  return launch_index_add_combine(as_stream(stream), acc, token_indices, expert_outputs,
+                                  expert_weights, T, H, A, out);
+}
+
+int inferno_moe_gather_tokens(void* stream, const float* x, const uint32_t* token_indices,
+                              size_t T, size_t H, size_t A, float* out) {
+  clear_error();
+  INF_CHECK_ARG(A == 0 || (x && token_indices && out), "null pointer");
+  return launch_gather(as_stream(stream), x, token_indices, T, H, A, out);
+}
+
+int inferno_rms_norm(void* stream, const float* x, const float* w, size_t rows, size_t H,
+                     float eps, float* out) {
+  clear_error();
+  INF_CHECK_ARG(H > 0 && eps >= 0.f, "rms_norm needs a positive width and eps >= 0");
+  INF_CHECK_ARG(rows == 0 || (x && w && out), "null pointer");
+  return launch_rms_norm(as_stream(stream), x, w, rows, H, eps, out);
+}
+
+// ------------------------------------------------------------- layer
+
+namespace {
+struct LayerScratch {
+  float* logits;
+  uint32_t* ids;
+  float* weights;
+  float* hs;
+  MoeScratch moe;
+};
+LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
+  LayerScratch s;
+  s.logits = c.take<float>(T * L->experts);
+  s.ids = c.take<uint32_t>(T * L->top_k);
+  s.weights = c.take<float>(T * L->top_k);
+  s.hs = c.take<float>(T * (L->shared_intermediate ? L->shared_intermediate : 1));
+  s.moe = carve_moe(c, T, L->top_k, L->experts, L->hidden, L->intermediate);
+  return s;
+}
+}  // namespace
+
+size_t inferno_moe_layer_workspace_bytes(const inferno_moe_layer* layer, size_t T) {
+  if (!layer) return 0;
+  Carver c{nullptr};
+  carve_layer(c, layer, T);
+  return c.used;
+}
+
+int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const void* x,
+                              int x_dtype, const float* residual, size_t T, float* out,
+                              uint32_t* expert_ids_out, float* expert_weights_out,
+                              void* workspace, size_t workspace_bytes) {
+  clear_error();
+  INF_CHECK_ARG(L != nullptr, "null layer");
+  const size_t H = L->hidden, E = L->experts, I = L->intermediate, k = L->top_k;
+  int st = validate_moe(L->quant, L->down_quant, L->gate_bytes, L->up_bytes, L->down_bytes, T, k,
+                        E, H, I);
+  if (st) return st;
+  INF_CHECK_ARG(x_dtype == INFERNO_F32 || x_dtype == INFERNO_BF16, "x dtype must be F32 or BF16");
+  INF_CHECK_ARG(L->score_fn == INFERNO_SCORE_SIGMOID || L->score_fn == INFERNO_SCORE_SOFTMAX,
+                "score_fn must be SIGMOID or SOFTMAX");
+  INF_CHECK_ARG(std::isfinite(L->routed_scaling_factor), "routed scaling factor must be finite");
+  INF_CHECK_ARG(L->router && L->gate && L->up && L->down && x && out && workspace, "null pointer");
+  const size_t Is = L->shared_intermediate;
+  if (Is) {
+    INF_CHECK_ARG(L->shared_gate && L->shared_up && L->shared_down, "null shared expert pointer");
+    if ((st = check_len("shared gate", L->shared_gate_bytes, 1, matrix_bytes(INFERNO_Q8_0, Is, H))))
+      return st;
+    if ((st = check_len("shared up", L->shared_up_bytes, 1, matrix_bytes(INFERNO_Q8_0, Is, H))))
+      return st;
+    if ((st = check_len("shared down", L->shared_down_bytes, 1, matrix_bytes(INFERNO_Q8_0, H, Is))))
+      return st;
+    INF_CHECK_ARG(Is % kKBlock == 0, "shared intermediate must be a multiple of 256");
+  }
+  size_t need = inferno_moe_layer_workspace_bytes(L, T);
+  if (workspace_bytes < need) {
+    set_error("workspace too small: need " + std::to_string(need) + " bytes");
+    return INFERNO_ERR_SIZE;
+  }
+  Carver c{static_cast<char*>(workspace)};
+  LayerScratch w = carve_layer(c, L, T);
+  hipStream_t s = as_stream(stream);
+  uint32_t* ids = expert_ids_out ? expert_ids_out : w.ids;
+  float* wts = expert_weights_out ? expert_weights_out : w.weights;
+  if ((st = launch_router_logits(s, x, x_dtype, L->router, T, H, E, w.logits))) return st;
+  if ((st = launch_router_topk(s, w.logits, L->router_bias, T, E, k, L->score_fn,
+                               L->norm_topk_prob, L->routed_scaling_factor, ids, wts, nullptr)))
+    return st;
+  if ((st = run_routed(s, L->quant, L->down_quant, L->gate, L->up, L->down, x, x_dtype, ids, wts,
+                       T, k, E, H, I, w.moe)))
+    return st;
+  if (Is) {
+    if ((st = launch_gemv_gate_up_dense(s, INFERNO_Q8_0, L->shared_gate, L->shared_up, x, x_dtype,
+                                        T, H, Is, w.hs)))
+      return st;
+    return launch_gemv_down_dense(s, INFERNO_Q8_0, L->shared_down, w.hs, w.moe.y, k, nullptr,
+                                  residual, T, Is, H, out);
+  }
+  return launch_topk_combine(s, nullptr, residual, w.moe.y, nullptr, T, H, k, out);
+}
+
+// ------------------------------------------------------ synthetic data
+
+int inferno_synth_normal(void* stream, uint64_t seed, float stddev, size_t n, int dtype,
+                         void* out) {
+  clear_error();
+  INF_CHECK_ARG(dtype == INFERNO_F32 || dtype == INFERNO_BF16, "dtype must be F32 or BF16");
+  INF_CHECK_ARG(n == 0 || out, "null pointer");
+  return launch_synth_normal(as_stream(stream), seed, stddev, n, dtype, out);
+}
+
+int inferno_synth_normal_host(uint64_t seed, float stddev, size_t n, float* out) {
+  clear_error();
+  INF_CHECK_ARG(n == 0 || out, "null pointer");
+  for (size_t i = 0; i < n; ++i) out[i] = stddev * synth_normal(seed, i);
+  return INFERNO_OK;
+}
+
+int inferno_quantize_rows_host(int quant, const float* x, size_t rows, size_t cols, void* out) {
+  clear_error();
+  INF_CHECK_ARG(block_bytes(quant) > 0, "unknown quant kind");
+  const size_t bv = size_t(block_values(quant)), bb = size_t(block_bytes(quant));
+  INF_CHECK_ARG(cols % bv == 0, "cols must be a multiple of the block size");
+  auto* o = static_cast<uint8_t*>(out);
+  for (size_t r = 0; r < rows; ++r)
+    for (size_t b = 0; b < cols / bv; ++b)
+      quantize_block(quant, x + r * cols + b * bv, o + (r * (cols / bv) + b) * bb);
+  return INFERNO_OK;
+}
+
+int inferno_synth_quantized(void* stream, int quant, uint64_t seed, float stddev, size_t rows,
+                            size_t cols, void* out) {
+  clear_error();
+  INF_CHECK_ARG(block_bytes(quant) > 0, "unknown quant kind");
+  INF_CHECK_ARG(cols % size_t(block_values(quant)) == 0, "cols must be a multiple of the block size");
+  return launch_synth_quantized(as_stream(stream), quant, seed, stddev, rows, cols, out);
+}
+
+int inferno_synth_quantized_host(int quant, uint64_t seed, float stddev, size_t rows, size_t cols,
+                                 void* out) {
+  clear_error();
+  INF_CHECK_ARG(block_bytes(quant) > 0, "unknown quant kind");
+  const size_t bv = size_t(block_values(quant)), bb = size_t(block_bytes(quant));
+  INF_CHECK_ARG(cols % bv == 0, "cols must be a multiple of the block size");
+  auto* o = static_cast<uint8_t*>(out);
+  float x[256];
+  for (size_t r = 0; r < rows; ++r)
+    for (size_t b = 0; b < cols / bv; ++b) {
+      for (size_t v = 0; v < bv; ++v) x[v] = stddev * synth_normal(seed, r * cols + b * bv + v);
+      quantize_block(quant, x, o + (r * (cols / bv) + b) * bb);
+    }
+  return INFERNO_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,110 @@
+// Data movement and combine kernels. Every output element is written by one
+// thread that sums its contributions in a fixed order — no float atomics, so
+// results are bitwise reproducible run to run.
+#include "kernels.hpp"
+
+namespace inferno {
+namespace {
+
+// shared + residual + sum_r y[t*k+r] * w[t*k+r] in rank order
+// (crates/backend/src/metal/kernels/moe_kernels.metal:210-238).
+__global__ void __launch_bounds__(256)
+    topk_combine_kernel(const float* __restrict__ shared, const float* __restrict__ residual,
+                        const float* __restrict__ y, const float* __restrict__ w, size_t T,
+                        size_t H, int k, float* __restrict__ out) {
+  size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= T * H) return;
+  size_t t = i / H, h = i % H;
+  float v = (shared ? shared[i] : 0.f) + (residual ? residual[i] : 0.f);
+  for (int r = 0; r < k; ++r) {
+    size_t a = t * size_t(k) + size_t(r);
+    v += y[a * H + h] * (w ? w[a] : 1.0f);
+  }
+  out[i] = v;
+}
+
+// acc + contributions of every assignment of token t, in assignment order
+// (crates/backend/src/backend.rs:10298-10352; moe_kernels.metal:53-81).
+__global__ void __launch_bounds__(256)
+    index_add_combine_kernel(const float* __restrict__ acc, const uint32_t* __restrict__ tok,
+                             const float* __restrict__ y, const float* __restrict__ w, size_t T,
+                             size_t H, size_t A, float* __restrict__ out) {
+  size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= T * H) return;
+  size_t t = i / H, h = i % H;
+  float v = acc[i];
+  for (size_t a = 0; a < A; ++a)
+    if (tok[a] == t) v += y[a * H + h] * w[a];
+  out[i] = v;
+}
+
+// moe_kernels.metal:5-28
+__global__ void __launch_bounds__(256)
+    gather_kernel(const float* __restrict__ x, const uint32_t* __restrict__ tok, size_t T,
+                  size_t H, size_t A, float* __restrict__ out) {
+  size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= A * H) return;
+  size_t a = i / H, h = i % H;
+  uint32_t t = tok[a];
+  out[i] = t < T ? x[size_t(t) * H + h] : 0.f;
+}
+
+// One workgroup per row; fp32 sum of squares reduced in a fixed tree order.
+__global__ void __launch_bounds__(256)
+    rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, size_t H, float eps,
+                    float* __restrict__ out) {
+  __shared__ float part[256];
+  const float* row = x + size_t(blockIdx.x) * H;
+  float s = 0.f;
+  for (size_t i = threadIdx.x; i < H; i += 256) s += row[i] * row[i];
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (int(threadIdx.x) < o) part[threadIdx.x] += part[threadIdx.x + o];
+    __syncthreads();
+  }
+  float scale = sqrtf(part[0] / float(H) + eps);
+  for (size_t i = threadIdx.x; i < H; i += 256)
+    out[size_t(blockIdx.x) * H + i] = row[i] / scale * w[i];
+}
+
+unsigned blocks_for(size_t n) { return unsigned((n + 255) / 256); }
+
+}  // namespace
+
+int launch_topk_combine(hipStream_t s, const float* shared, const float* residual,
+                        const float* y, const float* w, size_t T, size_t H, size_t k,
+                        float* out) {
+  if (T * H == 0) return INFERNO_OK;
+  topk_combine_kernel<<<blocks_for(T * H), 256, 0, s>>>(shared, residual, y, w, T, H, int(k),
+                                                        out);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+int launch_index_add_combine(hipStream_t s, const float* acc, const uint32_t* tok,
+                             const float* y, const float* w, size_t T, size_t H, size_t A,
+                             float* out) {
+  if (T * H == 0) return INFERNO_OK;
+  index_add_combine_kernel<<<blocks_for(T * H), 256, 0, s>>>(acc, tok, y, w, T, H, A, out);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+int launch_gather(hipStream_t s, const float* x, const uint32_t* tok, size_t T, size_t H,
+                  size_t A, float* out) {
+  if (A * H == 0) return INFERNO_OK;
+  gather_kernel<<<blocks_for(A * H), 256, 0, s>>>(x, tok, T, H, A, out);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+int launch_rms_norm(hipStream_t s, const float* x, const float* w, size_t rows, size_t H,
+                    float eps, float* out) {
+  if (rows == 0) return INFERNO_OK;
+  rms_norm_kernel<<<unsigned(rows), 256, 0, s>>>(x, w, H, eps, out);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+}  // namespace inferno

@@ -1,0 +1,51 @@
+// Internal launcher declarations shared by the kernel files and the C ABI.
+#pragma once
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace inferno {
+
+int launch_dequant(hipStream_t s, int quant, const void* blocks, size_t n_blocks, float* out);
+int launch_synth_normal(hipStream_t s, uint64_t seed, float stddev, size_t n, int dtype,
+                        void* out);
+int launch_synth_quantized(hipStream_t s, int quant, uint64_t seed, float stddev, size_t rows,
+                           size_t cols, void* out);
+
+int launch_router_logits(hipStream_t s, const void* x, int x_dtype, const float* w, size_t T,
+                         size_t H, size_t E, float* logits);
+int launch_router_topk(hipStream_t s, const float* logits, const float* bias, size_t T, size_t E,
+                       size_t k, int score_fn, int norm, float scale, uint32_t* ids,
+                       float* weights, uint32_t* token_idx);
+
+int launch_dispatch(hipStream_t s, const uint32_t* ids, size_t T, size_t k, size_t E,
+                    uint32_t* offsets, uint32_t* sorted, uint32_t* active);
+
+int launch_gemv_gate_up_routed(hipStream_t s, int quant, const void* gate, const void* up,
+                               const void* x, int x_dtype, const uint32_t* offsets,
+                               const uint32_t* sorted, const uint32_t* active,
+                               const float* route_w, size_t T, size_t k, size_t E, size_t H,
+                               size_t I, float* h_out);
+int launch_gemv_down_routed(hipStream_t s, int quant, const void* down, const float* h,
+                            const uint32_t* offsets, const uint32_t* sorted,
+                            const uint32_t* active, size_t T, size_t k, size_t E, size_t H,
+                            size_t I, float* y_out);
+int launch_gemv_gate_up_dense(hipStream_t s, int quant, const void* gate, const void* up,
+                              const void* x, int x_dtype, size_t T, size_t H, size_t I,
+                              float* out);
+int launch_gemv_down_dense(hipStream_t s, int quant, const void* w, const float* input,
+                           const float* yk, size_t k, const float* res_a, const float* res_b,
+                           size_t T, size_t In, size_t O, float* out);
+
+int launch_topk_combine(hipStream_t s, const float* shared, const float* residual,
+                        const float* expert_outputs, const float* expert_weights, size_t T,
+                        size_t H, size_t k, float* out);
+int launch_index_add_combine(hipStream_t s, const float* acc, const uint32_t* token_idx,
+                             const float* expert_outputs, const float* expert_weights, size_t T,
+                             size_t H, size_t A, float* out);
+int launch_gather(hipStream_t s, const float* x, const uint32_t* token_idx, size_t T, size_t H,
+                  size_t A, float* out);
+int launch_rms_norm(hipStream_t s, const float* x, const float* w, size_t rows, size_t H,
+                    float eps, float* out);
+
+}  // namespace inferno

@@ -1,0 +1,263 @@
+// Router: fp32 logits projection and exact top-k gating.
+//
+// Top-k follows crates/model/src/moe_router.rs:835-940: selection value
+// (sigmoid score + bias, or logit + bias for softmax), ordered by
+// f32::total_cmp descending with the lower expert id winning ties; weights
+// are the unbiased scores in rank order, renormalised by their rank-order
+// sum, times the routed scaling factor. One wavefront per token; every lane
+// holds up to four candidates and each round is a 64-bit max-reduction of
+// (order-preserving score bits, ~expert id).
+#include "kernels.hpp"
+
+namespace inferno {
+namespace {
+
+template <typename T>
+__device__ __forceinline__ float load_x(const T* p, size_t i);
+template <>
+__device__ __forceinline__ float load_x<float>(const float* p, size_t i) {
+  return p[i];
+}
+template <>
+__device__ __forceinline__ float load_x<uint16_t>(const uint16_t* p, size_t i) {
+  return bf16_bits_to_f32(p[i]);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// Few tokens: one wavefront per expert row; the row is read once with
+// 16-byte loads and dotted with every token (T <= 16).
+template <typename XT>
+__global__ void __launch_bounds__(256)
+    logits_small_kernel(const XT* __restrict__ x, const float* __restrict__ w, int T, int H,
+                        int E, float* __restrict__ logits) {
+  const int lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (e >= E) return;
+  float acc[16];
+#pragma unroll
+  for (int t = 0; t < 16; ++t) acc[t] = 0.f;
+  const float* row = w + size_t(e) * H;
+  for (int h0 = lane * 4; h0 < H; h0 += 256) {
+    float4 wv = *reinterpret_cast<const float4*>(row + h0);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      if (t < T) {
+        const size_t base = size_t(t) * H + h0;
+        acc[t] += wv.x * load_x(x, base) + wv.y * load_x(x, base + 1) +
+                  wv.z * load_x(x, base + 2) + wv.w * load_x(x, base + 3);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    if (t < T) {
+      float s = wave_sum(acc[t]);
+      if (lane == 0) logits[size_t(t) * E + e] = s;
+    }
+  }
+}
+
+// Many tokens: 64x64 output tile per 256-thread block, K staged through LDS,
+// 4x4 outputs per thread.
+template <typename XT>
+__global__ void __launch_bounds__(256)
+    logits_tiled_kernel(const XT* __restrict__ x, const float* __restrict__ w, int T, int H,
+                        int E, float* __restrict__ logits) {
+  constexpr int TM = 64, TN = 64, TK = 32;
+  __shared__ float xs[TK][TM + 4];
+  __shared__ float ws[TK][TN + 4];
+  const int tid = threadIdx.x;
+  const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
+  const int tm = (tid / 16) * 4, tn = (tid % 16) * 4;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < H; k0 += TK) {
+    for (int i = tid; i < TM * TK; i += 256) {
+      int r = i / TK, c = i % TK;
+      int gm = m0 + r, gk = k0 + c;
+      xs[c][r] = (gm < T && gk < H) ? load_x(x, size_t(gm) * H + gk) : 0.f;
+      int gn = n0 + r;
+      ws[c][r] = (gn < E && gk < H) ? w[size_t(gn) * H + gk] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int kk = 0; kk < TK; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = xs[kk][tm + i];
+        b[i] = ws[kk][tn + i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += a[i] * b[j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int gm = m0 + tm + i, gn = n0 + tn + j;
+      if (gm < T && gn < E) logits[size_t(gm) * E + gn] = acc[i][j];
+    }
+}
+
+// Order-preserving map of the f32 total order (f32::total_cmp) onto u32.
+__device__ __forceinline__ uint32_t total_order_key(float f) {
+  uint32_t b = f32_to_bits(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    uint64_t o = __shfl_xor(v, m, kWave);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
+__global__ void __launch_bounds__(256)
+    topk_kernel(const float* __restrict__ logits, const float* __restrict__ bias, int T, int E,
+                int k, int score_fn, int norm, float scale, uint32_t* __restrict__ ids,
+                float* __restrict__ weights, uint32_t* __restrict__ token_idx) {
+  constexpr int PER = kMaxExperts / kWave;  // 4 candidates per lane
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float* row = logits + size_t(t) * E;
+  float lg[PER], score[PER];
+  uint64_t key[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    int e = lane + j * kWave;
+    lg[j] = e < E ? row[e] : -INFINITY;
+  }
+  float lmax = 0.f, denom_all = 0.f;
+  if (score_fn == INFERNO_SCORE_SOFTMAX) {
+    float m = lg[0];
+#pragma unroll
+    for (int j = 1; j < PER; ++j) m = fmaxf(m, lg[j]);
+    lmax = wave_max(m);
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    int e = lane + j * kWave;
+    float s, sel;
+    if (score_fn == INFERNO_SCORE_SIGMOID) {
+      s = 1.0f / (1.0f + expf(-lg[j]));
+      sel = s;
+    } else {
+      s = e < E ? expf(lg[j] - lmax) : 0.f;
+      sel = lg[j];
+    }
+    score[j] = s;
+    float corrected = sel + ((bias != nullptr && e < E) ? bias[e] : 0.0f);
+    key[j] = e < E ? ((uint64_t(total_order_key(corrected)) << 32) | uint64_t(0xffffffffu - uint32_t(e)))
+                   : 0ull;
+  }
+  if (score_fn == INFERNO_SCORE_SOFTMAX && !norm) {
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) part += score[j];
+    denom_all = wave_sum(part);
+  }
+  float sel_score[kMaxTopK];
+  uint32_t sel_id[kMaxTopK];
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    if (r < k) {
+      uint64_t best = key[0];
+#pragma unroll
+      for (int j = 1; j < PER; ++j) best = key[j] > best ? key[j] : best;
+      best = wave_max_u64(best);
+      uint32_t id = 0xffffffffu - uint32_t(best & 0xffffffffu);
+      int owner = int(id & 63u), slot = int(id >> 6);
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (j == slot) s = score[j];
+      s = __shfl(s, owner, kWave);
+      if (lane == owner) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+          if (j == slot) key[j] = 0ull;
+      }
+      sel_score[r] = s;
+      sel_id[r] = id;
+    }
+  }
+  if (lane == 0) {
+    float sum = 0.f;
+    if (norm) {
+#pragma unroll
+      for (int r = 0; r < kMaxTopK; ++r)
+        if (r < k) sum += sel_score[r];
+    } else if (score_fn == INFERNO_SCORE_SOFTMAX) {
+      sum = denom_all;
+    }
+    const bool divide = (norm || score_fn == INFERNO_SCORE_SOFTMAX) && sum > 0.f && isfinite(sum);
+#pragma unroll
+    for (int r = 0; r < kMaxTopK; ++r) {
+      if (r < k) {
+        float wv = sel_score[r];
+        if (divide) wv /= sum;
+        size_t a = size_t(t) * k + r;
+        ids[a] = sel_id[r];
+        weights[a] = wv * scale;
+        if (token_idx) token_idx[a] = uint32_t(t);
+      }
+    }
+  }
+}
+
+}  // namespace
+
+int launch_router_logits(hipStream_t s, const void* x, int x_dtype, const float* w, size_t T,
+                         size_t H, size_t E, float* logits) {
+  if (T == 0 || E == 0) return INFERNO_OK;
+  if (T <= 16) {
+    dim3 grid(unsigned((E + 3) / 4));
+    if (x_dtype == INFERNO_BF16)
+      logits_small_kernel<uint16_t><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x), w,
+                                                         int(T), int(H), int(E), logits);
+    else
+      logits_small_kernel<float><<<grid, 256, 0, s>>>(static_cast<const float*>(x), w, int(T),
+                                                      int(H), int(E), logits);
+  } else {
+    dim3 grid(unsigned((E + 63) / 64), unsigned((T + 63) / 64));
+    if (x_dtype == INFERNO_BF16)
+      logits_tiled_kernel<uint16_t><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x), w,
+                                                         int(T), int(H), int(E), logits);
+    else
+      logits_tiled_kernel<float><<<grid, 256, 0, s>>>(static_cast<const float*>(x), w, int(T),
+                                                      int(H), int(E), logits);
+  }
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+int launch_router_topk(hipStream_t s, const float* logits, const float* bias, size_t T, size_t E,
+                       size_t k, int score_fn, int norm, float scale, uint32_t* ids,
+                       float* weights, uint32_t* token_idx) {
+  if (T == 0) return INFERNO_OK;
+  topk_kernel<<<unsigned((T + 3) / 4), 256, 0, s>>>(logits, bias, int(T), int(E), int(k),
+                                                    score_fn, norm, scale, ids, weights,
+                                                    token_idx);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+}  // namespace inferno

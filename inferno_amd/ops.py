@@ -1,0 +1,236 @@
+"""Torch-tensor wrappers over the C ABI (device memory and streams only).
+
+Every function here calls straight into libinferno_moe.so; tensors must live
+on the GPU. uint32 outputs of the ABI are held in torch.int32 tensors.
+"""
+import ctypes as C
+
+import torch
+
+from ._lib import BF16, F32, Q8_0, LayerDesc, check, lib
+
+_DT = {torch.float32: F32, torch.bfloat16: BF16}
+
+
+def _p(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _s():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(t):
+    if not t.is_cuda:
+        raise ValueError("inferno_amd ops need GPU tensors")
+    return t
+
+
+def block_bytes(quant):
+    return lib().inferno_block_bytes(quant)
+
+
+def block_values(quant):
+    return lib().inferno_block_values(quant)
+
+
+def matrix_bytes(quant, rows, cols):
+    return rows * (cols // block_values(quant)) * block_bytes(quant)
+
+
+def dequantize(quant, blocks):
+    n_blocks = blocks.numel() // block_bytes(quant)
+    out = torch.empty(n_blocks * block_values(quant), dtype=torch.float32, device=blocks.device)
+    check(lib().inferno_gguf_dequantize(_s(), quant, _p(_dev(blocks)), n_blocks, _p(out)))
+    return out
+
+
+def router_logits(x, w_router):
+    T, H = x.shape
+    E = w_router.shape[0]
+    out = torch.empty(T, E, dtype=torch.float32, device=x.device)
+    check(lib().inferno_router_logits(_s(), _p(_dev(x)), _DT[x.dtype], _p(w_router), T, H, E,
+                                      _p(out)))
+    return out
+
+
+def router_topk(logits, bias, k, score_fn, norm, scale):
+    T, E = logits.shape
+    ids = torch.empty(T * k, dtype=torch.int32, device=logits.device)
+    w = torch.empty(T * k, dtype=torch.float32, device=logits.device)
+    tok = torch.empty(T * k, dtype=torch.int32, device=logits.device)
+    check(lib().inferno_moe_router_topk(_s(), _p(_dev(logits)), _p(bias), T, E, k, score_fn,
+                                        int(norm), float(scale), _p(ids), _p(w), _p(tok)))
+    return ids, w, tok
+
+
+def dispatch(ids, T, k, E):
+    dev = ids.device
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    sorted_ = torch.empty(max(T * k, 1), dtype=torch.int32, device=dev)
+    active = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    check(lib().inferno_moe_dispatch(_s(), _p(_dev(ids)), T, k, E, _p(offsets), _p(sorted_),
+                                     _p(active)))
+    return offsets, sorted_[: T * k], active
+
+
+def gguf_moe(quant, down_quant, gate, up, down, x, ids, weights, k, E, I):
+    T, H = x.shape
+    ws_bytes = lib().inferno_gguf_moe_workspace_bytes(T, k, E, H, I)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    out = torch.empty(T, H, dtype=torch.float32, device=x.device)
+    check(lib().inferno_gguf_moe(_s(), quant, down_quant, _p(gate), gate.numel(), _p(up),
+                                 up.numel(), _p(down), down.numel(), _p(_dev(x)), _DT[x.dtype],
+                                 _p(ids), _p(weights), T, k, E, H, I, _p(out), _p(ws), ws_bytes))
+    return out
+
+
+def expert_gate_up_swiglu(quant, gate, up, x, offsets, sorted_, active, weights, k, E, I,
+                          out=None):
+    T, H = x.shape
+    if out is None:
+        out = torch.empty(T * k, I, dtype=torch.float32, device=x.device)
+    check(lib().inferno_moe_expert_gate_up_swiglu(
+        _s(), quant, _p(gate), gate.numel(), _p(up), up.numel(), _p(_dev(x)), _DT[x.dtype],
+        _p(offsets), _p(sorted_), _p(active), _p(weights), T, k, E, H, I, _p(out)))
+    return out
+
+
+def expert_down(down_quant, down, h, offsets, sorted_, active, T, k, E, H, out=None):
+    I = h.shape[1]
+    if out is None:
+        out = torch.empty(T * k, H, dtype=torch.float32, device=h.device)
+    check(lib().inferno_moe_expert_down(_s(), down_quant, _p(down), down.numel(), _p(_dev(h)),
+                                        _p(offsets), _p(sorted_), _p(active), T, k, E, H, I,
+                                        _p(out)))
+    return out
+
+
+def q8_0_gate_up_swiglu(gate, up, x, Is):
+    T, H = x.shape
+    out = torch.empty(T, Is, dtype=torch.float32, device=x.device)
+    check(lib().inferno_q8_0_gate_up_swiglu(_s(), _p(gate), gate.numel(), _p(up), up.numel(),
+                                            _p(_dev(x)), _DT[x.dtype], T, H, Is, _p(out)))
+    return out
+
+
+def q8_0_matvec_add2(w, inp, residual_a, residual_b, O):
+    T, In = inp.shape
+    out = torch.empty(T, O, dtype=torch.float32, device=inp.device)
+    check(lib().inferno_q8_0_matvec_add2(_s(), _p(w), w.numel(), _p(_dev(inp)), _p(residual_a),
+                                         _p(residual_b), T, In, O, _p(out)))
+    return out
+
+
+def topk_combine_residual(shared, residual, expert_outputs, expert_weights, k):
+    A, H = expert_outputs.shape
+    T = A // k
+    out = torch.empty(T, H, dtype=torch.float32, device=expert_outputs.device)
+    check(lib().inferno_moe_topk_combine_residual(_s(), _p(shared), _p(residual),
+                                                  _p(_dev(expert_outputs)), _p(expert_weights),
+                                                  T, H, k, _p(out)))
+    return out
+
+
+def weighted_index_add_combine(acc, token_indices, expert_outputs, expert_weights):
+    T, H = acc.shape
+    A = token_indices.numel()
+    out = torch.empty_like(acc)
+    check(lib().inferno_moe_weighted_index_add_combine(_s(), _p(_dev(acc)), _p(token_indices),
+                                                       _p(expert_outputs), _p(expert_weights),
+                                                       T, H, A, _p(out)))
+    return out
+
+
+def gather_tokens(x, token_indices):
+    T, H = x.shape
+    A = token_indices.numel()
+    out = torch.empty(A, H, dtype=torch.float32, device=x.device)
+    check(lib().inferno_moe_gather_tokens(_s(), _p(_dev(x)), _p(token_indices), T, H, A, _p(out)))
+    return out
+
+
+def rms_norm(x, w, eps):
+    rows, H = x.shape
+    out = torch.empty_like(x)
+    check(lib().inferno_rms_norm(_s(), _p(_dev(x)), _p(w), rows, H, float(eps), _p(out)))
+    return out
+
+
+def synth_normal(seed, stddev, n, dtype=torch.float32, device="cuda"):
+    out = torch.empty(n, dtype=dtype, device=device)
+    check(lib().inferno_synth_normal(_s(), seed, float(stddev), n, _DT[dtype], _p(out)))
+    return out
+
+
+def synth_quantized(quant, seed, stddev, rows, cols, device="cuda"):
+    out = torch.empty(matrix_bytes(quant, rows, cols), dtype=torch.uint8, device=device)
+    check(lib().inferno_synth_quantized(_s(), quant, seed, float(stddev), rows, cols, _p(out)))
+    return out
+
+
+def synth_normal_host(seed, stddev, n):
+    out = torch.empty(n, dtype=torch.float32)
+    check(lib().inferno_synth_normal_host(seed, float(stddev), n, _p(out)))
+    return out
+
+
+def synth_quantized_host(quant, seed, stddev, rows, cols):
+    out = torch.empty(matrix_bytes(quant, rows, cols), dtype=torch.uint8)
+    check(lib().inferno_synth_quantized_host(quant, seed, float(stddev), rows, cols, _p(out)))
+    return out
+
+
+def quantize_rows_host(quant, x):
+    rows, cols = x.shape
+    x = x.contiguous().float()
+    out = torch.empty(matrix_bytes(quant, rows, cols), dtype=torch.uint8)
+    check(lib().inferno_quantize_rows_host(quant, _p(x), rows, cols, _p(out)))
+    return out
+
+
+class MoELayer:
+    """One MoE FFN layer resident on the GPU (inferno_moe_layer_forward).
+
+    Holds device tensors for the router, routed experts and optional Q8_0
+    shared expert, and a reusable workspace sized for `max_tokens`.
+    """
+
+    def __init__(self, *, hidden, experts, intermediate, top_k, quant, down_quant, score_fn,
+                 norm_topk_prob, routed_scaling_factor, router, router_bias, gate, up, down,
+                 shared_intermediate=0, shared_gate=None, shared_up=None, shared_down=None,
+                 max_tokens=1):
+        self.tensors = [router, router_bias, gate, up, down, shared_gate, shared_up, shared_down]
+        d = LayerDesc()
+        d.hidden, d.experts, d.intermediate, d.top_k = hidden, experts, intermediate, top_k
+        d.quant, d.down_quant, d.score_fn = quant, down_quant, score_fn
+        d.norm_topk_prob, d.routed_scaling_factor = int(norm_topk_prob), routed_scaling_factor
+        d.router, d.router_bias = _p(router), _p(router_bias)
+        d.gate, d.up, d.down = _p(gate), _p(up), _p(down)
+        d.gate_bytes, d.up_bytes, d.down_bytes = gate.numel(), up.numel(), down.numel()
+        d.shared_intermediate = shared_intermediate
+        if shared_intermediate:
+            d.shared_gate, d.shared_up, d.shared_down = _p(shared_gate), _p(shared_up), _p(shared_down)
+            d.shared_gate_bytes = shared_gate.numel()
+            d.shared_up_bytes = shared_up.numel()
+            d.shared_down_bytes = shared_down.numel()
+        self.desc = d
+        self.hidden, self.top_k = hidden, top_k
+        self.device = gate.device
+        self._ws = None
+        self.reserve(max_tokens)
+
+    def reserve(self, T):
+        need = lib().inferno_moe_layer_workspace_bytes(C.byref(self.desc), T)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+
+    def forward(self, x, residual=None, out=None, ids=None, weights=None):
+        T = x.shape[0]
+        self.reserve(T)
+        if out is None:
+            out = torch.empty(T, self.hidden, dtype=torch.float32, device=x.device)
+        check(lib().inferno_moe_layer_forward(
+            _s(), C.byref(self.desc), _p(_dev(x)), _DT[x.dtype], _p(residual), T, _p(out),
+            _p(ids), _p(weights), _p(self._ws), self._ws.numel()))
+        return out

@@ -1,0 +1,284 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Bars: dequantised weights bit-exact; selected
+expert ids exact except near-ties within 1e-6 of the k-th selection value
+(counted and reported); MoE outputs within relative L2 2e-3.
+"""
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+import kat_blocks as kb
+import oracle_lib as orc
+import parity_helpers as ph
+import ref_numpy as rn
+from inferno_amd import configs as cf
+from inferno_amd import ops
+from inferno_amd._lib import Q2_K, Q3_K, Q4_K, Q6_K, Q8_0, SCORE_SIGMOID, SCORE_SOFTMAX
+
+pytestmark = pytest.mark.gpu
+rng = np.random.default_rng(7)
+BB = {Q2_K: 84, Q3_K: 110, Q4_K: 144, Q6_K: 210, Q8_0: 34}
+
+
+def random_blocks(quant, n):
+    raw = rng.integers(0, 256, size=(n, BB[quant]), dtype=np.uint8)
+    scale_at = {Q2_K: [80, 82], Q3_K: [108], Q4_K: [0, 2], Q6_K: [208], Q8_0: [0]}[quant]
+    for off in scale_at:
+        h = (0.01 * rng.standard_normal(n)).astype(np.float16).view(np.uint16)
+        raw[:, off] = h & 0xFF
+        raw[:, off + 1] = h >> 8
+    return raw.reshape(-1)
+
+
+def dev(a, cuda):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+
+
+@pytest.mark.parametrize("quant", [Q2_K, Q3_K, Q4_K, Q6_K, Q8_0])
+def test_dequant_bit_exact(cuda, quant):
+    raw = random_blocks(quant, 4096)
+    # include subnormal and zero scales
+    raw[BB[quant] * 0: BB[quant] * 1] = 0
+    got = ph.to_np(ops.dequantize(quant, dev(raw, cuda)))
+    ref = orc.dequantize(quant, raw)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_reference_kats(cuda):
+    sm = [(i + 1 if i < 15 else 0, i) for i in range(16)]
+    v = ph.to_np(ops.dequantize(Q2_K, dev(kb.q2_k_block(0x3C00, 0x3800, sm, 0xE4), cuda)))
+    assert v[16] == -0.5 and v[224] == 38.0 and v[240] == -7.5
+    v = ph.to_np(ops.dequantize(Q4_K, dev(kb.q4_k_block(0x3C00, 0, 1, 0, 0x21), cuda)))
+    assert v[0] == 1.0 and v[32] == 2.0
+    v = ph.to_np(ops.dequantize(Q8_0, dev(kb.q8_0_block(0x3800, -8), cuda)))
+    assert v[0] == -4.0 and v[31] == 11.5
+
+
+@pytest.mark.parametrize("T,H,E,bf16", [(1, 6144, 256, True), (16, 2048, 64, False),
+                                        (77, 4096, 128, True)])
+def test_router_logits(cuda, T, H, E, bf16):
+    x = torch.randn(T, H, device=cuda)
+    if bf16:
+        x = x.bfloat16()
+    w = 0.02 * torch.randn(E, H, device=cuda)
+    got = ph.to_np(ops.router_logits(x, w)).astype(np.float64)
+    xs, ws = ph.x_f32(x).astype(np.float64), ph.to_np(w).astype(np.float64)
+    ref64 = xs @ ws.T
+    cond = np.abs(xs) @ np.abs(ws).T  # fp32 summation error scales with sum |x*w|
+    orc_err = np.abs(orc.linear(ph.x_f32(x), ph.to_np(w)) - ref64)
+    assert np.all(np.abs(got - ref64) <= 2e-6 * cond)
+    assert np.all(orc_err <= 2e-5 * cond)
+
+
+@pytest.mark.parametrize("score_fn,norm,E,k", [(SCORE_SIGMOID, True, 256, 8),
+                                               (SCORE_SOFTMAX, True, 64, 8),
+                                               (SCORE_SOFTMAX, True, 128, 10),
+                                               (SCORE_SOFTMAX, False, 128, 10),
+                                               (SCORE_SIGMOID, False, 100, 16)])
+def test_router_topk_matches_oracle(cuda, score_fn, norm, E, k):
+    T = 333
+    logits = (1.5 * rng.standard_normal((T, E))).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(E)).astype(np.float32) if score_fn == SCORE_SIGMOID else None
+    ids, w, tok = ops.router_topk(dev(logits, cuda), None if bias is None else dev(bias, cuda),
+                                  k, score_fn, norm, 2.5)
+    oid, ow = orc.router_topk(logits, bias, k, score_fn, norm, 2.5)
+    spec = SimpleNamespace(score_fn=score_fn, top_k=k)
+    sel = ph.selection_values(spec, logits, bias)
+    _, flips = ph.compare_routing(spec, ph.to_np(ids).view(np.uint32), oid, sel)
+    print(f"near-tie tokens: {flips}")
+    same = (ph.to_np(ids).view(np.uint32).reshape(T, k) == oid.reshape(T, k)).all(1)
+    assert np.allclose(ph.to_np(w).reshape(T, k)[same], ow.reshape(T, k)[same], rtol=2e-6,
+                       atol=1e-7)
+    assert np.array_equal(ph.to_np(tok), np.repeat(np.arange(T), k))
+
+
+def test_router_tie_kat(cuda):
+    # crates/model/src/moe_router.rs:963-972
+    ids, w, _ = ops.router_topk(dev(np.array([[0.5, 0.5, 0.1, 0.2]], np.float32), cuda),
+                                dev(np.zeros(4, np.float32), cuda), 2, SCORE_SIGMOID, True, 2.5)
+    assert list(ph.to_np(ids)) == [0, 1]
+    assert np.allclose(ph.to_np(w), [1.25, 1.25], atol=1e-6)
+
+
+def test_router_specialised_decode_case(cuda):
+    # laguna_xs.rs:2269-2316 inputs; expected ids from the oracle
+    E = 256
+    logits = ((np.arange(E, dtype=np.float32) / 64.0) - 2.0)[None]
+    bias = np.zeros(E, np.float32)
+    bias[3], bias[7], bias[11] = 2.0, 1.9, 1.8
+    ids, w, _ = ops.router_topk(dev(logits, cuda), dev(bias, cuda), 8, SCORE_SIGMOID, True, 1.25)
+    oid, ow = orc.router_topk(logits, bias, 8, 0, True, 1.25)
+    assert list(ph.to_np(ids)) == list(oid)
+    assert np.allclose(ph.to_np(w), ow, rtol=2e-6)
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 8, 256), (16, 8, 64), (512, 8, 256), (4096, 8, 256),
+                                   (37, 10, 128), (3, 1, 1)])
+def test_dispatch_matches_oracle(cuda, T, k, E):
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).reshape(-1).astype(np.uint32)
+    if T == 4096:  # heavy skew: half the tokens share experts 0..7
+        ids.reshape(T, k)[: T // 2] = np.arange(8)
+    off, srt, act = ops.dispatch(dev(ids.view(np.int32), cuda), T, k, E)
+    ooff, osrt = orc.dispatch(ids, T, k, E)
+    assert np.array_equal(ph.to_np(off).view(np.uint32), ooff)
+    assert np.array_equal(ph.to_np(srt).view(np.uint32), osrt)
+    a = ph.to_np(act)
+    used = np.nonzero(np.diff(ooff))[0]
+    assert a[0] == len(used) and np.array_equal(a[1: 1 + len(used)], used)
+
+
+def test_dispatch_empty(cuda):
+    off, srt, act = ops.dispatch(torch.zeros(1, dtype=torch.int32, device=cuda), 0, 8, 16)
+    assert ph.to_np(off).sum() == 0 and ph.to_np(act)[0] == 0
+
+
+def _moe_case(cuda, quant, down, T, H, I, E, k, x_bf16):
+    gb = 256
+    gate = random_blocks(quant, E * I * H // gb)
+    up = random_blocks(quant, E * I * H // gb)
+    dn = random_blocks(down, E * H * I // 256)
+    x = torch.randn(T, H, device=cuda)
+    if x_bf16:
+        x = x.bfloat16()
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).reshape(-1).astype(np.uint32)
+    w = rng.random(T * k).astype(np.float32)
+    out = ops.gguf_moe(quant, down, dev(gate, cuda), dev(up, cuda), dev(dn, cuda), x,
+                       dev(ids.view(np.int32), cuda), dev(w, cuda), k, E, I)
+    ref = orc.moe_routed(quant, down, gate, up, dn, ph.x_f32(x), ids, w, E, k, I)
+    return ph.to_np(out), ref
+
+
+@pytest.mark.parametrize("quant,down", [(Q2_K, Q2_K), (Q3_K, Q3_K), (Q4_K, Q4_K), (Q4_K, Q6_K)])
+@pytest.mark.parametrize("T,H,I,E,k,bf16", [(1, 512, 256, 16, 4, True), (4, 256, 256, 16, 4, False),
+                                            (9, 768, 512, 8, 3, True), (33, 1536, 768, 12, 5, False)])
+def test_gguf_moe_matches_oracle(cuda, quant, down, T, H, I, E, k, bf16):
+    got, ref = _moe_case(cuda, quant, down, T, H, I, E, k, bf16)
+    err = rn.rel_l2(got, ref)
+    print(f"rel_l2={err:.3e}")
+    assert err < ph.TOL_REL_L2
+
+
+def test_q3_known_block(cuda):
+    # gguf_moe.rs:468-514: silu(d)*d*d with d = 384/1024
+    sel = kb.q3_k_block(0x1400, [33] * 16, 0xE4, 0xFF)
+    unused = kb.q3_k_block(0, [33] * 16, 0xE4, 0xFF)
+    wb = dev(np.concatenate([np.tile(sel, 256), np.tile(unused, 256)]), cuda)
+    x = torch.ones(1, 256, device=cuda)
+    ids, w, _ = ops.router_topk(dev(np.array([[10.0, -10.0]], np.float32), cuda),
+                                dev(np.zeros(2, np.float32), cuda), 1, SCORE_SIGMOID, True, 1.0)
+    out = ph.to_np(ops.gguf_moe(Q3_K, Q3_K, wb, wb, wb, x, ids, w, 1, 2, 256))
+    d = 384.0 / 1024
+    assert np.allclose(out, d / (1 + np.exp(-d)) * d * d, atol=1e-4)
+
+
+@pytest.mark.parametrize("down", [Q4_K, Q6_K])
+def test_xs_top8_known_sum(cuda, down):
+    # laguna_xs.rs:1905-1974 closed form sum_v (I/k) v^2 sigmoid(v)
+    E = k = 8
+    H, I = 256, 512
+    vals = list(range(1, 9))
+    gate = np.concatenate([np.tile(kb.q4_xs_block(v), I * H // 256) for v in vals])
+    blk = kb.q4_xs_block(1) if down == Q4_K else kb.q6_xs_block(1)
+    dn = np.concatenate([np.tile(blk, H * I // 256) for _ in vals])
+    x = torch.full((1, H), 1.0 / H, device=cuda)
+    ids, w, _ = ops.router_topk(torch.zeros(1, E, device=cuda), torch.zeros(E, device=cuda), k,
+                                SCORE_SIGMOID, True, 1.0)
+    g = dev(gate, cuda)
+    out = ph.to_np(ops.gguf_moe(Q4_K, down, g, g, dev(dn, cuda), x, ids, w, k, E, I))
+    expect = sum((I / k) * v * v / (1 + np.exp(-v)) for v in vals)
+    assert np.allclose(out, expect, rtol=1e-5)
+
+
+@pytest.mark.parametrize("T,H,Is", [(1, 6144, 2048), (5, 1024, 512)])
+def test_shared_q8_0(cuda, T, H, Is):
+    g = random_blocks(Q8_0, Is * H // 32)
+    u = random_blocks(Q8_0, Is * H // 32)
+    d = random_blocks(Q8_0, H * Is // 32)
+    x = torch.randn(T, H, device=cuda).bfloat16()
+    ra = torch.randn(T, H, device=cuda)
+    rb = torch.randn(T, H, device=cuda)
+    hs = ops.q8_0_gate_up_swiglu(dev(g, cuda), dev(u, cuda), x, Is)
+    out = ops.q8_0_matvec_add2(dev(d, cuda), hs, ra, rb, H)
+    ref = orc.shared_q8_0(g, u, d, ph.x_f32(x), Is, routed=ph.to_np(ra), residual=ph.to_np(rb))
+    assert rn.rel_l2(ph.to_np(out), ref) < ph.TOL_REL_L2
+
+
+def test_combine_and_gather_kats(cuda):
+    # backend.rs:11336-11384
+    acc = torch.zeros(4, 2, device=cuda)
+    tok = torch.tensor([0, 2, 2], dtype=torch.int32, device=cuda)
+    y = torch.arange(1, 7, dtype=torch.float32, device=cuda).view(3, 2)
+    w = torch.tensor([1.0, 0.5, 2.0], device=cuda)
+    out = ph.to_np(ops.weighted_index_add_combine(acc, tok, y, w))
+    assert list(out[0]) == [1.0, 2.0] and list(out[2]) == [11.5, 14.0]
+    x = torch.tensor([[1.0, 2.0], [3.0, 4.0], [5.0, 6.0]], device=cuda)
+    g = ph.to_np(ops.gather_tokens(x, torch.tensor([2, 0, 2], dtype=torch.int32, device=cuda)))
+    assert g.tolist() == [[5.0, 6.0], [1.0, 2.0], [5.0, 6.0]]
+    yk = torch.randn(6, 8, device=cuda)
+    wk = torch.rand(6, device=cuda)
+    sh, res = torch.randn(3, 8, device=cuda), torch.randn(3, 8, device=cuda)
+    c = ph.to_np(ops.topk_combine_residual(sh, res, yk, wk, 2))
+    ref = ph.to_np(sh + res + (yk * wk[:, None]).view(3, 2, 8).sum(1))
+    assert np.allclose(c, ref, rtol=1e-6, atol=1e-6)
+
+
+def test_rms_norm(cuda):
+    x = torch.randn(7, 4096, device=cuda)
+    w = torch.randn(4096, device=cuda)
+    got = ph.to_np(ops.rms_norm(x, w, 1e-6))
+    ref = orc.rms_norm(ph.to_np(x), ph.to_np(w), 1e-6)
+    assert np.allclose(got, ref, rtol=2e-6, atol=1e-6)
+
+
+def _layer_parity(cuda, key, T, tokens=None):
+    cfg = cf.CONFIGS[key]
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
+    x = cf.make_input(cfg, T, device=cuda)
+    residual = torch.randn(T, cfg.hidden, device=cuda)
+    ids = torch.empty(T * cfg.top_k, dtype=torch.int32, device=cuda)
+    w = torch.empty(T * cfg.top_k, dtype=torch.float32, device=cuda)
+    out = lt.layer.forward(x, residual, ids=ids, weights=w)
+    out2 = lt.layer.forward(x, residual)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), "layer output is not bitwise reproducible"
+    tokens = np.arange(T) if tokens is None else np.asarray(tokens)
+    ref, _, _, flips = ph.oracle_layer_tokens(cfg, lt, x, residual, tokens,
+                                              ph.to_np(ids).view(np.uint32), ph.to_np(w))
+    err = rn.rel_l2(ph.to_np(out)[tokens] - ph.to_np(residual)[tokens],
+                    ref - ph.to_np(residual)[tokens])
+    print(f"{cfg.name} T={T}: rel_l2(moe part)={err:.3e} near-tie tokens={flips}")
+    assert err < ph.TOL_REL_L2
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_layer_c1_q4k_softmax(cuda, T):
+    _layer_parity(cuda, "c1", T)
+
+
+def test_layer_c2_glm_q2k_decode_full_size(cuda):
+    _layer_parity(cuda, "c2", 1)
+
+
+def test_layer_c3_glm_q3k_prefill_sampled_tokens(cuda):
+    _layer_parity(cuda, "c3", 512, tokens=[0, 1, 255, 511])
+
+
+@pytest.mark.parametrize("T", [1, 32])
+def test_layer_c4_laguna_q2k_q3k_layers(cuda, T):
+    cfg = cf.CONFIGS["c4"]
+    # every layer kind once: layer 0 (Q2_K) and layer 2 (Q3_K)
+    for layer in (0, 2):
+        lt = cf.build_layer(cfg, layer, cuda, max_tokens=T)
+        x = cf.make_input(cfg, T, device=cuda)
+        ids = torch.empty(T * 10, dtype=torch.int32, device=cuda)
+        w = torch.empty(T * 10, device=cuda)
+        out = lt.layer.forward(x, None, ids=ids, weights=w)
+        toks = np.arange(T) if T <= 4 else np.array([0, 7, 31])
+        ref, _, _, flips = ph.oracle_layer_tokens(cfg, lt, x, None, toks,
+                                                  ph.to_np(ids).view(np.uint32), ph.to_np(w))
+        err = rn.rel_l2(ph.to_np(out)[toks], ref)
+        print(f"c4 layer {layer} T={T}: rel_l2={err:.3e} near-tie tokens={flips}")
+        assert err < ph.TOL_REL_L2
