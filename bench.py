@@ -106,17 +106,20 @@ def main():
         off, srt, act = ops.dispatch(ids, T, k, E)
         plans.append((lt, xs[j], off, srt, act, w, int(torch.unique(ids).numel())))
     h_out = torch.empty(T * k, I, device=dev)
+    gws = ops.gemv_workspace(T, H, dev)
     reps = max(args.steps, 64)
     for j in range(8):
         lt, x, off, srt, act, w, _ = plans[j]
-        ops.expert_gate_up_swiglu(q, lt.gate, lt.up, x, off, srt, act, w, k, E, I, out=h_out)
+        ops.expert_gate_up_swiglu(q, lt.gate, lt.up, x, off, srt, act, w, k, E, I, out=h_out,
+                                  ws=gws)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record()
     uniq = 0
     for j in range(reps):
         lt, x, off, srt, act, w, nu = plans[j % n_inputs]
-        ops.expert_gate_up_swiglu(q, lt.gate, lt.up, x, off, srt, act, w, k, E, I, out=h_out)
+        ops.expert_gate_up_swiglu(q, lt.gate, lt.up, x, off, srt, act, w, k, E, I, out=h_out,
+                                  ws=gws)
         uniq += nu
     ev1.record()
     torch.cuda.synchronize()

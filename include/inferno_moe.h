@@ -133,6 +133,12 @@ int inferno_gguf_moe(void* stream, int quant, int down_quant, const void* gate,
                      size_t k, size_t E, size_t H, size_t I, float* out, void* workspace,
                      size_t workspace_bytes);
 
+/* Workspace bytes of a GEMV entry point that reads `rows` activation rows of
+ * length K (it stages them as packed f16 pairs before streaming weights):
+ * gate/up: rows = T, K = H; down: rows = T*k, K = I; Q8_0 shared gate/up:
+ * rows = T, K = H; Q8_0 matvec: rows = T, K = In. */
+size_t inferno_gemv_workspace_bytes(size_t rows, size_t K);
+
 /* Stage-level entry points over a dispatch (inferno_moe_dispatch outputs).
  * gate/up: h[a, i] = silu(W_gate[e_a] x_t) * (W_up[e_a] x_t) * w_a for every
  * assignment a = t*k + r, h is [T*k, I] fp32. Replaces
@@ -143,14 +149,15 @@ int inferno_moe_expert_gate_up_swiglu(void* stream, int quant, const void* gate,
                                       const void* x, int x_dtype, const uint32_t* offsets,
                                       const uint32_t* sorted, const uint32_t* active,
                                       const float* expert_weights, size_t T, size_t k, size_t E,
-                                      size_t H, size_t I, float* h);
+                                      size_t H, size_t I, float* h, void* workspace,
+                                      size_t workspace_bytes);
 
 /* down: y[a, o] = W_down[e_a] . h[a] for every assignment, y is [T*k, H].
  * Replaces Backend::q2_k_multi_expert_matvec_device (backend.rs:1711). */
 int inferno_moe_expert_down(void* stream, int down_quant, const void* down, size_t down_bytes,
                             const float* h, const uint32_t* offsets, const uint32_t* sorted,
                             const uint32_t* active, size_t T, size_t k, size_t E, size_t H,
-                            size_t I, float* y);
+                            size_t I, float* y, void* workspace, size_t workspace_bytes);
 
 /* --------------------------------------------------------- shared expert */
 
@@ -158,14 +165,16 @@ int inferno_moe_expert_down(void* stream, int down_quant, const void* down, size
  * Replaces Backend::q8_0_gate_up_swiglu_device (backend.rs:1578). */
 int inferno_q8_0_gate_up_swiglu(void* stream, const void* gate, size_t gate_bytes,
                                 const void* up, size_t up_bytes, const void* x, int x_dtype,
-                                size_t T, size_t H, size_t Is, float* out);
+                                size_t T, size_t H, size_t Is, float* out, void* workspace,
+                                size_t workspace_bytes);
 
 /* out[T,O] = residual_a + residual_b + W . input, Q8_0 W [O rows of In].
  * residual_a / residual_b may be NULL (zero).
  * Replaces Backend::laguna_q8_0_matvec_add2_device (backend.rs:1682). */
 int inferno_q8_0_matvec_add2(void* stream, const void* w, size_t w_bytes, const float* input,
                              const float* residual_a, const float* residual_b, size_t T,
-                             size_t In, size_t O, float* out);
+                             size_t In, size_t O, float* out, void* workspace,
+                             size_t workspace_bytes);
 
 /* --------------------------------------------------------------- combine */
 

@@ -43,12 +43,15 @@ SIGNATURES = {
     "inferno_gguf_moe_workspace_bytes": (_sz, [_sz, _sz, _sz, _sz, _sz]),
     "inferno_gguf_moe": (_i, [_vp, _i, _i, _vp, _sz, _vp, _sz, _vp, _sz, _vp, _i, _vp, _vp,
                               _sz, _sz, _sz, _sz, _sz, _vp, _vp, _sz]),
+    "inferno_gemv_workspace_bytes": (_sz, [_sz, _sz]),
     "inferno_moe_expert_gate_up_swiglu": (_i, [_vp, _i, _vp, _sz, _vp, _sz, _vp, _i, _vp, _vp,
-                                               _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp]),
+                                               _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _sz]),
     "inferno_moe_expert_down": (_i, [_vp, _i, _vp, _sz, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz,
-                                     _sz, _vp]),
-    "inferno_q8_0_gate_up_swiglu": (_i, [_vp, _vp, _sz, _vp, _sz, _vp, _i, _sz, _sz, _sz, _vp]),
-    "inferno_q8_0_matvec_add2": (_i, [_vp, _vp, _sz, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+                                     _sz, _vp, _vp, _sz]),
+    "inferno_q8_0_gate_up_swiglu": (_i, [_vp, _vp, _sz, _vp, _sz, _vp, _i, _sz, _sz, _sz, _vp,
+                                         _vp, _sz]),
+    "inferno_q8_0_matvec_add2": (_i, [_vp, _vp, _sz, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _vp,
+                                      _sz]),
     "inferno_moe_topk_combine_residual": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "inferno_moe_weighted_index_add_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "inferno_moe_gather_tokens": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),

@@ -6,7 +6,7 @@
 #include <string>
 #include <vector>
 
-#include "kernels.hpp"
+#include "gemv_common.hpp"
 #include "quantize.hpp"
 
 namespace inferno {
@@ -58,7 +58,14 @@ struct MoeScratch {
   uint32_t* active;
   float* h;
   float* y;
+  uint32_t* stage_x;  // staged activations of x (sized for fp32 input)
+  uint32_t* stage_h;  // staged activations of h
 };
+
+// Staged activation rows, sized for the fp32 (split) layout, the larger one.
+size_t stage_words(size_t rows, size_t K) {
+  return gemv_stage_bytes(INFERNO_Q2_K, rows, K, INFERNO_F32) / 4;
+}
 
 MoeScratch carve_moe(Carver& c, size_t T, size_t k, size_t E, size_t H, size_t I) {
   MoeScratch m;
@@ -67,6 +74,8 @@ MoeScratch carve_moe(Carver& c, size_t T, size_t k, size_t E, size_t H, size_t I
   m.active = c.take<uint32_t>(E + 1);
   m.h = c.take<float>(T * k * I);
   m.y = c.take<float>(T * k * H);
+  m.stage_x = c.take<uint32_t>(stage_words(T, H));
+  m.stage_h = c.take<uint32_t>(stage_words(T * k, I));
   return m;
 }
 
@@ -99,14 +108,22 @@ int validate_moe(int quant, int down_quant, size_t gate_bytes, size_t up_bytes,
 int run_routed(hipStream_t s, int quant, int down_quant, const void* gate, const void* up,
                const void* down, const void* x, int x_dtype, const uint32_t* ids,
                const float* w, size_t T, size_t k, size_t E, size_t H, size_t I,
-               const MoeScratch& m) {
+               const MoeScratch& m, bool x_staged) {
   int st;
   if ((st = launch_dispatch(s, ids, T, k, E, m.offsets, m.sorted, m.active))) return st;
-  if ((st = launch_gemv_gate_up_routed(s, quant, gate, up, x, x_dtype, m.offsets, m.sorted,
-                                       m.active, w, T, k, E, H, I, m.h)))
+  if ((st = launch_gemv_gate_up_routed(s, quant, gate, up, x, x_dtype, m.stage_x, x_staged,
+                                       m.offsets, m.sorted, m.active, w, T, k, E, H, I, m.h)))
     return st;
-  return launch_gemv_down_routed(s, down_quant, down, m.h, m.offsets, m.sorted, m.active, T, k,
-                                 E, H, I, m.y);
+  return launch_gemv_down_routed(s, down_quant, down, m.h, m.stage_h, m.offsets, m.sorted,
+                                 m.active, T, k, E, H, I, m.y);
+}
+
+int need_ws(void* ws, size_t have, size_t need) {
+  if (need > 0 && (ws == nullptr || have < need)) {
+    set_error("workspace too small: need " + std::to_string(need) + " bytes");
+    return INFERNO_ERR_SIZE;
+  }
+  return INFERNO_OK;
 }
 
 }  // namespace
@@ -207,9 +224,13 @@ int inferno_gguf_moe(void* stream, int quant, int down_quant, const void* gate,
   MoeScratch m = carve_moe(c, T, k, E, H, I);
   hipStream_t s = as_stream(stream);
   if ((st = run_routed(s, quant, down_quant, gate, up, down, x, x_dtype, expert_ids,
-                       expert_weights, T, k, E, H, I, m)))
+                       expert_weights, T, k, E, H, I, m, false)))
     return st;
   return launch_topk_combine(s, nullptr, nullptr, m.y, nullptr, T, H, k, out);
+}
+
+size_t inferno_gemv_workspace_bytes(size_t rows, size_t K) {
+  return gemv_stage_bytes(INFERNO_Q2_K, rows, K, INFERNO_F32);
 }
 
 int inferno_moe_expert_gate_up_swiglu(void* stream, int quant, const void* gate,
@@ -217,7 +238,8 @@ int inferno_moe_expert_gate_up_swiglu(void* stream, int quant, const void* gate,
                                       const void* x, int x_dtype, const uint32_t* offsets,
                                       const uint32_t* sorted, const uint32_t* active,
                                       const float* expert_weights, size_t T, size_t k, size_t E,
-                                      size_t H, size_t I, float* h) {
+                                      size_t H, size_t I, float* h, void* workspace,
+                                      size_t workspace_bytes) {
   clear_error();
   int st = validate_moe(quant, quant, gate_bytes, up_bytes, E * matrix_bytes(quant, H, I), T, k,
                         E, H, I);
@@ -225,26 +247,32 @@ int inferno_moe_expert_gate_up_swiglu(void* stream, int quant, const void* gate,
   INF_CHECK_ARG(x_dtype == INFERNO_F32 || x_dtype == INFERNO_BF16, "x dtype must be F32 or BF16");
   INF_CHECK_ARG(gate && up && x && offsets && sorted && active && expert_weights && h,
                 "null pointer");
-  return launch_gemv_gate_up_routed(as_stream(stream), quant, gate, up, x, x_dtype, offsets,
-                                    sorted, active, expert_weights, T, k, E, H, I, h);
+  if ((st = need_ws(workspace, workspace_bytes, gemv_stage_bytes(quant, T, H, x_dtype)))) return st;
+  return launch_gemv_gate_up_routed(as_stream(stream), quant, gate, up, x, x_dtype,
+                                    static_cast<uint32_t*>(workspace), false, offsets, sorted,
+                                    active, expert_weights, T, k, E, H, I, h);
 }
 
 int inferno_moe_expert_down(void* stream, int down_quant, const void* down, size_t down_bytes,
                             const float* h, const uint32_t* offsets, const uint32_t* sorted,
                             const uint32_t* active, size_t T, size_t k, size_t E, size_t H,
-                            size_t I, float* y) {
+                            size_t I, float* y, void* workspace, size_t workspace_bytes) {
   clear_error();
   int st = validate_moe(INFERNO_Q2_K, down_quant, E * matrix_bytes(INFERNO_Q2_K, I, H),
                         E * matrix_bytes(INFERNO_Q2_K, I, H), down_bytes, T, k, E, H, I);
   if (st) return st;
   INF_CHECK_ARG(down && h && offsets && sorted && active && y, "null pointer");
-  return launch_gemv_down_routed(as_stream(stream), down_quant, down, h, offsets, sorted, active,
-                                 T, k, E, H, I, y);
+  if ((st = need_ws(workspace, workspace_bytes,
+                    gemv_stage_bytes(down_quant, T * k, I, INFERNO_F32))))
+    return st;
+  return launch_gemv_down_routed(as_stream(stream), down_quant, down, h,
+                                 static_cast<uint32_t*>(workspace), offsets, sorted, active, T, k,
+                                 E, H, I, y);
 }
 
 int inferno_q8_0_gate_up_swiglu(void* stream, const void* gate, size_t gate_bytes, const void* up,
                                 size_t up_bytes, const void* x, int x_dtype, size_t T, size_t H,
-                                size_t Is, float* out) {
+                                size_t Is, float* out, void* workspace, size_t workspace_bytes) {
   clear_error();
   INF_CHECK_ARG(H % kKBlock == 0 && Is > 0 && H > 0, "Q8_0 in_features must be a multiple of 256");
   INF_CHECK_ARG(x_dtype == INFERNO_F32 || x_dtype == INFERNO_BF16, "x dtype must be F32 or BF16");
@@ -253,21 +281,27 @@ int inferno_q8_0_gate_up_swiglu(void* stream, const void* gate, size_t gate_byte
   if ((st = check_len("shared up", up_bytes, 1, matrix_bytes(INFERNO_Q8_0, Is, H)))) return st;
   if (T == 0) return INFERNO_OK;
   INF_CHECK_ARG(gate && up && x && out, "null pointer");
-  return launch_gemv_gate_up_dense(as_stream(stream), INFERNO_Q8_0, gate, up, x, x_dtype, T, H,
-                                   Is, out);
+  if ((st = need_ws(workspace, workspace_bytes, gemv_stage_bytes(INFERNO_Q8_0, T, H, x_dtype))))
+    return st;
+  return launch_gemv_gate_up_dense(as_stream(stream), INFERNO_Q8_0, gate, up, x, x_dtype,
+                                   static_cast<uint32_t*>(workspace), false, T, H, Is, out);
 }
 
 int inferno_q8_0_matvec_add2(void* stream, const void* w, size_t w_bytes, const float* input,
                              const float* residual_a, const float* residual_b, size_t T,
-                             size_t In, size_t O, float* out) {
+                             size_t In, size_t O, float* out, void* workspace,
+                             size_t workspace_bytes) {
   clear_error();
   INF_CHECK_ARG(In % kKBlock == 0 && In > 0 && O > 0, "Q8_0 in_features must be a multiple of 256");
   int st;
   if ((st = check_len("shared down", w_bytes, 1, matrix_bytes(INFERNO_Q8_0, O, In)))) return st;
   if (T == 0) return INFERNO_OK;
   INF_CHECK_ARG(w && input && out, "null pointer");
-  return launch_gemv_down_dense(as_stream(stream), INFERNO_Q8_0, w, input, nullptr, 0,
-                                residual_a, residual_b, T, In, O, out);
+  if ((st = need_ws(workspace, workspace_bytes, gemv_stage_bytes(INFERNO_Q8_0, T, In, INFERNO_F32))))
+    return st;
+  return launch_gemv_down_dense(as_stream(stream), INFERNO_Q8_0, w, input,
+                                static_cast<uint32_t*>(workspace), nullptr, 0, residual_a,
+                                residual_b, T, In, O, out);
 }
 
 int inferno_moe_topk_combine_residual(void* stream, const float* shared, const float* residual,
@@ -315,6 +349,7 @@ struct LayerScratch {
   uint32_t* ids;
   float* weights;
   float* hs;
+  uint32_t* stage_hs;
   MoeScratch moe;
 };
 LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
@@ -323,6 +358,7 @@ LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   s.ids = c.take<uint32_t>(T * L->top_k);
   s.weights = c.take<float>(T * L->top_k);
   s.hs = c.take<float>(T * (L->shared_intermediate ? L->shared_intermediate : 1));
+  s.stage_hs = c.take<uint32_t>(L->shared_intermediate ? stage_words(T, L->shared_intermediate) : 1);
   s.moe = carve_moe(c, T, L->top_k, L->experts, L->hidden, L->intermediate);
   return s;
 }
@@ -375,15 +411,17 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
   if ((st = launch_router_topk(s, w.logits, L->router_bias, T, E, k, L->score_fn,
                                L->norm_topk_prob, L->routed_scaling_factor, ids, wts, nullptr)))
     return st;
+  // x is staged once for the routed and the shared gate/up
+  if ((st = launch_stage(s, x, x_dtype, T, H, w.moe.stage_x))) return st;
   if ((st = run_routed(s, L->quant, L->down_quant, L->gate, L->up, L->down, x, x_dtype, ids, wts,
-                       T, k, E, H, I, w.moe)))
+                       T, k, E, H, I, w.moe, true)))
     return st;
   if (Is) {
     if ((st = launch_gemv_gate_up_dense(s, INFERNO_Q8_0, L->shared_gate, L->shared_up, x, x_dtype,
-                                        T, H, Is, w.hs)))
+                                        w.moe.stage_x, true, T, H, Is, w.hs)))
       return st;
-    return launch_gemv_down_dense(s, INFERNO_Q8_0, L->shared_down, w.hs, w.moe.y, k, nullptr,
-                                  residual, T, Is, H, out);
+    return launch_gemv_down_dense(s, INFERNO_Q8_0, L->shared_down, w.hs, w.stage_hs, w.moe.y, k,
+                                  nullptr, residual, T, Is, H, out);
   }
   return launch_topk_combine(s, nullptr, residual, w.moe.y, nullptr, T, H, k, out);
 }

@@ -13,7 +13,7 @@
 // down -> per-assignment rows; dense down -> residual_a + residual_b + value
 // (q2_kernels.metal:2066-2131), where residual_a may be the rank-order sum of
 // the per-assignment routed rows (moe_kernels.metal:210-238).
-#include "kernels.hpp"
+#include "gemv_common.hpp"
 
 namespace inferno {
 namespace {
@@ -21,9 +21,7 @@ namespace {
 constexpr int kRowsPerWave = 8;
 constexpr int kRowsPerBlock = 4 * kRowsPerWave;
 
-__device__ __forceinline__ uint32_t ld32(const uint8_t* p) {
-  return *reinterpret_cast<const uint32_t __attribute__((aligned(1)))*>(p);
-}
+__device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return ld_u1(p); }
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
 
 // Value offsets (within the 256-value super-block) of the lane's four runs
@@ -162,40 +160,6 @@ __device__ __forceinline__ void decode_lane(const uint8_t* __restrict__ sb, int 
   }
 }
 
-enum Mode { kGateUpRouted = 0, kGateUpDense = 1, kDownRouted = 2, kDownDense = 3 };
-
-template <typename XT>
-__device__ __forceinline__ float to_f32(XT v);
-template <>
-__device__ __forceinline__ float to_f32<float>(float v) {
-  return v;
-}
-template <>
-__device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) {
-  return bf16_bits_to_f32(v);
-}
-
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
-
-struct GemvArgs {
-  const uint8_t* w0;       // gate (gate/up modes) or down
-  const uint8_t* w1;       // up (gate/up modes)
-  const void* x;           // [tokens or assignments, K]
-  const uint32_t* offsets; // [E+1] (routed)
-  const uint32_t* sorted;  // [A]   (routed)
-  const uint32_t* active;  // [1+E] (routed)
-  const float* route_w;    // [A]   (routed gate/up)
-  float* out;
-  const float* yk;         // dense down: per-assignment routed rows [T*k, rows] or null
-  const float* res_a;      // dense down: residual_a or null (ignored when yk set)
-  const float* res_b;      // dense down: residual_b or null
-  int rows;                // output rows per expert
-  int K;                   // reduction length
-  int k;                   // top-k (routed / yk)
-  int n_tokens;            // dense: T
-  size_t expert_stride;    // bytes per expert matrix
-};
-
 template <int Q, int MODE, typename XT, int NT>
 __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs p) {
   extern __shared__ float xs[];  // [NT][K]
@@ -326,22 +290,45 @@ int launch_mode(hipStream_t s, int quant, const GemvArgs& a, int n_slots, int nt
 }
 
 // Tokens per LDS chunk: every group of a T=1 step has one member; otherwise
-// as many as fit in 32 KiB of fp32 activations (at most 4).
-int pick_nt(size_t T, size_t K) {
+// as many as fit in 32 KiB of staged activations (at most 4).
+int pick_nt(size_t T, size_t bytes_per_row) {
   if (T <= 1) return 1;
-  size_t fit = (32 * 1024) / (K * sizeof(float));
+  size_t fit = (32 * 1024) / bytes_per_row;
   if (fit >= 4) return 4;
   if (fit >= 2) return 2;
   return 1;
 }
 
+// Runs MODE through the packed-f16 kernel when the format has one (staging
+// the activation rows first unless `staged_ready`), else through the fp32
+// reference-layout kernel.
+template <int MODE>
+int run(hipStream_t s, int quant, GemvArgs& a, const void* x, int x_dtype, size_t stage_rows,
+        uint32_t* stage, bool staged_ready, size_t T, int n_slots) {
+  if (dot2_supported(quant)) {
+    if (!staged_ready) {
+      int st = launch_stage(s, x, x_dtype, stage_rows, size_t(a.K), stage);
+      if (st) return st;
+    }
+    const size_t row_bytes = staged_bytes(1, size_t(a.K), x_dtype);
+    return launch_dot2<MODE>(s, quant, a, stage, x_dtype, n_slots, pick_nt(T, row_bytes));
+  }
+  const int nt = pick_nt(T, size_t(a.K) * sizeof(float));
+  if (x_dtype == INFERNO_BF16) return launch_mode<MODE, uint16_t>(s, quant, a, n_slots, nt);
+  return launch_mode<MODE, float>(s, quant, a, n_slots, nt);
+}
+
 }  // namespace
 
+size_t gemv_stage_bytes(int quant, size_t rows, size_t K, int x_dtype) {
+  return dot2_supported(quant) ? staged_bytes(rows, K, x_dtype) : 0;
+}
+
 int launch_gemv_gate_up_routed(hipStream_t s, int quant, const void* gate, const void* up,
-                               const void* x, int x_dtype, const uint32_t* offsets,
-                               const uint32_t* sorted, const uint32_t* active,
-                               const float* route_w, size_t T, size_t k, size_t E, size_t H,
-                               size_t I, float* h_out) {
+                               const void* x, int x_dtype, uint32_t* stage, bool staged_ready,
+                               const uint32_t* offsets, const uint32_t* sorted,
+                               const uint32_t* active, const float* route_w, size_t T, size_t k,
+                               size_t E, size_t H, size_t I, float* h_out) {
   GemvArgs a{};
   a.w0 = static_cast<const uint8_t*>(gate);
   a.w1 = static_cast<const uint8_t*>(up);
@@ -355,14 +342,12 @@ int launch_gemv_gate_up_routed(hipStream_t s, int quant, const void* gate, const
   a.K = int(H);
   a.k = int(k);
   a.expert_stride = I * (H / kKBlock) * size_t(super_bytes(quant));
-  int slots = int(std::min(E, T * k));
-  int nt = pick_nt(T, H);
-  if (x_dtype == INFERNO_BF16) return launch_mode<kGateUpRouted, uint16_t>(s, quant, a, slots, nt);
-  return launch_mode<kGateUpRouted, float>(s, quant, a, slots, nt);
+  return run<kGateUpRouted>(s, quant, a, x, x_dtype, T, stage, staged_ready, T,
+                            int(std::min(E, T * k)));
 }
 
 int launch_gemv_down_routed(hipStream_t s, int quant, const void* down, const float* h,
-                            const uint32_t* offsets, const uint32_t* sorted,
+                            uint32_t* stage, const uint32_t* offsets, const uint32_t* sorted,
                             const uint32_t* active, size_t T, size_t k, size_t E, size_t H,
                             size_t I, float* y_out) {
   GemvArgs a{};
@@ -376,13 +361,13 @@ int launch_gemv_down_routed(hipStream_t s, int quant, const void* down, const fl
   a.K = int(I);
   a.k = int(k);
   a.expert_stride = H * (I / kKBlock) * size_t(super_bytes(quant));
-  int slots = int(std::min(E, T * k));
-  return launch_mode<kDownRouted, float>(s, quant, a, slots, pick_nt(T, I));
+  return run<kDownRouted>(s, quant, a, h, INFERNO_F32, T * k, stage, false, T,
+                          int(std::min(E, T * k)));
 }
 
 int launch_gemv_gate_up_dense(hipStream_t s, int quant, const void* gate, const void* up,
-                              const void* x, int x_dtype, size_t T, size_t H, size_t I,
-                              float* out) {
+                              const void* x, int x_dtype, uint32_t* stage, bool staged_ready,
+                              size_t T, size_t H, size_t I, float* out) {
   GemvArgs a{};
   a.w0 = static_cast<const uint8_t*>(gate);
   a.w1 = static_cast<const uint8_t*>(up);
@@ -391,14 +376,12 @@ int launch_gemv_gate_up_dense(hipStream_t s, int quant, const void* gate, const 
   a.rows = int(I);
   a.K = int(H);
   a.n_tokens = int(T);
-  int nt = pick_nt(T, H);
-  if (x_dtype == INFERNO_BF16) return launch_mode<kGateUpDense, uint16_t>(s, quant, a, 1, nt);
-  return launch_mode<kGateUpDense, float>(s, quant, a, 1, nt);
+  return run<kGateUpDense>(s, quant, a, x, x_dtype, T, stage, staged_ready, T, 1);
 }
 
 int launch_gemv_down_dense(hipStream_t s, int quant, const void* w, const float* input,
-                           const float* yk, size_t k, const float* res_a, const float* res_b,
-                           size_t T, size_t In, size_t O, float* out) {
+                           uint32_t* stage, const float* yk, size_t k, const float* res_a,
+                           const float* res_b, size_t T, size_t In, size_t O, float* out) {
   GemvArgs a{};
   a.w0 = static_cast<const uint8_t*>(w);
   a.x = input;
@@ -410,7 +393,7 @@ int launch_gemv_down_dense(hipStream_t s, int quant, const void* w, const float*
   a.rows = int(O);
   a.K = int(In);
   a.n_tokens = int(T);
-  return launch_mode<kDownDense, float>(s, quant, a, 1, pick_nt(T, In));
+  return run<kDownDense>(s, quant, a, input, INFERNO_F32, T, stage, false, T, 1);
 }
 
 }  // namespace inferno

@@ -21,21 +21,26 @@ int launch_router_topk(hipStream_t s, const float* logits, const float* bias, si
 int launch_dispatch(hipStream_t s, const uint32_t* ids, size_t T, size_t k, size_t E,
                     uint32_t* offsets, uint32_t* sorted, uint32_t* active);
 
+// GEMV stages. Packed-f16 formats (Q2_K, Q3_K, Q4_K, Q8_0) stage their
+// activation rows into `stage` (gemv_stage_bytes bytes) first; with
+// staged_ready the rows are already there (the layer stages x once for the
+// routed and the shared gate/up).
+size_t gemv_stage_bytes(int quant, size_t rows, size_t K, int x_dtype);
 int launch_gemv_gate_up_routed(hipStream_t s, int quant, const void* gate, const void* up,
-                               const void* x, int x_dtype, const uint32_t* offsets,
-                               const uint32_t* sorted, const uint32_t* active,
-                               const float* route_w, size_t T, size_t k, size_t E, size_t H,
-                               size_t I, float* h_out);
+                               const void* x, int x_dtype, uint32_t* stage, bool staged_ready,
+                               const uint32_t* offsets, const uint32_t* sorted,
+                               const uint32_t* active, const float* route_w, size_t T, size_t k,
+                               size_t E, size_t H, size_t I, float* h_out);
 int launch_gemv_down_routed(hipStream_t s, int quant, const void* down, const float* h,
-                            const uint32_t* offsets, const uint32_t* sorted,
+                            uint32_t* stage, const uint32_t* offsets, const uint32_t* sorted,
                             const uint32_t* active, size_t T, size_t k, size_t E, size_t H,
                             size_t I, float* y_out);
 int launch_gemv_gate_up_dense(hipStream_t s, int quant, const void* gate, const void* up,
-                              const void* x, int x_dtype, size_t T, size_t H, size_t I,
-                              float* out);
+                              const void* x, int x_dtype, uint32_t* stage, bool staged_ready,
+                              size_t T, size_t H, size_t I, float* out);
 int launch_gemv_down_dense(hipStream_t s, int quant, const void* w, const float* input,
-                           const float* yk, size_t k, const float* res_a, const float* res_b,
-                           size_t T, size_t In, size_t O, float* out);
+                           uint32_t* stage, const float* yk, size_t k, const float* res_a,
+                           const float* res_b, size_t T, size_t In, size_t O, float* out);
 
 int launch_topk_combine(hipStream_t s, const float* shared, const float* residual,
                         const float* expert_outputs, const float* expert_weights, size_t T,

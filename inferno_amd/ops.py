@@ -85,40 +85,53 @@ def gguf_moe(quant, down_quant, gate, up, down, x, ids, weights, k, E, I):
     return out
 
 
+def gemv_workspace(rows, K, device):
+    n = lib().inferno_gemv_workspace_bytes(rows, K)
+    return torch.empty(max(n, 1), dtype=torch.uint8, device=device)
+
+
 def expert_gate_up_swiglu(quant, gate, up, x, offsets, sorted_, active, weights, k, E, I,
-                          out=None):
+                          out=None, ws=None):
     T, H = x.shape
     if out is None:
         out = torch.empty(T * k, I, dtype=torch.float32, device=x.device)
+    if ws is None:
+        ws = gemv_workspace(T, H, x.device)
     check(lib().inferno_moe_expert_gate_up_swiglu(
         _s(), quant, _p(gate), gate.numel(), _p(up), up.numel(), _p(_dev(x)), _DT[x.dtype],
-        _p(offsets), _p(sorted_), _p(active), _p(weights), T, k, E, H, I, _p(out)))
+        _p(offsets), _p(sorted_), _p(active), _p(weights), T, k, E, H, I, _p(out), _p(ws),
+        ws.numel()))
     return out
 
 
-def expert_down(down_quant, down, h, offsets, sorted_, active, T, k, E, H, out=None):
+def expert_down(down_quant, down, h, offsets, sorted_, active, T, k, E, H, out=None, ws=None):
     I = h.shape[1]
     if out is None:
         out = torch.empty(T * k, H, dtype=torch.float32, device=h.device)
+    if ws is None:
+        ws = gemv_workspace(T * k, I, h.device)
     check(lib().inferno_moe_expert_down(_s(), down_quant, _p(down), down.numel(), _p(_dev(h)),
                                         _p(offsets), _p(sorted_), _p(active), T, k, E, H, I,
-                                        _p(out)))
+                                        _p(out), _p(ws), ws.numel()))
     return out
 
 
 def q8_0_gate_up_swiglu(gate, up, x, Is):
     T, H = x.shape
     out = torch.empty(T, Is, dtype=torch.float32, device=x.device)
+    ws = gemv_workspace(T, H, x.device)
     check(lib().inferno_q8_0_gate_up_swiglu(_s(), _p(gate), gate.numel(), _p(up), up.numel(),
-                                            _p(_dev(x)), _DT[x.dtype], T, H, Is, _p(out)))
+                                            _p(_dev(x)), _DT[x.dtype], T, H, Is, _p(out), _p(ws),
+                                            ws.numel()))
     return out
 
 
 def q8_0_matvec_add2(w, inp, residual_a, residual_b, O):
     T, In = inp.shape
     out = torch.empty(T, O, dtype=torch.float32, device=inp.device)
+    ws = gemv_workspace(T, In, inp.device)
     check(lib().inferno_q8_0_matvec_add2(_s(), _p(w), w.numel(), _p(_dev(inp)), _p(residual_a),
-                                         _p(residual_b), T, In, O, _p(out)))
+                                         _p(residual_b), T, In, O, _p(out), _p(ws), ws.numel()))
     return out
 
 
