@@ -6,6 +6,7 @@
 #include <string>
 #include <vector>
 
+#include "decode.hpp"
 #include "gemv_common.hpp"
 #include "quantize.hpp"
 
@@ -111,11 +112,15 @@ int run_routed(hipStream_t s, int quant, int down_quant, const void* gate, const
                const MoeScratch& m, bool x_staged) {
   int st;
   if ((st = launch_dispatch(s, ids, T, k, E, m.offsets, m.sorted, m.active))) return st;
+  // gate/up writes h already staged for the down pass (when the down kind has a
+  // packed-f16 kernel; Q6_K reads the fp32 h)
+  const bool h_staged = dot2_supported(down_quant);
   if ((st = launch_gemv_gate_up_routed(s, quant, gate, up, x, x_dtype, m.stage_x, x_staged,
-                                       m.offsets, m.sorted, m.active, w, T, k, E, H, I, m.h)))
+                                       m.offsets, m.sorted, m.active, w, T, k, E, H, I, m.h,
+                                       h_staged ? m.stage_h : nullptr)))
     return st;
-  return launch_gemv_down_routed(s, down_quant, down, m.h, m.stage_h, m.offsets, m.sorted,
-                                 m.active, T, k, E, H, I, m.y);
+  return launch_gemv_down_routed(s, down_quant, down, m.h, m.stage_h, h_staged, m.offsets,
+                                 m.sorted, m.active, T, k, E, H, I, m.y);
 }
 
 int need_ws(void* ws, size_t have, size_t need) {
@@ -250,7 +255,7 @@ int inferno_moe_expert_gate_up_swiglu(void* stream, int quant, const void* gate,
   if ((st = need_ws(workspace, workspace_bytes, gemv_stage_bytes(quant, T, H, x_dtype)))) return st;
   return launch_gemv_gate_up_routed(as_stream(stream), quant, gate, up, x, x_dtype,
                                     static_cast<uint32_t*>(workspace), false, offsets, sorted,
-                                    active, expert_weights, T, k, E, H, I, h);
+                                    active, expert_weights, T, k, E, H, I, h, nullptr);
 }
 
 int inferno_moe_expert_down(void* stream, int down_quant, const void* down, size_t down_bytes,
@@ -266,8 +271,8 @@ int inferno_moe_expert_down(void* stream, int down_quant, const void* down, size
                     gemv_stage_bytes(down_quant, T * k, I, INFERNO_F32))))
     return st;
   return launch_gemv_down_routed(as_stream(stream), down_quant, down, h,
-                                 static_cast<uint32_t*>(workspace), offsets, sorted, active, T, k,
-                                 E, H, I, y);
+                                 static_cast<uint32_t*>(workspace), false, offsets, sorted, active,
+                                 T, k, E, H, I, y);
 }
 
 int inferno_q8_0_gate_up_swiglu(void* stream, const void* gate, size_t gate_bytes, const void* up,
@@ -284,7 +289,8 @@ int inferno_q8_0_gate_up_swiglu(void* stream, const void* gate, size_t gate_byte
   if ((st = need_ws(workspace, workspace_bytes, gemv_stage_bytes(INFERNO_Q8_0, T, H, x_dtype))))
     return st;
   return launch_gemv_gate_up_dense(as_stream(stream), INFERNO_Q8_0, gate, up, x, x_dtype,
-                                   static_cast<uint32_t*>(workspace), false, T, H, Is, out);
+                                   static_cast<uint32_t*>(workspace), false, T, H, Is, out,
+                                   nullptr);
 }
 
 int inferno_q8_0_matvec_add2(void* stream, const void* w, size_t w_bytes, const float* input,
@@ -300,7 +306,7 @@ int inferno_q8_0_matvec_add2(void* stream, const void* w, size_t w_bytes, const 
   if ((st = need_ws(workspace, workspace_bytes, gemv_stage_bytes(INFERNO_Q8_0, T, In, INFERNO_F32))))
     return st;
   return launch_gemv_down_dense(as_stream(stream), INFERNO_Q8_0, w, input,
-                                static_cast<uint32_t*>(workspace), nullptr, 0, residual_a,
+                                static_cast<uint32_t*>(workspace), false, nullptr, 0, residual_a,
                                 residual_b, T, In, O, out);
 }
 
@@ -351,6 +357,9 @@ struct LayerScratch {
   float* hs;
   uint32_t* stage_hs;
   MoeScratch moe;
+  // fused decode path
+  float* partials;
+  float* ys;
 };
 LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   LayerScratch s;
@@ -360,6 +369,8 @@ LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   s.hs = c.take<float>(T * (L->shared_intermediate ? L->shared_intermediate : 1));
   s.stage_hs = c.take<uint32_t>(L->shared_intermediate ? stage_words(T, L->shared_intermediate) : 1);
   s.moe = carve_moe(c, T, L->top_k, L->experts, L->hidden, L->intermediate);
+  s.partials = c.take<float>(size_t(L->hidden / decode_chunk(L->hidden)) * T * L->experts);
+  s.ys = c.take<float>(T * L->hidden);
   return s;
 }
 }  // namespace
@@ -407,6 +418,25 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
   hipStream_t s = as_stream(stream);
   uint32_t* ids = expert_ids_out ? expert_ids_out : w.ids;
   float* wts = expert_weights_out ? expert_weights_out : w.weights;
+  if (decode_supported(T, k, E, L->quant, L->down_quant)) {
+    DecodeArgs d{};
+    d.T = int(T); d.H = int(H); d.E = int(E); d.I = int(I); d.k = int(k); d.Is = int(Is);
+    d.score_fn = L->score_fn; d.norm = L->norm_topk_prob; d.scale = L->routed_scaling_factor;
+    d.x = x; d.x_dtype = x_dtype; d.router = L->router; d.bias = L->router_bias;
+    d.gate = static_cast<const uint8_t*>(L->gate);
+    d.up = static_cast<const uint8_t*>(L->up);
+    d.down = static_cast<const uint8_t*>(L->down);
+    d.gate_stride = matrix_bytes(L->quant, I, H);
+    d.down_stride = matrix_bytes(L->down_quant, H, I);
+    d.sgate = static_cast<const uint8_t*>(L->shared_gate);
+    d.sup = static_cast<const uint8_t*>(L->shared_up);
+    d.sdown = static_cast<const uint8_t*>(L->shared_down);
+    d.residual = residual; d.out = out; d.ids = ids; d.weights = wts;
+    d.partials = w.partials; d.stage_x = w.moe.stage_x; d.offsets = w.moe.offsets;
+    d.sorted = w.moe.sorted; d.active = w.moe.active; d.stage_h = w.moe.stage_h;
+    d.stage_hs = w.stage_hs; d.y = w.moe.y; d.ys = w.ys;
+    return launch_decode_layer(s, d, L->quant);
+  }
   if ((st = launch_router_logits(s, x, x_dtype, L->router, T, H, E, w.logits))) return st;
   if ((st = launch_router_topk(s, w.logits, L->router_bias, T, E, k, L->score_fn,
                                L->norm_topk_prob, L->routed_scaling_factor, ids, wts, nullptr)))
@@ -418,10 +448,10 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
     return st;
   if (Is) {
     if ((st = launch_gemv_gate_up_dense(s, INFERNO_Q8_0, L->shared_gate, L->shared_up, x, x_dtype,
-                                        w.moe.stage_x, true, T, H, Is, w.hs)))
+                                        w.moe.stage_x, true, T, H, Is, w.hs, w.stage_hs)))
       return st;
-    return launch_gemv_down_dense(s, INFERNO_Q8_0, L->shared_down, w.hs, w.stage_hs, w.moe.y, k,
-                                  nullptr, residual, T, Is, H, out);
+    return launch_gemv_down_dense(s, INFERNO_Q8_0, L->shared_down, w.hs, w.stage_hs, true,
+                                  w.moe.y, k, nullptr, residual, T, Is, H, out);
   }
   return launch_topk_combine(s, nullptr, residual, w.moe.y, nullptr, T, H, k, out);
 }

@@ -1,0 +1,47 @@
+// Fused decode path of one MoE layer (decode.hip).
+#pragma once
+#include <type_traits>
+
+#include "kernels.hpp"
+
+namespace inferno {
+
+struct DecodeArgs {
+  int T, H, E, I, k, Is;
+  int score_fn, norm;
+  float scale;
+  const void* x;
+  int x_dtype;
+  const float* router;  // [E, H] fp32
+  const float* bias;    // [E] or null
+  const uint8_t* gate;  // routed packed experts
+  const uint8_t* up;
+  const uint8_t* down;
+  size_t gate_stride;   // bytes per expert (gate, up)
+  size_t down_stride;   // bytes per expert (down)
+  const uint8_t* sgate; // Q8_0 shared expert (null when Is == 0)
+  const uint8_t* sup;
+  const uint8_t* sdown;
+  const float* residual;  // [T, H] or null
+  float* out;             // [T, H]
+  uint32_t* ids;          // [T*k]
+  float* weights;         // [T*k]
+  // workspace
+  float* partials;        // [n_chunks, T, E]
+  uint32_t* stage_x;      // [T, staged_stride(H, x fp32)]
+  uint32_t* offsets;      // [E+1]
+  uint32_t* sorted;       // [T*k]
+  uint32_t* active;       // [E+1]
+  uint32_t* stage_h;      // [T*k, staged_stride(I, true)]
+  uint32_t* stage_hs;     // [T, staged_stride(Is, true)]
+  float* y;               // [T*k, H]
+  float* ys;              // [T, H]
+  // filled by launch_decode_layer
+  int chunk, n_chunks, max_slots;
+};
+
+bool decode_supported(size_t T, size_t k, size_t E, int quant, int down_quant);
+int decode_chunk(size_t H);
+int launch_decode_layer(hipStream_t s, const DecodeArgs& a, int quant);
+
+}  // namespace inferno

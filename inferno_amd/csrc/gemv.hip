@@ -328,8 +328,10 @@ int launch_gemv_gate_up_routed(hipStream_t s, int quant, const void* gate, const
                                const void* x, int x_dtype, uint32_t* stage, bool staged_ready,
                                const uint32_t* offsets, const uint32_t* sorted,
                                const uint32_t* active, const float* route_w, size_t T, size_t k,
-                               size_t E, size_t H, size_t I, float* h_out) {
+                               size_t E, size_t H, size_t I, float* h_out,
+                               uint32_t* h_staged_out) {
   GemvArgs a{};
+  a.out_staged = h_staged_out;
   a.w0 = static_cast<const uint8_t*>(gate);
   a.w1 = static_cast<const uint8_t*>(up);
   a.x = x;
@@ -347,9 +349,9 @@ int launch_gemv_gate_up_routed(hipStream_t s, int quant, const void* gate, const
 }
 
 int launch_gemv_down_routed(hipStream_t s, int quant, const void* down, const float* h,
-                            uint32_t* stage, const uint32_t* offsets, const uint32_t* sorted,
-                            const uint32_t* active, size_t T, size_t k, size_t E, size_t H,
-                            size_t I, float* y_out) {
+                            uint32_t* stage, bool staged_ready, const uint32_t* offsets,
+                            const uint32_t* sorted, const uint32_t* active, size_t T, size_t k,
+                            size_t E, size_t H, size_t I, float* y_out) {
   GemvArgs a{};
   a.w0 = static_cast<const uint8_t*>(down);
   a.x = h;
@@ -361,14 +363,15 @@ int launch_gemv_down_routed(hipStream_t s, int quant, const void* down, const fl
   a.K = int(I);
   a.k = int(k);
   a.expert_stride = H * (I / kKBlock) * size_t(super_bytes(quant));
-  return run<kDownRouted>(s, quant, a, h, INFERNO_F32, T * k, stage, false, T,
+  return run<kDownRouted>(s, quant, a, h, INFERNO_F32, T * k, stage, staged_ready, T,
                           int(std::min(E, T * k)));
 }
 
 int launch_gemv_gate_up_dense(hipStream_t s, int quant, const void* gate, const void* up,
                               const void* x, int x_dtype, uint32_t* stage, bool staged_ready,
-                              size_t T, size_t H, size_t I, float* out) {
+                              size_t T, size_t H, size_t I, float* out, uint32_t* out_staged) {
   GemvArgs a{};
+  a.out_staged = out_staged;
   a.w0 = static_cast<const uint8_t*>(gate);
   a.w1 = static_cast<const uint8_t*>(up);
   a.x = x;
@@ -380,8 +383,9 @@ int launch_gemv_gate_up_dense(hipStream_t s, int quant, const void* gate, const 
 }
 
 int launch_gemv_down_dense(hipStream_t s, int quant, const void* w, const float* input,
-                           uint32_t* stage, const float* yk, size_t k, const float* res_a,
-                           const float* res_b, size_t T, size_t In, size_t O, float* out) {
+                           uint32_t* stage, bool staged_ready, const float* yk, size_t k,
+                           const float* res_a, const float* res_b, size_t T, size_t In, size_t O,
+                           float* out) {
   GemvArgs a{};
   a.w0 = static_cast<const uint8_t*>(w);
   a.x = input;
@@ -393,7 +397,7 @@ int launch_gemv_down_dense(hipStream_t s, int quant, const void* w, const float*
   a.rows = int(O);
   a.K = int(In);
   a.n_tokens = int(T);
-  return run<kDownDense>(s, quant, a, input, INFERNO_F32, T, stage, false, T, 1);
+  return run<kDownDense>(s, quant, a, input, INFERNO_F32, T, stage, staged_ready, T, 1);
 }
 
 }  // namespace inferno

@@ -15,6 +15,7 @@ struct GemvArgs {
   const uint32_t* active;   // [1+E] (routed)
   const float* route_w;     // [A]   (routed gate/up)
   float* out;
+  uint32_t* out_staged;     // gate/up: also write the output rows staged (fp32 layout) or null
   const float* yk;          // dense down: per-assignment routed rows [T*k, rows] or null
   const float* res_a;       // dense down: residual_a or null (ignored when yk set)
   const float* res_b;       // dense down: residual_b or null

@@ -30,17 +30,19 @@ int launch_gemv_gate_up_routed(hipStream_t s, int quant, const void* gate, const
                                const void* x, int x_dtype, uint32_t* stage, bool staged_ready,
                                const uint32_t* offsets, const uint32_t* sorted,
                                const uint32_t* active, const float* route_w, size_t T, size_t k,
-                               size_t E, size_t H, size_t I, float* h_out);
+                               size_t E, size_t H, size_t I, float* h_out,
+                               uint32_t* h_staged_out);
 int launch_gemv_down_routed(hipStream_t s, int quant, const void* down, const float* h,
-                            uint32_t* stage, const uint32_t* offsets, const uint32_t* sorted,
-                            const uint32_t* active, size_t T, size_t k, size_t E, size_t H,
-                            size_t I, float* y_out);
+                            uint32_t* stage, bool staged_ready, const uint32_t* offsets,
+                            const uint32_t* sorted, const uint32_t* active, size_t T, size_t k,
+                            size_t E, size_t H, size_t I, float* y_out);
 int launch_gemv_gate_up_dense(hipStream_t s, int quant, const void* gate, const void* up,
                               const void* x, int x_dtype, uint32_t* stage, bool staged_ready,
-                              size_t T, size_t H, size_t I, float* out);
+                              size_t T, size_t H, size_t I, float* out, uint32_t* out_staged);
 int launch_gemv_down_dense(hipStream_t s, int quant, const void* w, const float* input,
-                           uint32_t* stage, const float* yk, size_t k, const float* res_a,
-                           const float* res_b, size_t T, size_t In, size_t O, float* out);
+                           uint32_t* stage, bool staged_ready, const float* yk, size_t k,
+                           const float* res_a, const float* res_b, size_t T, size_t In, size_t O,
+                           float* out);
 
 int launch_topk_combine(hipStream_t s, const float* shared, const float* residual,
                         const float* expert_outputs, const float* expert_weights, size_t T,

@@ -7,7 +7,7 @@
 // sum, times the routed scaling factor. One wavefront per token; every lane
 // holds up to four candidates and each round is a 64-bit max-reduction of
 // (order-preserving score bits, ~expert id).
-#include "kernels.hpp"
+#include "routing_dev.hpp"
 
 namespace inferno {
 namespace {
@@ -23,11 +23,6 @@ __device__ __forceinline__ float load_x<uint16_t>(const uint16_t* p, size_t i) {
   return bf16_bits_to_f32(p[i]);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
-}
 
 // Few tokens: one wavefront per expert row; the row is read once with
 // 16-byte loads and dotted with every token (T <= 16).
@@ -108,119 +103,15 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-// Order-preserving map of the f32 total order (f32::total_cmp) onto u32.
-__device__ __forceinline__ uint32_t total_order_key(float f) {
-  uint32_t b = f32_to_bits(f);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    uint64_t o = __shfl_xor(v, m, kWave);
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
-  return v;
-}
-
 __global__ void __launch_bounds__(256)
     topk_kernel(const float* __restrict__ logits, const float* __restrict__ bias, int T, int E,
                 int k, int score_fn, int norm, float scale, uint32_t* __restrict__ ids,
                 float* __restrict__ weights, uint32_t* __restrict__ token_idx) {
-  constexpr int PER = kMaxExperts / kWave;  // 4 candidates per lane
-  const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  const float* row = logits + size_t(t) * E;
-  float lg[PER], score[PER];
-  uint64_t key[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    int e = lane + j * kWave;
-    lg[j] = e < E ? row[e] : -INFINITY;
-  }
-  float lmax = 0.f, denom_all = 0.f;
-  if (score_fn == INFERNO_SCORE_SOFTMAX) {
-    float m = lg[0];
-#pragma unroll
-    for (int j = 1; j < PER; ++j) m = fmaxf(m, lg[j]);
-    lmax = wave_max(m);
-  }
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    int e = lane + j * kWave;
-    float s, sel;
-    if (score_fn == INFERNO_SCORE_SIGMOID) {
-      s = 1.0f / (1.0f + expf(-lg[j]));
-      sel = s;
-    } else {
-      s = e < E ? expf(lg[j] - lmax) : 0.f;
-      sel = lg[j];
-    }
-    score[j] = s;
-    float corrected = sel + ((bias != nullptr && e < E) ? bias[e] : 0.0f);
-    key[j] = e < E ? ((uint64_t(total_order_key(corrected)) << 32) | uint64_t(0xffffffffu - uint32_t(e)))
-                   : 0ull;
-  }
-  if (score_fn == INFERNO_SCORE_SOFTMAX && !norm) {
-    float part = 0.f;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) part += score[j];
-    denom_all = wave_sum(part);
-  }
-  float sel_score[kMaxTopK];
-  uint32_t sel_id[kMaxTopK];
-#pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r) {
-    if (r < k) {
-      uint64_t best = key[0];
-#pragma unroll
-      for (int j = 1; j < PER; ++j) best = key[j] > best ? key[j] : best;
-      best = wave_max_u64(best);
-      uint32_t id = 0xffffffffu - uint32_t(best & 0xffffffffu);
-      int owner = int(id & 63u), slot = int(id >> 6);
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < PER; ++j)
-        if (j == slot) s = score[j];
-      s = __shfl(s, owner, kWave);
-      if (lane == owner) {
-#pragma unroll
-        for (int j = 0; j < PER; ++j)
-          if (j == slot) key[j] = 0ull;
-      }
-      sel_score[r] = s;
-      sel_id[r] = id;
-    }
-  }
-  if (lane == 0) {
-    float sum = 0.f;
-    if (norm) {
-#pragma unroll
-      for (int r = 0; r < kMaxTopK; ++r)
-        if (r < k) sum += sel_score[r];
-    } else if (score_fn == INFERNO_SCORE_SOFTMAX) {
-      sum = denom_all;
-    }
-    const bool divide = (norm || score_fn == INFERNO_SCORE_SOFTMAX) && sum > 0.f && isfinite(sum);
-#pragma unroll
-    for (int r = 0; r < kMaxTopK; ++r) {
-      if (r < k) {
-        float wv = sel_score[r];
-        if (divide) wv /= sum;
-        size_t a = size_t(t) * k + r;
-        ids[a] = sel_id[r];
-        weights[a] = wv * scale;
-        if (token_idx) token_idx[a] = uint32_t(t);
-      }
-    }
-  }
+  uint32_t sel[kMaxTopK];
+  topk_row_wave(logits + size_t(t) * E, bias, E, k, score_fn, norm, scale, t, ids, weights,
+                token_idx, sel);
 }
 
 }  // namespace

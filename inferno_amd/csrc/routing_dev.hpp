@@ -1,0 +1,234 @@
+// Device-side routing helpers shared by the router kernels and the fused
+// decode path: exact top-k per token on one wavefront
+// (crates/model/src/moe_router.rs:835-940 semantics) and the deterministic
+// single-workgroup dispatch.
+#pragma once
+#include "kernels.hpp"
+
+namespace inferno {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// Order-preserving map of the f32 total order (f32::total_cmp) onto u32.
+__device__ __forceinline__ uint32_t total_order_key(float f) {
+  uint32_t b = f32_to_bits(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    uint64_t o = __shfl_xor(v, m, kWave);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
+// Exact top-k of one token's logits by one wavefront (lane holds experts
+// lane, lane+64, lane+128, lane+192). `row` may live in global memory or LDS.
+// Lane 0 stores the results; every lane also gets the selected ids in rank
+// order in `sel_id` (wave-uniform).
+__device__ __forceinline__ void topk_row_wave(const float* row, const float* __restrict__ bias,
+                                              int E, int k, int score_fn, int norm, float scale,
+                                              int t, uint32_t* __restrict__ ids,
+                                              float* __restrict__ weights,
+                                              uint32_t* __restrict__ token_idx,
+                                              uint32_t (&sel_id)[kMaxTopK]) {
+  constexpr int PER = kMaxExperts / kWave;  // 4 candidates per lane
+  const int lane = threadIdx.x & 63;
+  float lg[PER], score[PER];
+  uint64_t key[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    int e = lane + j * kWave;
+    lg[j] = e < E ? row[e] : -INFINITY;
+  }
+  float lmax = 0.f, denom_all = 0.f;
+  if (score_fn == INFERNO_SCORE_SOFTMAX) {
+    float m = lg[0];
+#pragma unroll
+    for (int j = 1; j < PER; ++j) m = fmaxf(m, lg[j]);
+    lmax = wave_max(m);
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    int e = lane + j * kWave;
+    float s, sel;
+    if (score_fn == INFERNO_SCORE_SIGMOID) {
+      s = 1.0f / (1.0f + expf(-lg[j]));
+      sel = s;
+    } else {
+      s = e < E ? expf(lg[j] - lmax) : 0.f;
+      sel = lg[j];
+    }
+    score[j] = s;
+    float corrected = sel + ((bias != nullptr && e < E) ? bias[e] : 0.0f);
+    key[j] = e < E ? ((uint64_t(total_order_key(corrected)) << 32) | uint64_t(0xffffffffu - uint32_t(e)))
+                   : 0ull;
+  }
+  if (score_fn == INFERNO_SCORE_SOFTMAX && !norm) {
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) part += score[j];
+    denom_all = wave_sum(part);
+  }
+  float sel_score[kMaxTopK];
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) sel_id[r] = 0xffffffffu;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    if (r < k) {
+      uint64_t best = key[0];
+#pragma unroll
+      for (int j = 1; j < PER; ++j) best = key[j] > best ? key[j] : best;
+      best = wave_max_u64(best);
+      uint32_t id = 0xffffffffu - uint32_t(best & 0xffffffffu);
+      int owner = int(id & 63u), slot = int(id >> 6);
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (j == slot) s = score[j];
+      s = __shfl(s, owner, kWave);
+      if (lane == owner) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+          if (j == slot) key[j] = 0ull;
+      }
+      sel_score[r] = s;
+      sel_id[r] = id;
+    }
+  }
+  if (lane == 0) {
+    float sum = 0.f;
+    if (norm) {
+#pragma unroll
+      for (int r = 0; r < kMaxTopK; ++r)
+        if (r < k) sum += sel_score[r];
+    } else if (score_fn == INFERNO_SCORE_SOFTMAX) {
+      sum = denom_all;
+    }
+    const bool divide = (norm || score_fn == INFERNO_SCORE_SOFTMAX) && sum > 0.f && isfinite(sum);
+#pragma unroll
+    for (int r = 0; r < kMaxTopK; ++r) {
+      if (r < k) {
+        float wv = sel_score[r];
+        if (divide) wv /= sum;
+        size_t a = size_t(t) * k + r;
+        ids[a] = sel_id[r];
+        weights[a] = wv * scale;
+        if (token_idx) token_idx[a] = uint32_t(t);
+      }
+    }
+  }
+}
+
+
+constexpr int kDispatchThreads = 1024;
+constexpr int kDispatchWaves = kDispatchThreads / kWave;
+
+
+// Body of the dispatch: must run on a 1024-thread workgroup; `ids` may
+// live in global memory or LDS.
+__device__ __forceinline__ void dispatch_block(const uint32_t* ids, int A, int E,
+                                               uint32_t* __restrict__ offsets,
+                                               uint32_t* __restrict__ sorted,
+                                               uint32_t* __restrict__ active) {
+  __shared__ uint32_t count[kMaxExperts];
+  __shared__ uint32_t cursor[kMaxExperts];
+  __shared__ uint32_t wcount[kDispatchWaves * kMaxExperts];  // [wave][expert], row stride E
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < E; e += kDispatchThreads) count[e] = 0;
+  __syncthreads();
+  for (int a = tid; a < A; a += kDispatchThreads) {
+    uint32_t e = ids[a];
+    if (e < uint32_t(E)) atomicAdd(&count[e], 1u);
+  }
+  __syncthreads();
+  // exclusive scan of counts and of the "has assignments" flags on wave 0:
+  // each lane owns four consecutive experts (E <= 256)
+  if (wave == 0) {
+    uint32_t c4[4], f4[4], cs = 0, fs = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * lane + j;
+      c4[j] = e < E ? count[e] : 0u;
+      f4[j] = c4[j] > 0 ? 1u : 0u;
+      cs += c4[j];
+      fs += f4[j];
+    }
+    uint32_t ci = cs, fi = fs;  // inclusive wave scans
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t cu = __shfl_up(ci, o, kWave), fu = __shfl_up(fi, o, kWave);
+      if (lane >= o) {
+        ci += cu;
+        fi += fu;
+      }
+    }
+    uint32_t cex = ci - cs, fex = fi - fs;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * lane + j;
+      if (e < E) {
+        offsets[e] = cex;
+        cursor[e] = cex;
+        if (c4[j] > 0) active[1 + fex] = uint32_t(e);
+      }
+      cex += c4[j];
+      fex += f4[j];
+    }
+    if (lane == 63) {
+      offsets[E] = ci;
+      active[0] = fi;
+    }
+  }
+  __syncthreads();
+
+  // stable scatter
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  for (int base = 0; base < A; base += kDispatchThreads) {
+    const int a = base + tid;
+    const bool valid = a < A;
+    const uint32_t e = valid ? ids[a] : 0xffffffffu;
+    const bool ok = valid && e < uint32_t(E);
+    uint64_t match = __ballot(ok);
+    for (int bit = 0; bit < nbits; ++bit) {
+      uint64_t b = __ballot(ok && ((e >> bit) & 1u));
+      match &= ((e >> bit) & 1u) ? b : ~b;
+    }
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const uint32_t rank = uint32_t(__popcll(match & lt));
+    const bool leader = ok && (match & lt) == 0ull;
+    // per-wave per-expert counts, written by each match group's first lane
+    for (int i = tid; i < kDispatchWaves * E; i += kDispatchThreads) wcount[i] = 0u;
+    __syncthreads();
+    if (leader) wcount[wave * E + int(e)] = uint32_t(__popcll(match));
+    __syncthreads();
+    if (ok) {
+      uint32_t before = 0;
+      for (int w = 0; w < wave; ++w) before += wcount[w * E + int(e)];
+      sorted[cursor[e] + before + rank] = uint32_t(a);
+    }
+    __syncthreads();
+    for (int ex = tid; ex < E; ex += kDispatchThreads) {
+      uint32_t tot = 0;
+      for (int w = 0; w < kDispatchWaves; ++w) tot += wcount[w * E + ex];
+      cursor[ex] += tot;
+    }
+    __syncthreads();
+  }
+}
+
+
+}  // namespace inferno
