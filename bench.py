@@ -8,9 +8,13 @@ one token. Several independent layers are resident in HBM and the steps
 cycle through them with a fresh token each, like a decode pass through a
 model, so the 256 MB Infinity Cache cannot hold the experts a step reads.
 
-The roofline leg times the dominant kernel (routed gate/up dequant-GEMV)
-alone with HIP events on the stream it runs on; its algorithmic bytes are
-the quantised gate+up bytes of the selected (unique) experts.
+The roofline leg re-runs the same layer steps with the library's event hook
+on: HIP events on the layer's stream bracket the dominant kernel (the routed
+gate/up dequant-GEMV of the fused decode path) and the routed down kernel.
+Algorithmic bytes per gate/up launch = quantised gate+up bytes of the step's
+unique selected experts. `traffic` (HBM bytes per launch) comes from the
+committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, scaled by the same
+counters read for a plain device copy of known size (--calibrate-copy).
 
 The cpu_baseline leg times the CPU oracle (test infrastructure, C++,
 multithreaded) on a bounded sample of the same decode workload.
@@ -41,9 +45,14 @@ def main():
     ap.add_argument("--config", default="c2")
     ap.add_argument("--tokens", type=int, default=0, help="T (default: the config's first)")
     ap.add_argument("--layers", type=int, default=8, help="resident layer copies")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 10 device copies of 256 MiB (counter calibration)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU expert parallelism is design-only)"}))
@@ -92,45 +101,47 @@ def main():
     ms_per_step = 1e3 * elapsed / args.steps
     tokens_per_s = T * args.steps / elapsed
 
-    # ---- dominant kernel alone: routed gate/up dequant-GEMV -------------
+    # ---- dominant kernel: routed gate/up of the fused decode path ---------
+    # Same layer steps again with the event hook on: the C library brackets
+    # the routed gate/up kernel (and the routed down kernel) with HIP events
+    # on the layer's stream. Algorithmic bytes per launch = quantised gate+up
+    # bytes of the step's unique selected experts.
     q = cfg.quants[0]
     bb = ops.block_bytes(q)
     gu_bytes_per_expert = 2 * I * (H // 256) * bb
-    expert_bytes = gu_bytes_per_expert + H * (I // 256) * bb
-    plans = []
-    for j in range(n_inputs):
-        l = j % L
-        lt = layers[l]
-        logits = ops.router_logits(xs[j], lt.router)
-        ids, w, _ = ops.router_topk(logits, lt.bias, k, cfg.score_fn, cfg.norm, cfg.scale)
-        off, srt, act = ops.dispatch(ids, T, k, E)
-        plans.append((lt, xs[j], off, srt, act, w, int(torch.unique(ids).numel())))
-    h_out = torch.empty(T * k, I, device=dev)
-    gws = ops.gemv_workspace(T, H, dev)
+    dn_bytes_per_expert = H * (I // 256) * bb
     reps = max(args.steps, 64)
-    for j in range(8):
-        lt, x, off, srt, act, w, _ = plans[j]
-        ops.expert_gate_up_swiglu(q, lt.gate, lt.up, x, off, srt, act, w, k, E, I, out=h_out,
-                                  ws=gws)
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    uniq = 0
-    for j in range(reps):
-        lt, x, off, srt, act, w, nu = plans[j % n_inputs]
-        ops.expert_gate_up_swiglu(q, lt.gate, lt.up, x, off, srt, act, w, k, E, I, out=h_out,
-                                  ws=gws)
-        uniq += nu
-    ev1.record()
-    torch.cuda.synchronize()
-    gu_us = 1e3 * ev0.elapsed_time(ev1) / reps
-    gu_bytes = gu_bytes_per_expert * uniq / reps
+    ops.kernel_timing(True)
+    try:
+        ops.kernel_timing_read(ops.TIMER_GATE_UP)
+        ops.kernel_timing_read(ops.TIMER_DOWN)
+        uniq = 0
+        for i in range(reps):
+            step(i)
+            l = i % L
+            uniq += int(torch.unique(ids_buf[l]).numel())
+        torch.cuda.synchronize()
+        gu_ms, gu_n = ops.kernel_timing_read(ops.TIMER_GATE_UP)
+        dn_ms, dn_n = ops.kernel_timing_read(ops.TIMER_DOWN)
+    finally:
+        ops.kernel_timing(False)
+    if gu_n != reps or dn_n != reps:
+        raise RuntimeError(f"kernel timers saw {gu_n}/{dn_n} launches for {reps} layer steps "
+                           "(the fused decode path did not run)")
+    uniq_layer = uniq / reps
+    gu_us = 1e3 * gu_ms / gu_n
+    dn_us = 1e3 * dn_ms / dn_n
+    gu_bytes = gu_bytes_per_expert * uniq_layer
     gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
+    dn_gbs = dn_bytes_per_expert * uniq_layer / (dn_us * 1e-6) / 1e9
 
-    # whole-layer algorithmic bytes (routed experts of the step's unique experts)
-    uniq_layer = np.mean([p[6] for p in plans])
-    layer_routed_bytes = expert_bytes * uniq_layer
+    # whole-layer bytes: routed experts of the step's unique experts, plus the
+    # shared expert (Q8_0), the fp32 router and the token's activations
+    layer_routed_bytes = (gu_bytes_per_expert + dn_bytes_per_expert) * uniq_layer
+    shared_bytes = 3 * cfg.shared_intermediate * (H // 32) * 34 if cfg.shared_intermediate else 0
+    router_bytes = E * H * 4
     layer_us = ms_per_step * 1e3
+    traffic = read_traffic(ROOT / "profiles" / "gate_up_q2k_c2_decode_traffic.txt")
 
     # ---- CPU baseline: oracle on the host cores -------------------------
     cpu = None
@@ -148,7 +159,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16-dot2/f32-acc",
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantised on device)",
         "config": {"workload": cfg.name, "tokens": T, "hidden": H, "experts": E,
                    "intermediate": I, "top_k": k, "quant": "Q2_K" if q == 10 else str(q),
@@ -156,13 +167,43 @@ def main():
         "us_per_token": round(layer_us / T, 3),
         "layer_routed_bytes": int(layer_routed_bytes),
         "layer_routed_GBps": round(layer_routed_bytes / (layer_us * 1e-6) / 1e9, 1),
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel<gate_up routed>",
+        "layer_total_bytes": int(layer_routed_bytes + shared_bytes + router_bytes),
+        "layer_total_GBps": round((layer_routed_bytes + shared_bytes + router_bytes)
+                                  / (layer_us * 1e-6) / 1e9, 1),
+        "roofline": {"bound": "hbm", "kernel": "gate_up_kernel<Q2_K, bf16, routed> (decode.hip)",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "launch_us": round(gu_us, 3), "bytes_per_launch": int(gu_bytes)},
+        "down_kernel": {"kernel": "down_sum_kernel<Q2_K> (decode.hip)", "launch_us": round(dn_us, 3),
+                        "GBps": round(dn_gbs, 1)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+
+
+def calibrate_copy():
+    """10 plain device-to-device copies of 256 MiB: the HBM counters of a
+    copy kernel of known size (256 MiB read + 256 MiB written per launch)."""
+    import torch
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(7)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": n, "launches": 10}), flush=True)
+
+
+def read_traffic(path):
+    """HBM bytes per launch of the roofline kernel, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (null when absent)."""
+    try:
+        for line in Path(path).read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(cfg, layers, xs, residual, T, seconds):
@@ -183,7 +224,7 @@ def cpu_baseline(cfg, layers, xs, residual, T, seconds):
     orc.THREADS = cores
     k, E = cfg.top_k, cfg.experts
     busy, n = 0.0, 0
-    while busy < seconds and n < 256:
+    while busy < seconds and n < 2048:
         lt = layers[n % len(layers)]
         x = xs[n % len(xs)][:1].float().cpu().numpy()
         router = lt.router.cpu().numpy()

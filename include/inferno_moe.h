@@ -244,6 +244,20 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* layer, cons
                               uint32_t* expert_ids_out, float* expert_weights_out,
                               void* workspace, size_t workspace_bytes);
 
+/* ------------------------------------------------------- kernel timing */
+
+/* Measurement hook with no counterpart in the reference (benchmarks only).
+ * While enabled, inferno_moe_layer_forward's fused decode path brackets its
+ * routed gate/up kernel and its routed down kernel with HIP events on the
+ * layer's stream, waits for the second event and adds the elapsed time to a
+ * process-wide accumulator. The wait serialises the host with the layer:
+ * leave timing off outside measurement. */
+enum { INFERNO_TIMER_GATE_UP = 0, INFERNO_TIMER_DOWN = 1 };
+int inferno_kernel_timing_enable(int enable);
+/* Returns the accumulated milliseconds and launch count of one timer and
+ * resets it. */
+int inferno_kernel_timing_read(int which, double* total_ms, uint64_t* launches);
+
 /* -------------------------------------------------------- synthetic data */
 
 /* Seeded synthetic inputs (splitmix64 + Box-Muller, counter based, so any

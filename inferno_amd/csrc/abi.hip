@@ -143,6 +143,19 @@ const char* inferno_last_error(void) { return g_last_error.c_str(); }
 int inferno_block_bytes(int quant) { return block_bytes(quant); }
 int inferno_block_values(int quant) { return block_values(quant); }
 
+int inferno_kernel_timing_enable(int enable) {
+  clear_error();
+  kernel_timing_enable(enable != 0);
+  return INFERNO_OK;
+}
+
+int inferno_kernel_timing_read(int which, double* total_ms, uint64_t* launches) {
+  clear_error();
+  INF_CHECK_ARG(total_ms && launches, "null output pointer");
+  INF_CHECK_ARG(kernel_timing_read(which, total_ms, launches), "unknown timer");
+  return INFERNO_OK;
+}
+
 int inferno_stream_synchronize(void* stream) {
   clear_error();
   INF_HIP(hipStreamSynchronize(as_stream(stream)));
@@ -360,6 +373,7 @@ struct LayerScratch {
   // fused decode path
   float* partials;
   float* ys;
+  uint4* slots;
 };
 LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   LayerScratch s;
@@ -371,6 +385,7 @@ LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   s.moe = carve_moe(c, T, L->top_k, L->experts, L->hidden, L->intermediate);
   s.partials = c.take<float>(size_t(L->hidden / decode_chunk(L->hidden)) * T * L->experts);
   s.ys = c.take<float>(T * L->hidden);
+  s.slots = c.take<uint4>(L->experts);
   return s;
 }
 }  // namespace
@@ -418,7 +433,7 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
   hipStream_t s = as_stream(stream);
   uint32_t* ids = expert_ids_out ? expert_ids_out : w.ids;
   float* wts = expert_weights_out ? expert_weights_out : w.weights;
-  if (decode_supported(T, k, E, L->quant, L->down_quant)) {
+  if (decode_supported(T, k, E, H, I, Is, x_dtype, L->quant, L->down_quant)) {
     DecodeArgs d{};
     d.T = int(T); d.H = int(H); d.E = int(E); d.I = int(I); d.k = int(k); d.Is = int(Is);
     d.score_fn = L->score_fn; d.norm = L->norm_topk_prob; d.scale = L->routed_scaling_factor;
@@ -434,7 +449,7 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
     d.residual = residual; d.out = out; d.ids = ids; d.weights = wts;
     d.partials = w.partials; d.stage_x = w.moe.stage_x; d.offsets = w.moe.offsets;
     d.sorted = w.moe.sorted; d.active = w.moe.active; d.stage_h = w.moe.stage_h;
-    d.stage_hs = w.stage_hs; d.y = w.moe.y; d.ys = w.ys;
+    d.stage_hs = w.stage_hs; d.ys = w.ys; d.slots = w.slots;
     return launch_decode_layer(s, d, L->quant);
   }
   if ((st = launch_router_logits(s, x, x_dtype, L->router, T, H, E, w.logits))) return st;

@@ -83,21 +83,41 @@ __global__ void __launch_bounds__(256) route_kernel(DecodeArgs p) {
 
 // ----------------------------------------------------------------- select
 
-// T = 1: one wavefront does everything. The k selected ids are distinct,
-// so the dispatch is the k ids sorted ascending (one assignment each).
-__global__ void __launch_bounds__(64) select1_kernel(DecodeArgs p) {
-  __shared__ float logit_row[kMaxExperts];
-  const int lane = threadIdx.x;
-  const int E = p.E, k = p.k;
-  for (int e = lane; e < E; e += 64) {
+// Sums the chunk partials of token t into an LDS logit row with all the
+// workgroup's threads; the loads of one expert's chunks are issued together.
+__device__ __forceinline__ void sum_partials(const DecodeArgs& p, int t, float* logit_row,
+                                             int first, int stride) {
+  const int E = p.E, T = p.T;
+  for (int e = first; e < E; e += stride) {
     float s = 0.f;
-    for (int c = 0; c < p.n_chunks; ++c) s += p.partials[size_t(c) * E + e];
+    for (int c0 = 0; c0 < p.n_chunks; c0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        v[c] = c0 + c < p.n_chunks ? p.partials[(size_t(c0 + c) * T + t) * E + e] : 0.f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) s += v[c];
+    }
     logit_row[e] = s;
   }
-  __builtin_amdgcn_wave_barrier();  // LDS is in order within a wavefront
+}
+
+// T = 1: the k selected ids are distinct, so the dispatch is the k ids
+// sorted ascending (one assignment each); wavefront 0 does top-k and the
+// dispatch after the workgroup has summed the partials.
+__global__ void __launch_bounds__(256) select1_kernel(DecodeArgs p) {
+  __shared__ float logit_row[kMaxExperts];
+  __shared__ float bias[kMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int E = p.E, k = p.k;
+  if (p.bias)
+    for (int e = tid; e < E; e += 256) bias[e] = p.bias[e];
+  sum_partials(p, 0, logit_row, tid, 256);
+  __syncthreads();
+  if (tid >= 64) return;
   uint32_t all[kMaxTopK];  // the k selected ids, held by every lane
-  topk_row_wave(logit_row, p.bias, E, k, p.score_fn, p.norm, p.scale, 0, p.ids, p.weights,
-                nullptr, all);
+  topk_row_wave(logit_row, p.bias ? bias : nullptr, E, k, p.score_fn, p.norm, p.scale, 0, p.ids,
+                p.weights, nullptr, all);
   uint32_t id = 0xffffffffu;
 #pragma unroll
   for (int j = 0; j < kMaxTopK; ++j)
@@ -109,6 +129,7 @@ __global__ void __launch_bounds__(64) select1_kernel(DecodeArgs p) {
   if (lane < k) {
     p.sorted[rank] = uint32_t(lane);  // assignment index t*k + r with t = 0
     p.active[1 + rank] = id;
+    p.slots[rank] = make_uint4(id, rank, rank + 1, uint32_t(lane));
   }
   if (lane == 0) p.active[0] = uint32_t(k);
   // offsets[e] = number of ids below e
@@ -122,25 +143,32 @@ __global__ void __launch_bounds__(64) select1_kernel(DecodeArgs p) {
 
 __global__ void __launch_bounds__(1024) select_kernel(DecodeArgs p) {
   __shared__ float logit_row[16][kMaxExperts];
+  __shared__ float bias[kMaxExperts];
   __shared__ uint32_t ids_lds[kMaxDecodeTokens * kMaxTopK];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = p.T, E = p.E, k = p.k;
+  if (p.bias)
+    for (int e = tid; e < E; e += 1024) bias[e] = p.bias[e];
+  __syncthreads();
   for (int t = wave; t < T; t += 16) {
-    for (int e = lane; e < E; e += 64) {
-      float s = 0.f;
-      for (int c = 0; c < p.n_chunks; ++c) s += p.partials[(size_t(c) * T + t) * E + e];
-      logit_row[wave][e] = s;
-    }
+    sum_partials(p, t, logit_row[wave], lane, 64);
     __builtin_amdgcn_wave_barrier();  // LDS is in order within a wavefront
     uint32_t sel[kMaxTopK];
-    topk_row_wave(logit_row[wave], p.bias, E, k, p.score_fn, p.norm, p.scale, t, p.ids,
-                  p.weights, nullptr, sel);
+    topk_row_wave(logit_row[wave], p.bias ? bias : nullptr, E, k, p.score_fn, p.norm, p.scale, t,
+                  p.ids, p.weights, nullptr, sel);
 #pragma unroll
     for (int r = 0; r < kMaxTopK; ++r)
       if (r < k && lane == r) ids_lds[t * k + r] = sel[r];
   }
   __syncthreads();
   dispatch_block(ids_lds, T * k, E, p.offsets, p.sorted, p.active);
+  // per-slot work descriptors; dispatch_block ended with a barrier, which
+  // orders this workgroup's global writes before these reads
+  const uint32_t n = p.active[0];
+  for (uint32_t j = tid; j < n; j += 1024) {
+    const uint32_t e = p.active[1 + j], lo = p.offsets[e];
+    p.slots[j] = make_uint4(e, lo, p.offsets[e + 1], p.sorted[lo]);
+  }
 }
 
 // ---------------------------------------------------------------- experts
@@ -164,32 +192,36 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
   const int tiles_i = I / kRows;
   const uint32_t item = blockIdx.x;
   constexpr bool shared = SHARED;
-  const uint32_t j = shared ? 0u : item / uint32_t(tiles_i);
-  if (!shared && j >= p.active[0]) return;
-  const int tile = shared ? int(item) : int(item % uint32_t(tiles_i));
-  const int row = tile * kRows + slot;
-  uint32_t* xs = smem;
-  float* part = reinterpret_cast<float*>(smem + Sx);
-  float* res = part + tile_part_floats(1);
-  uint32_t lo = 0, hi = uint32_t(T);
+  uint32_t lo = 0, hi = uint32_t(T), first = 0;
+  int tile = int(item);
   const uint8_t *r0, *r1;
   const size_t rb = size_t(H / kKBlock) * Fmt<Q>::kBytes;
   if constexpr (!shared) {
-    const uint32_t e = p.active[1 + j];
-    lo = p.offsets[e];
-    hi = p.offsets[e + 1];
-    r0 = p.gate + size_t(e) * p.gate_stride + size_t(row) * rb;
-    r1 = p.up + size_t(e) * p.gate_stride + size_t(row) * rb;
+    const uint32_t j = item / uint32_t(tiles_i);
+    const uint4 sl = p.slots[j];  // read before the bound check: one round trip
+    if (j >= p.active[0]) return;
+    tile = int(item % uint32_t(tiles_i));
+    const size_t off = size_t(sl.x) * p.gate_stride + size_t(tile * kRows + slot) * rb;
+    r0 = p.gate + off;
+    r1 = p.up + off;
+    lo = sl.y;
+    hi = sl.z;
+    first = sl.w;
   } else {
-    r0 = p.sgate + size_t(row) * rb;
-    r1 = p.sup + size_t(row) * rb;
+    r0 = p.sgate + size_t(tile * kRows + slot) * rb;
+    r1 = p.sup + size_t(tile * kRows + slot) * rb;
   }
+  uint32_t* xs = smem;
+  float* part = reinterpret_cast<float*>(smem + Sx);
+  float* res = part + tile_part_floats(1);
+  TileDot<Q, 2, 1, XSPLIT> td(r0, r1, H);
   for (uint32_t c = lo; c < hi; ++c) {
-    const uint32_t a = shared ? c : p.sorted[c];
+    const uint32_t a = shared ? c : (c == lo ? first : p.sorted[c]);
     const uint32_t tok = shared ? c : a / uint32_t(k);
+    td.prefetch();  // quant loads in flight while x is copied
     copy_rows_to_lds(xs, Sx, 1, [&](int) { return p.stage_x + size_t(tok) * Sx; });
     __syncthreads();
-    tile_dot<Q, 2, 1, XSPLIT>(r0, r1, H, xs, Sx, 1, part, res);
+    td.run(xs, Sx, 1, part, res);
     if (tid < 16) {
       if constexpr (!shared)
         swiglu_tile_out(res, 1, 0, p.weights[a], nullptr,
@@ -202,75 +234,102 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
   }
 }
 
-// down: routed grid = max_slots * tiles_h tiles writing rows of y (per
-// assignment); shared grid = tiles_h tiles writing rows of ys.
-template <int Q, bool SHARED>
+// Routed down with the combine folded in: one workgroup per (token, 16-row
+// output tile) runs through all k ranks' experts (the token's k staged h
+// rows sit in LDS), so the sum over ranks never leaves registers; then
+// out = residual + shared + routed. The four wavefronts take the
+// (rank, super-block column) pairs round robin and meet in LDS: a fixed
+// order, deterministic without float atomics.
+template <int Q>
+__global__ void __launch_bounds__(256) down_sum_kernel(DecodeArgs p) {
+  using F = Fmt<Q>;
+  extern __shared__ uint32_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int slot = lane >> 2, sub = lane & 3;
+  const int H = p.H, I = p.I, k = p.k;
+  const int tiles_h = H / kRows;
+  const int t = int(blockIdx.x) / tiles_h, tile = int(blockIdx.x) % tiles_h;
+  const int S = staged_stride(I, true);
+  uint32_t* xs = smem;                                   // k staged h rows
+  float* part = reinterpret_cast<float*>(smem + k * S);  // 4 * kRows
+  const int bpr = I / kKBlock;
+  const size_t rb = size_t(bpr) * F::kBytes;
+  const uint8_t* wrow = p.down + size_t(tile * kRows + slot) * rb;
+  const uint32_t* ids = p.ids + size_t(t) * k;
+  const int nq = k * bpr;
+  constexpr int kU = 4;
+  uint32_t raw[kU][F::kDw];
+  // pairs q = wave + 4 (u + kU i) -> rank q / bpr, column q % bpr
+  auto issue = [&](int q0) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int q = q0 + 4 * u;
+      if (q < nq) {
+        const int r = q / bpr, col = q - r * bpr;
+        F::load(wrow + size_t(ids[r]) * p.down_stride + size_t(col) * F::kBytes, sub, raw[u]);
+      }
+    }
+  };
+  issue(wave);  // quant loads in flight while the h rows are copied
+  // the token's k assignments t*k .. t*k+k-1 are consecutive rows
+  copy_to_lds<8>(reinterpret_cast<uint4*>(xs),
+              reinterpret_cast<const uint4*>(p.stage_h + size_t(t) * k * S), k * S / 4);
+  __syncthreads();
+  float acc = 0.f;
+  for (int q0 = wave; q0 < nq; q0 += 4 * kU) {
+    if (q0 != wave) issue(q0);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int q = q0 + 4 * u;
+      if (q < nq) {
+        const int r = q / bpr, col = q - r * bpr;
+        acc += F::dot(raw[u], sub, xrow_at<true>(xs + r * S, I, col));
+      }
+    }
+  }
+  acc += __shfl_xor(acc, 1, kWave);
+  acc += __shfl_xor(acc, 2, kWave);
+  if (sub == 0) part[wave * kRows + slot] = acc;
+  __syncthreads();
+  if (tid < kRows) {
+    const float v = ((part[tid] + part[kRows + tid]) + part[2 * kRows + tid]) + part[3 * kRows + tid];
+    const size_t o = size_t(t) * H + size_t(tile) * kRows + tid;
+    p.out[o] = ((p.residual ? p.residual[o] : 0.f) + (p.Is ? p.ys[o] : 0.f)) + v;
+  }
+}
+
+// Shared-expert down (Q8_0): one 16-row tile per workgroup, rows of ys.
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
-    down_kernel(DecodeArgs p) {
+    shared_down_kernel(DecodeArgs p) {
   extern __shared__ uint32_t smem[];
   const int tid = threadIdx.x, slot = (tid & 63) >> 2;
-  const int T = p.T, H = p.H, I = p.I, Is = p.Is;
-  const int tiles_h = H / kRows;
-  const uint32_t item = blockIdx.x;
-  constexpr bool shared = SHARED;
-  const uint32_t j = shared ? 0u : item / uint32_t(tiles_h);
-  if (!shared && j >= p.active[0]) return;
-  const int tile = shared ? int(item) : int(item % uint32_t(tiles_h));
+  const int T = p.T, H = p.H, Is = p.Is;
+  const int tile = int(blockIdx.x);
   const int row = tile * kRows + slot;
-  const int K = shared ? Is : I;
-  const int S = staged_stride(K, true);
+  const int S = staged_stride(Is, true);
   uint32_t* xs = smem;
   float* part = reinterpret_cast<float*>(smem + S);  // after the staged row
   float* res = part + tile_part_floats(1);
-  uint32_t lo = 0, hi = uint32_t(T);
-  const uint8_t* r0;
-  if constexpr (!shared) {
-    const uint32_t e = p.active[1 + j];
-    lo = p.offsets[e];
-    hi = p.offsets[e + 1];
-    r0 = p.down + size_t(e) * p.down_stride + size_t(row) * size_t(I / kKBlock) * Fmt<Q>::kBytes;
-  } else {
-    r0 = p.sdown + size_t(row) * size_t(Is / kKBlock) * Fmt<Q>::kBytes;
-  }
-  for (uint32_t c = lo; c < hi; ++c) {
-    const uint32_t orow = shared ? c : p.sorted[c];
-    copy_rows_to_lds(xs, S, 1, [&](int) {
-      return shared ? p.stage_hs + size_t(c) * S : p.stage_h + size_t(orow) * S;
-    });
+  const uint8_t* r0 = p.sdown + size_t(row) * size_t(Is / kKBlock) * Fmt<INFERNO_Q8_0>::kBytes;
+  TileDot<INFERNO_Q8_0, 1, 1, true> td(r0, nullptr, Is);
+  for (int c = 0; c < T; ++c) {
+    td.prefetch();
+    copy_rows_to_lds(xs, S, 1, [&](int) { return p.stage_hs + size_t(c) * S; });
     __syncthreads();
-    tile_dot<Q, 1, 1, true>(r0, nullptr, K, xs, S, 1, part, res);
-    if (tid < kRows) (shared ? p.ys : p.y)[size_t(orow) * H + tile * kRows + tid] = res[tid];
+    td.run(xs, S, 1, part, res);
+    if (tid < kRows) p.ys[size_t(c) * H + tile * kRows + tid] = res[tid];
     __syncthreads();
   }
 }
 
-// out = residual + ys + sum over ranks of y (rank order): one thread per output.
-__global__ void __launch_bounds__(256) combine_kernel(DecodeArgs p) {
-  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= size_t(p.T) * p.H) return;
-  const size_t t = i / p.H, r = i % p.H;
-  float y[kMaxTopK];
-#pragma unroll
-  for (int rk = 0; rk < kMaxTopK; ++rk)
-    y[rk] = rk < p.k ? p.y[(t * p.k + rk) * p.H + r] : 0.f;
-  float v = (p.residual ? p.residual[i] : 0.f) + (p.Is ? p.ys[i] : 0.f);
-#pragma unroll
-  for (int rk = 0; rk < kMaxTopK; ++rk)
-    if (rk < p.k) v += y[rk];
-  p.out[i] = v;
-}
+size_t down_sum_lds(int k, int I) { return (size_t(k) * staged_stride(I, true) + 4 * kRows) * 4; }
 
 template <int Q, bool XSPLIT>
-int launch_routed(hipStream_t s, const DecodeArgs& a) {
-  const size_t gu_tiles = size_t(a.max_slots) * (a.I / kRows);
-  const size_t gu_lds = (size_t(staged_stride(a.H, XSPLIT)) + tile_part_floats(1) + 2 * kRows) * 4;
-  gate_up_kernel<Q, XSPLIT, false><<<unsigned(gu_tiles), 256, gu_lds, s>>>(a);
-  INF_LAUNCHED();
-  const size_t dn_tiles = size_t(a.max_slots) * (a.H / kRows);
-  const size_t dn_lds = (size_t(staged_stride(a.I, true)) + tile_part_floats(1) + 2 * kRows) * 4;
-  down_kernel<Q, false><<<unsigned(dn_tiles), 256, dn_lds, s>>>(a);
-  INF_LAUNCHED();
-  return INFERNO_OK;
+void launch_gate_up(hipStream_t s, const DecodeArgs& a) {
+  const size_t tiles = size_t(a.max_slots) * (a.I / kRows);
+  const size_t lds = (size_t(staged_stride(a.H, XSPLIT)) + tile_part_floats(1) + 2 * kRows) * 4;
+  gate_up_kernel<Q, XSPLIT, false><<<unsigned(tiles), 256, lds, s>>>(a);
 }
 
 template <bool XSPLIT>
@@ -279,7 +338,7 @@ int launch_shared(hipStream_t s, const DecodeArgs& a) {
   gate_up_kernel<INFERNO_Q8_0, XSPLIT, true><<<unsigned(a.Is / kRows), 256, gu_lds, s>>>(a);
   INF_LAUNCHED();
   const size_t dn_lds = (size_t(staged_stride(a.Is, true)) + tile_part_floats(1) + 2 * kRows) * 4;
-  down_kernel<INFERNO_Q8_0, true><<<unsigned(a.H / kRows), 256, dn_lds, s>>>(a);
+  shared_down_kernel<<<unsigned(a.H / kRows), 256, dn_lds, s>>>(a);
   INF_LAUNCHED();
   return INFERNO_OK;
 }
@@ -311,12 +370,86 @@ int side_stream(SideStream** out) {
   return INFERNO_OK;
 }
 
+// Measurement hook: events around the routed expert kernels (see the C ABI).
+struct KernelTimers {
+  std::mutex mu;
+  bool on = false;
+  double ms[2] = {0, 0};
+  uint64_t n[2] = {0, 0};
+  hipEvent_t ev[64][2] = {};
+};
+KernelTimers& timers() {
+  static KernelTimers t;
+  return t;
+}
+
+// Launches `launch` on s; when timing is on, brackets it with events and
+// accumulates its elapsed time under `which`.
+template <typename Fn>
+int timed(hipStream_t s, int which, Fn launch) {
+  KernelTimers& tm = timers();
+  bool on;
+  {
+    std::lock_guard<std::mutex> lock(tm.mu);
+    on = tm.on;
+  }
+  if (!on) {
+    launch();
+    INF_LAUNCHED();
+    return INFERNO_OK;
+  }
+  int dev = 0;
+  INF_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) {
+    set_error("device index out of range");
+    return INFERNO_ERR_DEVICE;
+  }
+  hipEvent_t* ev = tm.ev[dev];
+  if (!ev[0]) {
+    INF_HIP(hipEventCreate(&ev[0]));
+    INF_HIP(hipEventCreate(&ev[1]));
+  }
+  INF_HIP(hipEventRecord(ev[0], s));
+  launch();
+  INF_LAUNCHED();
+  INF_HIP(hipEventRecord(ev[1], s));
+  INF_HIP(hipEventSynchronize(ev[1]));
+  float ms = 0.f;
+  INF_HIP(hipEventElapsedTime(&ms, ev[0], ev[1]));
+  std::lock_guard<std::mutex> lock(tm.mu);
+  tm.ms[which] += ms;
+  tm.n[which] += 1;
+  return INFERNO_OK;
+}
+
 }  // namespace
 
-bool decode_supported(size_t T, size_t k, size_t E, int quant, int down_quant) {
-  return T >= 1 && T <= size_t(kMaxDecodeTokens) && T * k <= size_t(kMaxDecodeTokens * kMaxTopK) &&
-         E <= size_t(kMaxExperts) && quant == down_quant &&
-         (quant == INFERNO_Q2_K || quant == INFERNO_Q3_K || quant == INFERNO_Q4_K);
+void kernel_timing_enable(bool on) {
+  std::lock_guard<std::mutex> lock(timers().mu);
+  timers().on = on;
+}
+
+bool kernel_timing_read(int which, double* ms, uint64_t* n) {
+  if (which < 0 || which > 1) return false;
+  std::lock_guard<std::mutex> lock(timers().mu);
+  *ms = timers().ms[which];
+  *n = timers().n[which];
+  timers().ms[which] = 0;
+  timers().n[which] = 0;
+  return true;
+}
+
+bool decode_supported(size_t T, size_t k, size_t E, size_t H, size_t I, size_t Is, int x_dtype,
+                      int quant, int down_quant) {
+  if (!(T >= 1 && T <= size_t(kMaxDecodeTokens) && E <= size_t(kMaxExperts) && k <= size_t(kMaxTopK) &&
+        quant == down_quant &&
+        (quant == INFERNO_Q2_K || quant == INFERNO_Q3_K || quant == INFERNO_Q4_K)))
+    return false;
+  const size_t kLds = 160 * 1024;
+  const size_t tile_extra = size_t(tile_part_floats(1) + 2 * kRows) * 4;
+  const size_t gate_up = size_t(staged_stride(int(H), x_dtype == INFERNO_F32)) * 4 + tile_extra;
+  const size_t shared_down = Is ? size_t(staged_stride(int(Is), true)) * 4 + tile_extra : 0;
+  return gate_up <= kLds && shared_down <= kLds && down_sum_lds(int(k), int(I)) + 64 <= kLds;
 }
 
 int decode_chunk(size_t H) {
@@ -331,10 +464,8 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   a.n_chunks = a.H / a.chunk;
   a.max_slots = std::min(a.E, a.T * a.k);
   const bool xsplit = a.x_dtype == INFERNO_F32;
-  if ((size_t(std::max({staged_stride(a.H, xsplit), staged_stride(a.I, true),
-                        a.Is ? staged_stride(a.Is, true) : 0})) +
-       tile_part_floats(1) + 2 * kRows) * 4 > 160 * 1024) {
-    set_error("fused decode: activation rows too long for LDS");
+  if (!decode_supported(a.T, a.k, a.E, a.H, a.I, a.Is, a.x_dtype, quant, quant)) {
+    set_error("fused decode path does not cover this layer shape");
     return INFERNO_ERR_INVALID;
   }
   // route: grid covers E/4 x chunks workgroups (and enough threads to stage x)
@@ -362,23 +493,29 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
     INF_HIP(hipEventRecord(side->join, side->stream));
   }
   if (a.T == 1)
-    select1_kernel<<<1, 64, 0, s>>>(a);
+    select1_kernel<<<1, 256, 0, s>>>(a);
   else
     select_kernel<<<1, 1024, 0, s>>>(a);
   INF_LAUNCHED();
-  switch (quant) {
-    case INFERNO_Q2_K: st = xsplit ? launch_routed<INFERNO_Q2_K, true>(s, a) : launch_routed<INFERNO_Q2_K, false>(s, a); break;
-    case INFERNO_Q3_K: st = xsplit ? launch_routed<INFERNO_Q3_K, true>(s, a) : launch_routed<INFERNO_Q3_K, false>(s, a); break;
-    case INFERNO_Q4_K: st = xsplit ? launch_routed<INFERNO_Q4_K, true>(s, a) : launch_routed<INFERNO_Q4_K, false>(s, a); break;
-    default:
-      set_error("fused decode path needs Q2_K, Q3_K or Q4_K routed experts");
-      return INFERNO_ERR_INVALID;
-  }
+  st = timed(s, 0, [&] {
+    switch (quant) {
+      case INFERNO_Q2_K: xsplit ? launch_gate_up<INFERNO_Q2_K, true>(s, a) : launch_gate_up<INFERNO_Q2_K, false>(s, a); break;
+      case INFERNO_Q3_K: xsplit ? launch_gate_up<INFERNO_Q3_K, true>(s, a) : launch_gate_up<INFERNO_Q3_K, false>(s, a); break;
+      default: xsplit ? launch_gate_up<INFERNO_Q4_K, true>(s, a) : launch_gate_up<INFERNO_Q4_K, false>(s, a); break;
+    }
+  });
   if (st) return st;
+  // the combined down pass adds the shared expert's rows
   if (a.Is) INF_HIP(hipStreamWaitEvent(s, side->join, 0));
-  combine_kernel<<<unsigned((size_t(a.T) * a.H + 255) / 256), 256, 0, s>>>(a);
-  INF_LAUNCHED();
-  return INFERNO_OK;
+  const unsigned grid = unsigned(size_t(a.T) * (a.H / kRows));
+  const size_t lds = down_sum_lds(a.k, a.I);
+  return timed(s, 1, [&] {
+    switch (quant) {
+      case INFERNO_Q2_K: down_sum_kernel<INFERNO_Q2_K><<<grid, 256, lds, s>>>(a); break;
+      case INFERNO_Q3_K: down_sum_kernel<INFERNO_Q3_K><<<grid, 256, lds, s>>>(a); break;
+      default: down_sum_kernel<INFERNO_Q4_K><<<grid, 256, lds, s>>>(a); break;
+    }
+  });
 }
 
 }  // namespace inferno

@@ -32,16 +32,21 @@ struct DecodeArgs {
   uint32_t* offsets;      // [E+1]
   uint32_t* sorted;       // [T*k]
   uint32_t* active;       // [E+1]
+  uint4* slots;           // [E] per active slot: expert, lo, hi, first assignment
   uint32_t* stage_h;      // [T*k, staged_stride(I, true)]
   uint32_t* stage_hs;     // [T, staged_stride(Is, true)]
-  float* y;               // [T*k, H]
   float* ys;              // [T, H]
   // filled by launch_decode_layer
   int chunk, n_chunks, max_slots;
 };
 
-bool decode_supported(size_t T, size_t k, size_t E, int quant, int down_quant);
+// True when the fused path covers the layer (token count, format and LDS fit).
+bool decode_supported(size_t T, size_t k, size_t E, size_t H, size_t I, size_t Is, int x_dtype,
+                      int quant, int down_quant);
 int decode_chunk(size_t H);
 int launch_decode_layer(hipStream_t s, const DecodeArgs& a, int quant);
+// Event timing of the routed gate/up (0) and down (1) kernels.
+void kernel_timing_enable(bool on);
+bool kernel_timing_read(int which, double* ms, uint64_t* n);
 
 }  // namespace inferno

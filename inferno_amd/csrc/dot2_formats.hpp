@@ -319,10 +319,11 @@ struct Fmt<INFERNO_Q8_0> {
 
 
 // Waves per SIMD the single-activation kernels are compiled for: four (128
-// VGPRs) where the format fits without spilling, three otherwise.
+// VGPRs) where the format fits without spilling in the streaming loop,
+// three (168 VGPRs) for Q3_K and for split (fp32) activations.
 template <int Q, bool SPLIT>
 struct Occupancy {
-  static constexpr int value = (Q == INFERNO_Q3_K) ? 3 : 4;
+  static constexpr int value = (Q == INFERNO_Q3_K || SPLIT) ? 3 : 4;
 };
 
 // ------------------------------------------------------------ tile compute
@@ -332,27 +333,28 @@ __host__ __device__ constexpr int tile_part_floats(int nt) { return 4 * kRows * 
 
 // One 16-row tile of one (or two: gate and up) expert matrices against NT
 // staged activation rows held in LDS (`xs`, row stride S words). Lane =
-// row slot * 4 + sub; the four wavefronts split the super-block columns and
-// meet in LDS. `row0`/`row1` point at this lane's row of each matrix. On
-// return (after a barrier) res[(m * kRows + slot) * NT + t] holds the dot
-// product of matrix m, row slot, activation t, in unscaled units.
+// row slot * 4 + sub; the four wavefronts split the super-block columns
+// and meet in LDS. `row0`/`row1` point at this lane's row of each matrix.
+// The first batch of quant loads can be issued (prefetch) before the
+// activations are in LDS, so the two memory latencies overlap.
 template <int Q, int NMAT, int NT, bool SPLIT>
-__device__ __forceinline__ void tile_dot(const uint8_t* row0, const uint8_t* row1, int K,
-                                         const uint32_t* xs, int S, int nt, float* part,
-                                         float* res) {
+struct TileDot {
   using F = Fmt<Q>;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int slot = lane >> 2, sub = lane & 3;
-  const int bpr = K / kKBlock;
-  float acc[NMAT][NT];
-#pragma unroll
-  for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[m][t] = 0.f;
   // split activations double the LDS reads per field: keep one super-block in flight
-  constexpr int kU = SPLIT ? 1 : F::kU;
-  for (int cb = wave; cb < bpr; cb += 4 * kU) {
-    uint32_t raw[NMAT][kU][F::kDw];
+  static constexpr int kU = SPLIT ? 1 : F::kU;
+  const uint8_t* row0;
+  const uint8_t* row1;
+  int K, bpr, wave, sub;
+  uint32_t raw[NMAT][kU][F::kDw];
+  float acc[NMAT][NT];
+
+  __device__ __forceinline__ TileDot(const uint8_t* r0, const uint8_t* r1, int K_)
+      : row0(r0), row1(r1), K(K_), bpr(K_ / kKBlock) {
+    const int tid = threadIdx.x;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    sub = tid & 3;
+  }
+  __device__ __forceinline__ void load(int cb) {
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int col = cb + 4 * u;
@@ -361,49 +363,78 @@ __device__ __forceinline__ void tile_dot(const uint8_t* row0, const uint8_t* row
         if constexpr (NMAT == 2) F::load(row1 + size_t(col) * F::kBytes, sub, raw[1][u]);
       }
     }
+  }
+  // Issues the first batch of this wavefront's quant loads.
+  __device__ __forceinline__ void prefetch() { load(wave); }
+  // Dot products against the NT (nt live) staged rows; prefetch() must have
+  // been called since the last run(). Ends with a barrier; afterwards
+  // res[(m * kRows + slot) * NT + t] holds matrix m, row slot, activation t.
+  __device__ __forceinline__ void run(const uint32_t* xs, int S, int nt, float* part, float* res) {
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int col = cb + 4 * u;
-      if (col < bpr) {
+    for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          if (t < nt) {
-            const XRow<SPLIT> xv = xrow_at<SPLIT>(xs + t * S, K, col);
+      for (int t = 0; t < NT; ++t) acc[m][t] = 0.f;
+    for (int cb = wave; cb < bpr; cb += 4 * kU) {
+      if (cb != wave) load(cb);
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m) acc[m][t] += F::dot(raw[m][u], sub, xv);
+      for (int u = 0; u < kU; ++u) {
+        const int col = cb + 4 * u;
+        if (col < bpr) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            if (t < nt) {
+              const XRow<SPLIT> xv = xrow_at<SPLIT>(xs + t * S, K, col);
+#pragma unroll
+              for (int m = 0; m < NMAT; ++m) acc[m][t] += F::dot(raw[m][u], sub, xv);
+            }
           }
         }
       }
     }
-  }
+    const int tid = threadIdx.x, slot = (tid & 63) >> 2;
 #pragma unroll
-  for (int m = 0; m < NMAT; ++m)
+    for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      float v = acc[m][t];
-      v += __shfl_xor(v, 1, kWave);
-      v += __shfl_xor(v, 2, kWave);
-      if (sub == 0) part[((m * 4 + wave) * kRows + slot) * NT + t] = v;
+      for (int t = 0; t < NT; ++t) {
+        float v = acc[m][t];
+        v += __shfl_xor(v, 1, kWave);
+        v += __shfl_xor(v, 2, kWave);
+        if (sub == 0) part[((m * 4 + wave) * kRows + slot) * NT + t] = v;
+      }
+    __syncthreads();
+    if (tid < NMAT * kRows * NT) {
+      const int m = tid / (kRows * NT), rest = tid % (kRows * NT);
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) v += part[(m * 4 + w) * kRows * NT + rest];
+      res[tid] = v;
     }
-  __syncthreads();
-  if (tid < NMAT * kRows * NT) {
-    const int m = tid / (kRows * NT), rest = tid % (kRows * NT);
-    float v = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) v += part[(m * 4 + w) * kRows * NT + rest];
-    res[tid] = v;
+    __syncthreads();
   }
-  __syncthreads();
+};
+
+// Copies n 16-byte words from global memory into LDS with every thread of
+// the 256-thread workgroup, DEPTH loads in flight per thread (loads clamped
+// to the last word, stores guarded, so the batch stays in registers).
+template <int DEPTH = 4>
+__device__ __forceinline__ void copy_to_lds(uint4* to, const uint4* from, int n) {
+  const int tid = threadIdx.x;
+  for (int base = 0; base < n; base += 256 * DEPTH) {
+    uint4 v[DEPTH];
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j) v[j] = from[min(base + j * 256 + tid, n - 1)];
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j)
+      if (base + j * 256 + tid < n) to[base + j * 256 + tid] = v[j];
+  }
 }
 
-// Copies `nt` staged rows (S words each) into LDS; src(t) gives the row pointer.
+// Copies `nt` staged rows (S words each, S a multiple of 4) into LDS; src(t)
+// gives the row pointer.
 template <typename SrcFn>
 __device__ __forceinline__ void copy_rows_to_lds(uint32_t* xs, int S, int nt, SrcFn src) {
-  for (int t = 0; t < nt; ++t) {
-    const uint4* from = reinterpret_cast<const uint4*>(src(t));
-    uint4* to = reinterpret_cast<uint4*>(xs + t * S);
-    for (int i = threadIdx.x; i < S / 4; i += 256) to[i] = from[i];
-  }
+  for (int t = 0; t < nt; ++t)
+    copy_to_lds(reinterpret_cast<uint4*>(xs + t * S), reinterpret_cast<const uint4*>(src(t)), S / 4);
 }
 
 // Stages one 16-value run held one value per lane by lanes 0..15 of a

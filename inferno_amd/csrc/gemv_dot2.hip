@@ -59,8 +59,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& p, const uint32_t* __r
   const uint8_t* base1 =
       kGateUp ? p.w1 + size_t(e) * p.expert_stride + size_t(rowc) * row_bytes : nullptr;
 
+  TileDot<Q, kMats, NT, SPLIT> td(base0, base1, K);
   for (uint32_t c0 = lo; c0 < hi; c0 += NT) {
     const int nt = int(min(uint32_t(NT), hi - c0));
+    td.prefetch();
     copy_rows_to_lds(xs, S, nt, [&](int t) {
       uint32_t src = c0 + uint32_t(t);
       if constexpr (MODE == kGateUpRouted) src = p.sorted[src] / uint32_t(p.k);
@@ -68,7 +70,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& p, const uint32_t* __r
       return staged + size_t(src) * S;
     });
     __syncthreads();
-    tile_dot<Q, kMats, NT, SPLIT>(base0, base1, K, xs, S, nt, part, res);
+    td.run(xs, S, nt, part, res);
     if constexpr (kGateUp) {
       // wave t (< nt) writes activation t's 16 outputs and staged run
       const int t = tid >> 6;

@@ -19,25 +19,30 @@ __device__ __forceinline__ uint32_t total_order_key(float f) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    uint64_t o = __shfl_xor(v, m, kWave);
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
   return v;
 }
 
-// Exact top-k of one token's logits by one wavefront (lane holds experts
-// lane, lane+64, lane+128, lane+192). `row` may live in global memory or LDS.
-// Lane 0 stores the results; every lane also gets the selected ids in rank
-// order in `sel_id` (wave-uniform).
+// Wavefront max of a u32 with DPP row moves and four readlanes; every lane
+// of the wavefront must be active. Returns the (uniform) maximum.
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0xB1, 0xF, 0xF, false)));   // quad [1,0,3,2]
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x4E, 0xF, 0xF, false)));   // quad [2,3,0,1]
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x141, 0xF, 0xF, false)));  // half mirror
+  v = max(v, uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x140, 0xF, 0xF, false)));  // row mirror
+  const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+  return max(max(a, b), max(c, d));
+}
+
+// Exact top-k of one token's logits by one full wavefront (lane holds
+// experts lane, lane+64, lane+128, lane+192). `row` may live in global
+// memory or LDS. Each round takes the largest (selection key, lowest id):
+// a wavefront max of the f32 total-order key, then among the lanes holding
+// that key a max of ~id. Lane 0 stores the results; every lane also gets
+// the selected ids in rank order in `sel_id` (wave-uniform).
 __device__ __forceinline__ void topk_row_wave(const float* row, const float* __restrict__ bias,
                                               int E, int k, int score_fn, int norm, float scale,
                                               int t, uint32_t* __restrict__ ids,
@@ -47,10 +52,11 @@ __device__ __forceinline__ void topk_row_wave(const float* row, const float* __r
   constexpr int PER = kMaxExperts / kWave;  // 4 candidates per lane
   const int lane = threadIdx.x & 63;
   float lg[PER], score[PER];
-  uint64_t key[PER];
+  uint32_t key[PER];
+  bool live[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    int e = lane + j * kWave;
+    const int e = lane + j * kWave;
     lg[j] = e < E ? row[e] : -INFINITY;
   }
   float lmax = 0.f, denom_all = 0.f;
@@ -62,7 +68,7 @@ __device__ __forceinline__ void topk_row_wave(const float* row, const float* __r
   }
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    int e = lane + j * kWave;
+    const int e = lane + j * kWave;
     float s, sel;
     if (score_fn == INFERNO_SCORE_SIGMOID) {
       s = 1.0f / (1.0f + expf(-lg[j]));
@@ -72,9 +78,9 @@ __device__ __forceinline__ void topk_row_wave(const float* row, const float* __r
       sel = lg[j];
     }
     score[j] = s;
-    float corrected = sel + ((bias != nullptr && e < E) ? bias[e] : 0.0f);
-    key[j] = e < E ? ((uint64_t(total_order_key(corrected)) << 32) | uint64_t(0xffffffffu - uint32_t(e)))
-                   : 0ull;
+    const float corrected = sel + ((bias != nullptr && e < E) ? bias[e] : 0.0f);
+    key[j] = total_order_key(corrected);
+    live[j] = e < E;
   }
   if (score_fn == INFERNO_SCORE_SOFTMAX && !norm) {
     float part = 0.f;
@@ -84,25 +90,39 @@ __device__ __forceinline__ void topk_row_wave(const float* row, const float* __r
   }
   float sel_score[kMaxTopK];
 #pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r) sel_id[r] = 0xffffffffu;
+  for (int r = 0; r < kMaxTopK; ++r) {
+    sel_id[r] = 0xffffffffu;
+    sel_score[r] = 0.f;
+  }
 #pragma unroll
   for (int r = 0; r < kMaxTopK; ++r) {
     if (r < k) {
-      uint64_t best = key[0];
+      // this lane's best live candidate: highest key, lowest id (j ascending = id ascending)
+      uint32_t bk = 0, bj = 0;
+      bool any = false;
 #pragma unroll
-      for (int j = 1; j < PER; ++j) best = key[j] > best ? key[j] : best;
-      best = wave_max_u64(best);
-      uint32_t id = 0xffffffffu - uint32_t(best & 0xffffffffu);
-      int owner = int(id & 63u), slot = int(id >> 6);
-      float s = 0.f;
+      for (int j = 0; j < PER; ++j) {
+        if (live[j] && (!any || key[j] > bk)) {
+          bk = key[j];
+          bj = uint32_t(j);
+          any = true;
+        }
+      }
+      const uint32_t mk = wave_umax(any ? bk : 0u);
+      const uint32_t my_id = uint32_t(lane) + bj * kWave;
+      const uint32_t inv = wave_umax((any && bk == mk) ? ~my_id : 0u);
+      const uint32_t id = ~inv;
+      const int owner = int(id & 63u), slot = int(id >> 6);
+      float mine = score[0];
 #pragma unroll
-      for (int j = 0; j < PER; ++j)
-        if (j == slot) s = score[j];
-      s = __shfl(s, owner, kWave);
+      for (int j = 1; j < PER; ++j)
+        if (j == slot) mine = score[j];
+      const float s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                    __builtin_bit_cast(int, mine), owner));
       if (lane == owner) {
 #pragma unroll
         for (int j = 0; j < PER; ++j)
-          if (j == slot) key[j] = 0ull;
+          if (j == slot) live[j] = false;
       }
       sel_score[r] = s;
       sel_id[r] = id;
@@ -123,7 +143,7 @@ __device__ __forceinline__ void topk_row_wave(const float* row, const float* __r
       if (r < k) {
         float wv = sel_score[r];
         if (divide) wv /= sum;
-        size_t a = size_t(t) * k + r;
+        const size_t a = size_t(t) * k + r;
         ids[a] = sel_id[r];
         weights[a] = wv * scale;
         if (token_idx) token_idx[a] = uint32_t(t);

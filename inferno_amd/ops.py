@@ -170,6 +170,22 @@ def rms_norm(x, w, eps):
     return out
 
 
+TIMER_GATE_UP, TIMER_DOWN = 0, 1
+
+
+def kernel_timing(enable):
+    """Turns the event timing of the fused decode path's routed gate/up and
+    down kernels on or off (measurement only: it waits on every launch)."""
+    check(lib().inferno_kernel_timing_enable(1 if enable else 0))
+
+
+def kernel_timing_read(which):
+    """(total ms, launches) accumulated by one timer since the last read."""
+    ms, n = C.c_double(0.0), C.c_uint64(0)
+    check(lib().inferno_kernel_timing_read(which, C.byref(ms), C.byref(n)))
+    return ms.value, n.value
+
+
 def synth_normal(seed, stddev, n, dtype=torch.float32, device="cuda"):
     out = torch.empty(n, dtype=dtype, device=device)
     check(lib().inferno_synth_normal(_s(), seed, float(stddev), n, _DT[dtype], _p(out)))
