@@ -30,6 +30,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+QUANT_NAMES = {8: "Q8_0", 10: "Q2_K", 11: "Q3_K", 12: "Q4_K", 14: "Q6_K"}
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -44,7 +45,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="c2")
     ap.add_argument("--tokens", type=int, default=0, help="T (default: the config's first)")
-    ap.add_argument("--layers", type=int, default=8, help="resident layer copies")
+    ap.add_argument("--layers", type=int, default=0,
+                    help="resident layer copies (default 8 for decode, 2 for prefill)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -68,17 +70,25 @@ def main():
     dev = torch.device("cuda:0")
     cfg = cf.CONFIGS[args.config]
     T = args.tokens or cfg.tokens[0]
-    L = max(1, args.layers)
+    L = args.layers or (8 if T <= 64 else 2)
     H, E, I, k = cfg.hidden, cfg.experts, cfg.intermediate, cfg.top_k
 
+    prefill = T > 64
     t0 = time.time()
     layers = []
     for l in range(L):
         c = cf.Config(**{**cfg.__dict__, "index": cfg.index + 100 * l}) if l else cfg
         layers.append(cf.build_layer(c, 0, dev, max_tokens=T))
         log(f"[bench] built layer {l + 1}/{L} ({time.time() - t0:.1f}s)")
-    n_inputs = 64
+    n_inputs = 4 if prefill else 64
     xs = [cf.make_input(cfg, T, variant=v, device=dev) for v in range(n_inputs)]
+    if cfg.zipf:
+        # correction bias fitted so that the top-k load of the first input
+        # follows Zipf(s); written in place (the layer holds its pointer)
+        for lt in layers:
+            logits = ops.router_logits(xs[0], lt.router)
+            lt.bias.copy_(torch.from_numpy(cf.zipf_bias(cfg, logits.cpu().numpy())).to(dev))
+        log(f"[bench] Zipf({cfg.zipf}) bias fitted ({time.time() - t0:.1f}s)")
     residual = torch.randn(T, H, device=dev)
     out = torch.empty(T, H, device=dev)
     ids_buf = [torch.empty(T * k, dtype=torch.int32, device=dev) for _ in range(L)]
@@ -101,47 +111,73 @@ def main():
     ms_per_step = 1e3 * elapsed / args.steps
     tokens_per_s = T * args.steps / elapsed
 
-    # ---- dominant kernel: routed gate/up of the fused decode path ---------
+    # ---- dominant kernel: the routed gate/up launch -------------------------
     # Same layer steps again with the event hook on: the C library brackets
-    # the routed gate/up kernel (and the routed down kernel) with HIP events
-    # on the layer's stream. Algorithmic bytes per launch = quantised gate+up
-    # bytes of the step's unique selected experts.
+    # the routed gate/up launch (and the routed down launch) with HIP events
+    # on the layer's stream. Decode: algorithmic bytes per launch = quantised
+    # gate+up bytes of the step's unique selected experts. Prefill: flops per
+    # launch = 2 * (2 * H * I) * assignments.
     q = cfg.quants[0]
     bb = ops.block_bytes(q)
     gu_bytes_per_expert = 2 * I * (H // 256) * bb
     dn_bytes_per_expert = H * (I // 256) * bb
-    reps = max(args.steps, 64)
+    reps = max(args.steps, 64) if not prefill else max(args.steps, 10)
     ops.kernel_timing(True)
     try:
         ops.kernel_timing_read(ops.TIMER_GATE_UP)
         ops.kernel_timing_read(ops.TIMER_DOWN)
         uniq = 0
+        loads = []
         for i in range(reps):
             step(i)
             l = i % L
             uniq += int(torch.unique(ids_buf[l]).numel())
+            if prefill and i < L:
+                loads.append(torch.bincount(ids_buf[l].long(), minlength=E).cpu())
         torch.cuda.synchronize()
         gu_ms, gu_n = ops.kernel_timing_read(ops.TIMER_GATE_UP)
         dn_ms, dn_n = ops.kernel_timing_read(ops.TIMER_DOWN)
     finally:
         ops.kernel_timing(False)
     if gu_n != reps or dn_n != reps:
-        raise RuntimeError(f"kernel timers saw {gu_n}/{dn_n} launches for {reps} layer steps "
-                           "(the fused decode path did not run)")
+        raise RuntimeError(f"kernel timers saw {gu_n}/{dn_n} launches for {reps} layer steps")
     uniq_layer = uniq / reps
     gu_us = 1e3 * gu_ms / gu_n
     dn_us = 1e3 * dn_ms / dn_n
-    gu_bytes = gu_bytes_per_expert * uniq_layer
-    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
-    dn_gbs = dn_bytes_per_expert * uniq_layer / (dn_us * 1e-6) / 1e9
-
-    # whole-layer bytes: routed experts of the step's unique experts, plus the
-    # shared expert (Q8_0), the fp32 router and the token's activations
+    layer_us = ms_per_step * 1e3
     layer_routed_bytes = (gu_bytes_per_expert + dn_bytes_per_expert) * uniq_layer
     shared_bytes = 3 * cfg.shared_intermediate * (H // 32) * 34 if cfg.shared_intermediate else 0
     router_bytes = E * H * 4
-    layer_us = ms_per_step * 1e3
-    traffic = read_traffic(ROOT / "profiles" / "gate_up_q2k_c2_decode_traffic.txt")
+    extra = {}
+    if not prefill:
+        gu_bytes = gu_bytes_per_expert * uniq_layer
+        gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
+        dn_gbs = dn_bytes_per_expert * uniq_layer / (dn_us * 1e-6) / 1e9
+        traffic = read_traffic(ROOT / "profiles" / "gate_up_q2k_c2_decode_traffic.txt")
+        roofline = {"bound": "hbm", "kernel": "gate_up_kernel<Q2_K, bf16, routed> (decode.hip)",
+                    "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                    "launch_us": round(gu_us, 3), "bytes_per_launch": int(gu_bytes)}
+        extra["down_kernel"] = {"kernel": "down_sum_kernel (decode.hip)",
+                                "launch_us": round(dn_us, 3), "GBps": round(dn_gbs, 1)}
+    else:
+        A = T * k
+        gu_flops = 4.0 * H * I * A
+        gu_tfs = gu_flops / (gu_us * 1e-6) / 1e12
+        dn_tfs = 2.0 * H * I * A / (dn_us * 1e-6) / 1e12
+        roofline = {"bound": "mfma", "kernel": "routed gate/up launch (prefill)",
+                    "achieved": round(gu_tfs, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(gu_tfs / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "traffic": None, "launch_us": round(gu_us, 3),
+                    "flops_per_launch": gu_flops,
+                    "routed_bytes_per_launch": int(gu_bytes_per_expert * uniq_layer)}
+        extra["down_launch"] = {"launch_us": round(dn_us, 3), "TFLOPs": round(dn_tfs, 2)}
+        extra["layer_mfma_frac"] = round(6.0 * H * I * A / (layer_us * 1e-6) / 1e12
+                                         / MFMA_BF16_PEAK_TFLOPS, 4)
+        load = torch.stack(loads).float().mean(0)
+        extra["expert_load"] = {"active": int((load > 0).sum()), "hottest_share":
+                                round(float(load.max() / A), 4),
+                                "empty": int((load == 0).sum())}
 
     # ---- CPU baseline: oracle on the host cores -------------------------
     cpu = None
@@ -162,7 +198,7 @@ def main():
         "dtype": "f16-dot2/f32-acc",
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantised on device)",
         "config": {"workload": cfg.name, "tokens": T, "hidden": H, "experts": E,
-                   "intermediate": I, "top_k": k, "quant": "Q2_K" if q == 10 else str(q),
+                   "intermediate": I, "top_k": k, "quant": QUANT_NAMES.get(q, str(q)),
                    "shared_intermediate": cfg.shared_intermediate, "layers_resident": L},
         "us_per_token": round(layer_us / T, 3),
         "layer_routed_bytes": int(layer_routed_bytes),
@@ -170,12 +206,8 @@ def main():
         "layer_total_bytes": int(layer_routed_bytes + shared_bytes + router_bytes),
         "layer_total_GBps": round((layer_routed_bytes + shared_bytes + router_bytes)
                                   / (layer_us * 1e-6) / 1e9, 1),
-        "roofline": {"bound": "hbm", "kernel": "gate_up_kernel<Q2_K, bf16, routed> (decode.hip)",
-                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "launch_us": round(gu_us, 3), "bytes_per_launch": int(gu_bytes)},
-        "down_kernel": {"kernel": "down_sum_kernel<Q2_K> (decode.hip)", "launch_us": round(dn_us, 3),
-                        "GBps": round(dn_gbs, 1)},
+        "roofline": roofline,
+        **extra,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
@@ -207,9 +239,10 @@ def read_traffic(path):
 
 
 def cpu_baseline(cfg, layers, xs, residual, T, seconds):
-    """Times the C++ oracle on a bounded sample of decode tokens (one layer
-    each, cycling layers). Only the oracle calls are timed; copying the
-    selected experts' bytes to the host is not."""
+    """Times the C++ oracle on a bounded sample of the workload's tokens:
+    decode one token per layer call, prefill chunks of 4 consecutive tokens
+    of the batch, cycling layers. Only the oracle calls are timed; copying
+    the selected experts' bytes to the host is not."""
     import numpy as np
     import torch
 
@@ -223,10 +256,12 @@ def cpu_baseline(cfg, layers, xs, residual, T, seconds):
     cores = max(1, min(cores, 16))
     orc.THREADS = cores
     k, E = cfg.top_k, cfg.experts
+    chunk = 1 if T <= 64 else 4
     busy, n = 0.0, 0
     while busy < seconds and n < 2048:
         lt = layers[n % len(layers)]
-        x = xs[n % len(xs)][:1].float().cpu().numpy()
+        j = (n * chunk) % T
+        x = xs[n % len(xs)][j:j + chunk].float().cpu().numpy()
         router = lt.router.cpu().numpy()
         bias = None if lt.bias is None else lt.bias.cpu().numpy()
         t0 = time.perf_counter()
@@ -241,7 +276,7 @@ def cpu_baseline(cfg, layers, xs, residual, T, seconds):
         remap = {int(e): i for i, e in enumerate(experts)}
         ids_c = np.array([remap[int(e)] for e in ids], np.uint32)
         shared = [s.cpu().numpy() for s in lt.shared] if lt.shared else None
-        res = residual[:1].cpu().numpy()
+        res = residual[j:j + chunk].cpu().numpy()
         t0 = time.perf_counter()
         routed = orc.moe_routed(lt.quant, lt.quant, g, u, d, x, ids_c, w, len(experts), k,
                                 cfg.intermediate)
@@ -249,9 +284,12 @@ def cpu_baseline(cfg, layers, xs, residual, T, seconds):
             orc.shared_q8_0(*shared, x, cfg.shared_intermediate, routed=routed, residual=res)
         busy += time.perf_counter() - t0
         n += 1
-    return {"value": round(n / busy, 4), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"{n} decode tokens (T=1 layer forwards incl. router, routed experts and "
-                      f"shared expert) in {busy:.1f}s of oracle time"}
+    what = "decode tokens (T=1 layer forwards" if chunk == 1 else \
+        f"prefill tokens (layer forwards over chunks of {chunk} tokens"
+    return {"value": round(n * chunk / busy, 4), "unit": "tokens/s", "cores": cores,
+            "kind": "port",
+            "sample": f"{n * chunk} {what} incl. router, routed experts and shared expert) "
+                      f"in {busy:.1f}s of oracle time"}
 
 
 if __name__ == "__main__":

@@ -247,9 +247,10 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* layer, cons
 /* ------------------------------------------------------- kernel timing */
 
 /* Measurement hook with no counterpart in the reference (benchmarks only).
- * While enabled, inferno_moe_layer_forward's fused decode path brackets its
- * routed gate/up kernel and its routed down kernel with HIP events on the
- * layer's stream, waits for the second event and adds the elapsed time to a
+ * While enabled, the routed gate/up launch and the routed down launch of
+ * inferno_moe_layer_forward / inferno_gguf_moe (fused decode kernels or the
+ * stage path) are bracketed with HIP events on the caller's stream; the
+ * library waits for the second event and adds the elapsed time to a
  * process-wide accumulator. The wait serialises the host with the layer:
  * leave timing off outside measurement. */
 enum { INFERNO_TIMER_GATE_UP = 0, INFERNO_TIMER_DOWN = 1 };

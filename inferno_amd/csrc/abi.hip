@@ -7,6 +7,8 @@
 #include <vector>
 
 #include "decode.hpp"
+#include "prefill.hpp"
+#include "timing.hpp"
 #include "gemv_common.hpp"
 #include "quantize.hpp"
 
@@ -59,8 +61,9 @@ struct MoeScratch {
   uint32_t* active;
   float* h;
   float* y;
-  uint32_t* stage_x;  // staged activations of x (sized for fp32 input)
+  uint32_t* stage_x;  // staged activations of x (sized for fp32 input); f16 x on the MFMA path
   uint32_t* stage_h;  // staged activations of h
+  uint32_t* plan;     // MFMA path: expert tile lists
 };
 
 // Staged activation rows, sized for the fp32 (split) layout, the larger one.
@@ -77,6 +80,7 @@ MoeScratch carve_moe(Carver& c, size_t T, size_t k, size_t E, size_t H, size_t I
   m.y = c.take<float>(T * k * H);
   m.stage_x = c.take<uint32_t>(stage_words(T, H));
   m.stage_h = c.take<uint32_t>(stage_words(T * k, I));
+  m.plan = c.take<uint32_t>(prefill_plan_words(T * k, E));
   return m;
 }
 
@@ -106,21 +110,42 @@ int validate_moe(int quant, int down_quant, size_t gate_bytes, size_t up_bytes,
 
 // Routed part shared by inferno_gguf_moe and the layer: dispatch, gate/up,
 // down. Leaves per-assignment down rows (already routing-weighted) in m.y.
+// Many assignments take the MFMA grouped GEMM; few take the packed-f16 GEMV.
+bool use_mfma(int quant, int down_quant, size_t T, size_t k, size_t E, size_t H, size_t I) {
+  return T * k >= kPrefillMinAssignments && prefill_routed_supported(quant, down_quant, H, I, E);
+}
+
+// `x16`: x already converted to f16 (MFMA path), or null.
 int run_routed(hipStream_t s, int quant, int down_quant, const void* gate, const void* up,
                const void* down, const void* x, int x_dtype, const uint32_t* ids,
                const float* w, size_t T, size_t k, size_t E, size_t H, size_t I,
-               const MoeScratch& m, bool x_staged) {
+               const MoeScratch& m, bool x_staged, const uint16_t* x16 = nullptr) {
   int st;
   if ((st = launch_dispatch(s, ids, T, k, E, m.offsets, m.sorted, m.active))) return st;
+  if (use_mfma(quant, down_quant, T, k, E, H, I)) {
+    if (!x16) {
+      uint16_t* conv = reinterpret_cast<uint16_t*>(m.stage_x);
+      if ((st = launch_to_f16(s, x, x_dtype, T, H, conv))) return st;
+      x16 = conv;
+    }
+    PrefillRouted p{quant, down_quant, gate, up, down, x16, m.offsets, m.sorted, m.active, w,
+                    T, k, E, H, I, reinterpret_cast<uint16_t*>(m.h), m.y, m.plan};
+    if ((st = timed(s, kTimerGateUp, [&] { return launch_prefill_gate_up(s, p); }))) return st;
+    return timed(s, kTimerDown, [&] { return launch_prefill_down(s, p); });
+  }
   // gate/up writes h already staged for the down pass (when the down kind has a
   // packed-f16 kernel; Q6_K reads the fp32 h)
   const bool h_staged = dot2_supported(down_quant);
-  if ((st = launch_gemv_gate_up_routed(s, quant, gate, up, x, x_dtype, m.stage_x, x_staged,
-                                       m.offsets, m.sorted, m.active, w, T, k, E, H, I, m.h,
-                                       h_staged ? m.stage_h : nullptr)))
+  if ((st = timed(s, kTimerGateUp, [&] {
+         return launch_gemv_gate_up_routed(s, quant, gate, up, x, x_dtype, m.stage_x, x_staged,
+                                           m.offsets, m.sorted, m.active, w, T, k, E, H, I, m.h,
+                                           h_staged ? m.stage_h : nullptr);
+       })))
     return st;
-  return launch_gemv_down_routed(s, down_quant, down, m.h, m.stage_h, h_staged, m.offsets,
-                                 m.sorted, m.active, T, k, E, H, I, m.y);
+  return timed(s, kTimerDown, [&] {
+    return launch_gemv_down_routed(s, down_quant, down, m.h, m.stage_h, h_staged, m.offsets,
+                                   m.sorted, m.active, T, k, E, H, I, m.y);
+  });
 }
 
 int need_ws(void* ws, size_t have, size_t need) {
@@ -456,6 +481,18 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
   if ((st = launch_router_topk(s, w.logits, L->router_bias, T, E, k, L->score_fn,
                                L->norm_topk_prob, L->routed_scaling_factor, ids, wts, nullptr)))
     return st;
+  if (use_mfma(L->quant, L->down_quant, T, k, E, H, I)) {
+    // x in f16 once for the routed and the shared expert GEMMs
+    uint16_t* x16 = reinterpret_cast<uint16_t*>(w.moe.stage_x);
+    if ((st = launch_to_f16(s, x, x_dtype, T, H, x16))) return st;
+    if ((st = run_routed(s, L->quant, L->down_quant, L->gate, L->up, L->down, x, x_dtype, ids,
+                         wts, T, k, E, H, I, w.moe, false, x16)))
+      return st;
+    if (Is && (st = launch_prefill_dense(s, L->shared_gate, L->shared_up, L->shared_down, x16, T,
+                                         H, Is, reinterpret_cast<uint16_t*>(w.hs), w.ys)))
+      return st;
+    return launch_prefill_combine(s, w.moe.y, Is ? w.ys : nullptr, residual, T, k, H, out);
+  }
   // x is staged once for the routed and the shared gate/up
   if ((st = launch_stage(s, x, x_dtype, T, H, w.moe.stage_x))) return st;
   if ((st = run_routed(s, L->quant, L->down_quant, L->gate, L->up, L->down, x, x_dtype, ids, wts,

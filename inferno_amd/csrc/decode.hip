@@ -19,6 +19,7 @@
 // (shared expert plus two residual adds), moe_kernels.metal:210-238 (rank
 // order combine).
 #include "decode.hpp"
+#include "timing.hpp"
 #include "dot2_formats.hpp"
 #include "routing_dev.hpp"
 
@@ -370,74 +371,7 @@ int side_stream(SideStream** out) {
   return INFERNO_OK;
 }
 
-// Measurement hook: events around the routed expert kernels (see the C ABI).
-struct KernelTimers {
-  std::mutex mu;
-  bool on = false;
-  double ms[2] = {0, 0};
-  uint64_t n[2] = {0, 0};
-  hipEvent_t ev[64][2] = {};
-};
-KernelTimers& timers() {
-  static KernelTimers t;
-  return t;
-}
-
-// Launches `launch` on s; when timing is on, brackets it with events and
-// accumulates its elapsed time under `which`.
-template <typename Fn>
-int timed(hipStream_t s, int which, Fn launch) {
-  KernelTimers& tm = timers();
-  bool on;
-  {
-    std::lock_guard<std::mutex> lock(tm.mu);
-    on = tm.on;
-  }
-  if (!on) {
-    launch();
-    INF_LAUNCHED();
-    return INFERNO_OK;
-  }
-  int dev = 0;
-  INF_HIP(hipGetDevice(&dev));
-  if (dev < 0 || dev >= 64) {
-    set_error("device index out of range");
-    return INFERNO_ERR_DEVICE;
-  }
-  hipEvent_t* ev = tm.ev[dev];
-  if (!ev[0]) {
-    INF_HIP(hipEventCreate(&ev[0]));
-    INF_HIP(hipEventCreate(&ev[1]));
-  }
-  INF_HIP(hipEventRecord(ev[0], s));
-  launch();
-  INF_LAUNCHED();
-  INF_HIP(hipEventRecord(ev[1], s));
-  INF_HIP(hipEventSynchronize(ev[1]));
-  float ms = 0.f;
-  INF_HIP(hipEventElapsedTime(&ms, ev[0], ev[1]));
-  std::lock_guard<std::mutex> lock(tm.mu);
-  tm.ms[which] += ms;
-  tm.n[which] += 1;
-  return INFERNO_OK;
-}
-
 }  // namespace
-
-void kernel_timing_enable(bool on) {
-  std::lock_guard<std::mutex> lock(timers().mu);
-  timers().on = on;
-}
-
-bool kernel_timing_read(int which, double* ms, uint64_t* n) {
-  if (which < 0 || which > 1) return false;
-  std::lock_guard<std::mutex> lock(timers().mu);
-  *ms = timers().ms[which];
-  *n = timers().n[which];
-  timers().ms[which] = 0;
-  timers().n[which] = 0;
-  return true;
-}
 
 bool decode_supported(size_t T, size_t k, size_t E, size_t H, size_t I, size_t Is, int x_dtype,
                       int quant, int down_quant) {
@@ -497,24 +431,28 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   else
     select_kernel<<<1, 1024, 0, s>>>(a);
   INF_LAUNCHED();
-  st = timed(s, 0, [&] {
+  st = timed(s, kTimerGateUp, [&] {
     switch (quant) {
       case INFERNO_Q2_K: xsplit ? launch_gate_up<INFERNO_Q2_K, true>(s, a) : launch_gate_up<INFERNO_Q2_K, false>(s, a); break;
       case INFERNO_Q3_K: xsplit ? launch_gate_up<INFERNO_Q3_K, true>(s, a) : launch_gate_up<INFERNO_Q3_K, false>(s, a); break;
       default: xsplit ? launch_gate_up<INFERNO_Q4_K, true>(s, a) : launch_gate_up<INFERNO_Q4_K, false>(s, a); break;
     }
+    INF_LAUNCHED();
+    return INFERNO_OK;
   });
   if (st) return st;
   // the combined down pass adds the shared expert's rows
   if (a.Is) INF_HIP(hipStreamWaitEvent(s, side->join, 0));
   const unsigned grid = unsigned(size_t(a.T) * (a.H / kRows));
   const size_t lds = down_sum_lds(a.k, a.I);
-  return timed(s, 1, [&] {
+  return timed(s, kTimerDown, [&] {
     switch (quant) {
       case INFERNO_Q2_K: down_sum_kernel<INFERNO_Q2_K><<<grid, 256, lds, s>>>(a); break;
       case INFERNO_Q3_K: down_sum_kernel<INFERNO_Q3_K><<<grid, 256, lds, s>>>(a); break;
       default: down_sum_kernel<INFERNO_Q4_K><<<grid, 256, lds, s>>>(a); break;
     }
+    INF_LAUNCHED();
+    return INFERNO_OK;
   });
 }
 

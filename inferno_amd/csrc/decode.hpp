@@ -45,8 +45,6 @@ bool decode_supported(size_t T, size_t k, size_t E, size_t H, size_t I, size_t I
                       int quant, int down_quant);
 int decode_chunk(size_t H);
 int launch_decode_layer(hipStream_t s, const DecodeArgs& a, int quant);
-// Event timing of the routed gate/up (0) and down (1) kernels.
-void kernel_timing_enable(bool on);
-bool kernel_timing_read(int which, double* ms, uint64_t* n);
+
 
 }  // namespace inferno

@@ -1,0 +1,632 @@
+// Prefill MoE experts as grouped dequant-GEMMs on the gfx950 matrix cores.
+//
+// For every active expert e with n_e assignments (dispatch groups), gate/up:
+//   h[a, :] = silu(x[t_a] G_e^T) * (x[t_a] U_e^T) * w_a      (f16 rows of h)
+// then down: y[a, :] = h[a, :] D_e^T (fp32 rows per assignment), summed over
+// ranks in rank order by the combine. Semantics follow the reference's
+// prefill kernels (crates/backend/src/metal/kernels/gguf_moe_prefill_kernels.metal:
+// 256-508 gate/up with the routing weight folded, :510-691 down, :693-714
+// combine), which also run the expert products on f16 operands with fp32
+// accumulation.
+//
+// Work item: 128 weight rows (gate and up rows together for the SwiGLU pass)
+// x TM dispatch rows (TM = 128, or 32 for an expert's small remainder). Each
+// wavefront owns 32 weight rows and all TM tokens, issuing
+// v_mfma_f32_32x32x16_f16 with the weights as the A operand and the tokens
+// as B. Every lane dequantises its own A fragments (8 values of one row per
+// 16-deep k step) straight from the GGUF bytes: a quant field masked in place
+// out of a 32-bit word, at bits p and 16 + p, is a pair of exact f16
+// subnormals q * 2^(p-24), and one v_fma_mix per value (f16 field, fp32
+// scale * 2^(24-p), fp32 offset) yields the value rounded once to f16. The
+// mask takes bytes 0 and 2 (then 1 and 3) of a word, so within every group of
+// eight k the operands run in the order 0 2 1 3 4 6 5 7; the f16 activations
+// (x16, h16) are stored in that same order, which leaves the sum unchanged.
+// The token tile (TM x 64 f16) is double buffered in LDS. Tiles come from a
+// per-expert list built on the device from the dispatch, so nothing waits on
+// the host.
+#include "prefill.hpp"
+
+#include <algorithm>
+#include <type_traits>
+
+#include "gemv_common.hpp"
+
+namespace inferno {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kUnit = 256;       // values per K unit (super-block / eight Q8_0 blocks)
+constexpr int kTileN = 128;      // weight rows per workgroup
+constexpr int kLdsPitch = 72;    // halfs per LDS token row (64 + 8 pad: conflict-free reads)
+
+__device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
+__device__ __forceinline__ uint32_t as_u32(half2v v) { return __builtin_bit_cast(uint32_t, v); }
+
+// v(f) = f * mult + off for both f16 subnormal fields of a masked word, in f16.
+__device__ __forceinline__ uint32_t fma_pair(uint32_t fields, float mult, float off) {
+  const half2v f = as_h2(fields);
+  const half2v r = {(_Float16)__builtin_fmaf((float)f[0], mult, off),
+                    (_Float16)__builtin_fmaf((float)f[1], mult, off)};
+  return as_u32(r);
+}
+
+// Eight values from bytes 0..7 of (w0, w1) with the field under `mask` (the
+// same mask in both 16-bit halves, at bit position p): value = field * mult +
+// off, mult already holding the 2^(24 - p). Output order 0 2 1 3 4 6 5 7.
+__device__ __forceinline__ half8 dequant8(uint32_t w0, uint32_t w1, uint32_t mask, float mult,
+                                          float off) {
+  const uint32_t a = fma_pair(w0 & mask, mult, off);
+  const uint32_t b = fma_pair((w0 >> 8) & mask, mult, off);
+  const uint32_t c = fma_pair(w1 & mask, mult, off);
+  const uint32_t d = fma_pair((w1 >> 8) & mask, mult, off);
+  return __builtin_bit_cast(half8, make_uint4(a, b, c, d));
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
+
+// ------------------------------------------------------------- A fragments
+// A lane (row i, k half kg) dequantises, for 64-value chunk QC of a K unit
+// and k step s = 0..3, the values 64 QC + 16 s + 8 kg .. +8 of its row.
+// load() fetches everything the four k steps of one chunk need; get()
+// returns the eight f16 values of step s (order 0 2 1 3 4 6 5 7).
+
+template <int Q>
+struct Frag;
+
+// Q2_K [scales 16 | qs 64 | d | dmin]: value j = 128 h + 32 p + l uses
+// q = (qs[32 h + l] >> 2 p) & 3 and scale byte 16-group j / 16
+// (crates/gguf/src/lib.rs:1226-1293).
+template <>
+struct Frag<INFERNO_Q2_K> {
+  static constexpr int kBytes = 84, kRaw = 6;
+  __device__ static void load(const uint8_t* b, int qc, int kg, uint32_t r[kRaw]) {
+    const int h = qc >> 1;
+    const uint2 a = ld_u2(b + 16 + 32 * h + 8 * kg);
+    const uint2 c = ld_u2(b + 32 + 32 * h + 8 * kg);
+    r[0] = a.x; r[1] = a.y; r[2] = c.x; r[3] = c.y;
+    r[4] = ld_u1(b + 4 * qc);  // scale bytes of groups 4 qc .. 4 qc + 3
+    r[5] = ld_u1(b + 80);      // d | dmin
+  }
+  template <int QC>
+  __device__ static half8 get(const uint32_t r[kRaw], int s) {
+    const int p = 2 * (QC & 1) + (s >> 1);
+    const uint32_t sc = byte_of(r[4], s);
+    const float d = f16_bits_to_f32_fast(uint16_t(r[5]));
+    const float dmin = f16_bits_to_f32_fast(uint16_t(r[5] >> 16));
+    const float mult = __builtin_amdgcn_ldexpf(d * float(sc & 15u), 24 - 2 * p);
+    return dequant8((s & 1) ? r[2] : r[0], (s & 1) ? r[3] : r[1], 0x00030003u << (2 * p), mult,
+                    -(dmin * float(sc >> 4)));
+  }
+};
+
+// Q3_K [hmask 32 | qs 64 | scales 12 | d]: value j = 128 n + 32 jj + l uses
+// q = (qs[32 n + l] >> 2 jj) & 3, high bit hmask[l] bit (4 n + jj), 6-bit
+// signed group scale; value = d (s6 - 32) (q + 4 hbit - 4)
+// (crates/gguf/src/lib.rs:1295-1367).
+template <>
+struct Frag<INFERNO_Q3_K> {
+  static constexpr int kBytes = 110, kRaw = 11;
+  __device__ static void load(const uint8_t* b, int qc, int kg, uint32_t r[kRaw]) {
+    const int n = qc >> 1;
+    const uint2 qa = ld_u2(b + 32 + 32 * n + 8 * kg);
+    const uint2 qb = ld_u2(b + 48 + 32 * n + 8 * kg);
+    const uint2 ha = ld_u2(b + 8 * kg);
+    const uint2 hb = ld_u2(b + 16 + 8 * kg);
+    r[0] = qa.x; r[1] = qa.y; r[2] = qb.x; r[3] = qb.y;
+    r[4] = ha.x; r[5] = ha.y; r[6] = hb.x; r[7] = hb.y;
+    r[8] = ld_u1(b + 96 + 4 * (qc & 1));  // low-nibble bytes of groups (4 qc + s) % 8
+    r[9] = ld_u1(b + 104);                // high-bit bytes
+    r[10] = *reinterpret_cast<const uint16_t*>(b + 108);  // d
+  }
+  template <int QC>
+  __device__ static half8 get(const uint32_t r[kRaw], int s) {
+    const int n = QC >> 1, jj = 2 * (QC & 1) + (s >> 1);
+    const int hshift = 4 * n + jj;
+    // q + 4 hbit as a 3-bit field in every byte
+    const uint32_t w0 = ((((s & 1) ? r[2] : r[0]) >> (2 * jj)) & 0x03030303u) |
+                        (((((s & 1) ? r[6] : r[4]) >> hshift) & 0x01010101u) << 2);
+    const uint32_t w1 = ((((s & 1) ? r[3] : r[1]) >> (2 * jj)) & 0x03030303u) |
+                        (((((s & 1) ? r[7] : r[5]) >> hshift) & 0x01010101u) << 2);
+    const uint32_t lob = byte_of(r[8], s);
+    const uint32_t lo = QC < 2 ? (lob & 15u) : (lob >> 4);
+    const uint32_t hi = (byte_of(r[9], s) >> (2 * QC)) & 3u;
+    const float dl = f16_bits_to_f32_fast(uint16_t(r[10])) * float(int(lo | (hi << 4)) - 32);
+    return dequant8(w0, w1, 0x00070007u, __builtin_amdgcn_ldexpf(dl, 24), -4.0f * dl);
+  }
+};
+
+// Q4_K [d | dmin | scales 12 | qs 128]: value j = 64 c + 32 hh + l uses
+// q = (qs[32 c + l] >> 4 hh) & 15 and the 6-bit (sc, m) of group 2 c + hh
+// (crates/gguf/src/lib.rs:1369-1416).
+template <>
+struct Frag<INFERNO_Q4_K> {
+  static constexpr int kBytes = 144, kRaw = 8;
+  __device__ static void load(const uint8_t* b, int qc, int kg, uint32_t r[kRaw]) {
+    const uint2 a = ld_u2(b + 16 + 32 * qc + 8 * kg);
+    const uint2 c = ld_u2(b + 32 + 32 * qc + 8 * kg);
+    r[0] = a.x; r[1] = a.y; r[2] = c.x; r[3] = c.y;
+    r[4] = ld_u1(b + 4); r[5] = ld_u1(b + 8); r[6] = ld_u1(b + 12);  // scales
+    r[7] = ld_u1(b);  // d | dmin
+  }
+  template <int QC>
+  __device__ static half8 get(const uint32_t r[kRaw], int s) {
+    const int hh = s >> 1, g = 2 * QC + hh;
+    auto sb = [&](int i) -> uint32_t {
+      const uint32_t w = i < 4 ? r[4] : (i < 8 ? r[5] : r[6]);
+      return byte_of(w, i & 3);
+    };
+    uint32_t sc, m;
+    if (g < 4) {
+      sc = sb(g) & 63u;
+      m = sb(g + 4) & 63u;
+    } else {
+      sc = (sb(g + 4) & 15u) | ((sb(g - 4) >> 6) << 4);
+      m = (sb(g + 4) >> 4) | ((sb(g) >> 6) << 4);
+    }
+    const float d = f16_bits_to_f32_fast(uint16_t(r[7]));
+    const float dmin = f16_bits_to_f32_fast(uint16_t(r[7] >> 16));
+    const float mult = __builtin_amdgcn_ldexpf(d * float(sc), 24 - 4 * hh);
+    return dequant8((s & 1) ? r[2] : r[0], (s & 1) ? r[3] : r[1], 0x000f000fu << (4 * hh), mult,
+                    -(dmin * float(m)));
+  }
+};
+
+// Q8_0: a K unit is eight 34-byte blocks [d | int8 x32]; value = d * q
+// (crates/gguf/src/lib.rs:1472-1499). Codes enter as q ^ 0x80 = q + 128.
+template <>
+struct Frag<INFERNO_Q8_0> {
+  static constexpr int kBytes = 272, kRaw = 10;
+  __device__ static void load(const uint8_t* b, int qc, int kg, uint32_t r[kRaw]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int blk = 2 * qc + (s >> 1);
+      const uint2 v = ld_u2(b + 34 * blk + 2 + 16 * (s & 1) + 8 * kg);
+      r[2 * s] = v.x;
+      r[2 * s + 1] = v.y;
+    }
+    r[8] = *reinterpret_cast<const uint16_t*>(b + 68 * qc);
+    r[9] = *reinterpret_cast<const uint16_t*>(b + 68 * qc + 34);
+  }
+  template <int QC>
+  __device__ static half8 get(const uint32_t r[kRaw], int s) {
+    const float d = f16_bits_to_f32_fast(uint16_t((s >> 1) ? r[9] : r[8]));
+    return dequant8(r[2 * s] ^ 0x80808080u, r[2 * s + 1] ^ 0x80808080u, 0x00ff00ffu,
+                    __builtin_amdgcn_ldexpf(d, 24), -128.0f * d);
+  }
+};
+
+// ------------------------------------------------------------------ GEMM
+
+struct GemmArgs {
+  const uint8_t* w0;       // gate (or the down / single matrix)
+  const uint8_t* w1;       // up, null for one matrix
+  size_t stride;           // bytes per expert matrix
+  const uint16_t* xin;     // f16 input rows (k order 0 2 1 3 4 6 5 7), K halfs each
+  uint32_t in_div;         // input row = (sorted[c] or c) / in_div
+  const uint32_t* sorted;  // dispatch order, null = dense (identity)
+  const float* route_w;    // routing weight per assignment, null = 1
+  const uint4* tiles;      // {expert, c0, c1, 0}; null = dense tiles of TM rows
+  const uint32_t* n_tiles;
+  uint32_t rows;           // dense: number of rows
+  int N, K;                // output rows per matrix, reduction length
+  uint16_t* h_out;         // two matrices: f16 SwiGLU rows [*, N] (k order as xin)
+  float* y_out;            // one matrix: fp32 rows [*, N]
+};
+
+template <int TM>
+constexpr size_t gemm_lds_bytes() {
+  return size_t(2) * TM * kLdsPitch * 2;
+}
+
+// Two waves per SIMD: the accumulators fit beside the operands in 256
+// registers, and a second workgroup per CU hides the load latency.
+template <int TM>
+struct GemmOcc {
+  static constexpr int value = 2;
+};
+
+template <int Q, int NMAT, int TM>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GemmOcc<TM>::value, 8)))
+    gemm_kernel(GemmArgs p) {
+  using F = Frag<Q>;
+  constexpr int NB = TM / 32;  // 32-token blocks
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs_raw[];
+  auto xs = [&](int buf, int row) { return xs_raw + (size_t(buf) * TM + row) * kLdsPitch; };
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, kg = lane >> 5;
+  uint32_t e = 0, c0, c1;
+  if (p.tiles) {
+    if (blockIdx.y >= *p.n_tiles) return;
+    const uint4 t = p.tiles[blockIdx.y];
+    e = t.x;
+    c0 = t.y;
+    c1 = t.z;
+  } else {
+    c0 = blockIdx.y * TM;
+    c1 = min(c0 + uint32_t(TM), p.rows);
+  }
+  const int n0 = blockIdx.x * kTileN;
+  const int K = p.K;
+  const size_t row_bytes = size_t(K / kUnit) * F::kBytes;
+  const size_t roff = size_t(e) * p.stride + size_t(n0 + 32 * wave + i) * row_bytes;
+  const uint8_t* w0 = p.w0 + roff;
+  const uint8_t* w1 = NMAT == 2 ? p.w1 + roff : nullptr;
+
+  // token rows this thread stages: piece pc (8 halfs) of rows (tid >> 3) + 32 j
+  const int pc = tid & 7;
+  const uint16_t* src[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const uint32_t c = c0 + uint32_t((tid >> 3) + 32 * j);
+    src[j] = nullptr;
+    if (c < c1) {
+      const uint32_t a = p.sorted ? p.sorted[c] : c;
+      src[j] = p.xin + size_t(a / p.in_div) * K + 8 * pc;
+    }
+  }
+  uint4 xv[NB];
+  auto load_x = [&](int st) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+      xv[j] = src[j] ? *reinterpret_cast<const uint4*>(src[j] + 64 * st) : make_uint4(0, 0, 0, 0);
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+      *reinterpret_cast<uint4*>(xs(buf, (tid >> 3) + 32 * j) + 8 * pc) = xv[j];
+  };
+
+  floatx16 acc0[NB], acc1[NB];
+#pragma unroll
+  for (int tb = 0; tb < NB; ++tb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      acc0[tb][v] = 0.f;
+      acc1[tb][v] = 0.f;
+    }
+  }
+  // two register sets for the quant bytes: chunk qc uses set qc & 1, while
+  // the next chunk's bytes land in the other
+  uint32_t ra0[F::kRaw], ra1[F::kRaw], rb0[F::kRaw], rb1[F::kRaw];
+  const int nkb = K / kUnit;
+  load_x(0);
+  F::load(w0, 0, kg, ra0);
+  if constexpr (NMAT == 2) F::load(w1, 0, kg, ra1);
+  store_x(0);
+  __syncthreads();
+
+  auto step = [&](auto qc_c, int kb, uint32_t (&c0r)[F::kRaw], uint32_t (&c1r)[F::kRaw],
+                  uint32_t (&n0r)[F::kRaw], uint32_t (&n1r)[F::kRaw]) {
+    constexpr int QC = decltype(qc_c)::value;
+    constexpr int buf = QC & 1;
+    const int st = 4 * kb + QC;
+    const bool more = QC < 3 || kb + 1 < nkb;
+    if (more) {
+      load_x(st + 1);
+      const size_t boff = size_t(QC < 3 ? kb : kb + 1) * F::kBytes;
+      F::load(w0 + boff, (QC + 1) & 3, kg, n0r);
+      if constexpr (NMAT == 2) F::load(w1 + boff, (QC + 1) & 3, kg, n1r);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const half8 a0 = F::template get<QC>(c0r, s);
+      half8 a1;
+      if constexpr (NMAT == 2) a1 = F::template get<QC>(c1r, s);
+#pragma unroll
+      for (int tb = 0; tb < NB; ++tb) {
+        const half8 b = *reinterpret_cast<const half8*>(xs(buf, tb * 32 + i) + 16 * s + 8 * kg);
+        acc0[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc0[tb], 0, 0, 0);
+        if constexpr (NMAT == 2)
+          acc1[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc1[tb], 0, 0, 0);
+      }
+    }
+    if (more) store_x(buf ^ 1);
+    __syncthreads();
+  };
+  for (int kb = 0; kb < nkb; ++kb) {
+    step(std::integral_constant<int, 0>{}, kb, ra0, ra1, rb0, rb1);
+    step(std::integral_constant<int, 1>{}, kb, rb0, rb1, ra0, ra1);
+    step(std::integral_constant<int, 2>{}, kb, ra0, ra1, rb0, rb1);
+    step(std::integral_constant<int, 3>{}, kb, rb0, rb1, ra0, ra1);
+  }
+
+  // accumulator element v of lane (i, kg): weight row 8 (v / 4) + 4 kg + v % 4
+  // of this wavefront's 32, token column i of the 32-token block
+#pragma unroll
+  for (int tb = 0; tb < NB; ++tb) {
+    const uint32_t c = c0 + uint32_t(tb * 32 + i);
+    if (c >= c1) continue;
+    const uint32_t a = p.sorted ? p.sorted[c] : c;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int r0 = n0 + 32 * wave + 8 * g4 + 4 * kg;
+      if constexpr (NMAT == 2) {
+        const float wa = p.route_w ? p.route_w[a] : 1.0f;
+        float h[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          h[r] = silu(acc0[tb][4 * g4 + r]) * acc1[tb][4 * g4 + r] * wa;
+        // rows r0 .. r0 + 3 stored in the k order 0 2 1 3 of the next GEMM
+        const half2v lo = {(_Float16)h[0], (_Float16)h[2]};
+        const half2v hi = {(_Float16)h[1], (_Float16)h[3]};
+        *reinterpret_cast<uint2*>(p.h_out + size_t(a) * p.N + r0) = make_uint2(as_u32(lo), as_u32(hi));
+      } else {
+        *reinterpret_cast<float4*>(p.y_out + size_t(a) * p.N + r0) =
+            make_float4(acc0[tb][4 * g4], acc0[tb][4 * g4 + 1], acc0[tb][4 * g4 + 2],
+                        acc0[tb][4 * g4 + 3]);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- planning
+
+// Tiles of one expert with n rows: full 128-row tiles, then the remainder r
+// as one 128-row tile (r > 32) or one 32-row tile. The dequantisation cost
+// of a tile does not depend on its row count, the MFMA cost does: small
+// remainders take the cheap 32-row tile.
+struct TileCounts {
+  uint32_t t128, t32;
+};
+__device__ __forceinline__ TileCounts tile_counts(uint32_t n) {
+  const uint32_t r = n % 128;
+  TileCounts t{n / 128, 0};
+  if (r > 32) t.t128 += 1;
+  else if (r > 0) t.t32 = 1;
+  return t;
+}
+
+// One workgroup: the two tile lists of all active experts, expert order.
+__global__ void __launch_bounds__(256)
+    plan_kernel(const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ active,
+                uint4* __restrict__ l128, uint4* __restrict__ l32, uint32_t* __restrict__ counts) {
+  __shared__ uint32_t sc[2][256];
+  const int j = threadIdx.x;
+  const uint32_t n_act = active[0];
+  uint32_t e = 0, lo = 0, hi = 0;
+  TileCounts t{0, 0};
+  if (uint32_t(j) < n_act) {
+    e = active[1 + j];
+    lo = offsets[e];
+    hi = offsets[e + 1];
+    t = tile_counts(hi - lo);
+  }
+  sc[0][j] = t.t128;
+  sc[1][j] = t.t32;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {
+    const uint32_t v0 = j >= o ? sc[0][j - o] : 0u, v1 = j >= o ? sc[1][j - o] : 0u;
+    __syncthreads();
+    sc[0][j] += v0;
+    sc[1][j] += v1;
+    __syncthreads();
+  }
+  const uint32_t o128 = sc[0][j] - t.t128, o32 = sc[1][j] - t.t32;
+  for (uint32_t q = 0; q < t.t128; ++q)
+    l128[o128 + q] = make_uint4(e, lo + 128 * q, min(hi, lo + 128 * (q + 1)), 0);
+  if (t.t32) l32[o32] = make_uint4(e, lo + 128 * t.t128, hi, 0);
+  if (j == 255) {
+    counts[0] = sc[0][255];
+    counts[1] = sc[1][255];
+  }
+}
+
+// Upper bounds of the tile lists (grid heights): a 128-row tile covers at
+// least 33 rows, the 32-row list holds at most one tile per expert.
+size_t bound128(size_t A, size_t E) { return A / 33 + 1; }
+size_t bound32(size_t A, size_t E) { return std::min(E, A) + 1; }
+
+// ----------------------------------------------------------- conversions
+
+// x -> f16 with the k order 0 2 1 3 4 6 5 7 inside every group of eight.
+template <typename XT>
+__global__ void __launch_bounds__(256)
+    to_f16_kernel(const XT* __restrict__ x, size_t n8, uint4* __restrict__ out) {
+  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n8) return;
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = to_f32(x[8 * i + j]);
+  const half2v a = {(_Float16)v[0], (_Float16)v[2]}, b = {(_Float16)v[1], (_Float16)v[3]};
+  const half2v c = {(_Float16)v[4], (_Float16)v[6]}, d = {(_Float16)v[5], (_Float16)v[7]};
+  out[i] = make_uint4(as_u32(a), as_u32(b), as_u32(c), as_u32(d));
+}
+
+__global__ void __launch_bounds__(256)
+    combine_kernel(const float* __restrict__ y, const float* __restrict__ ys,
+                   const float* __restrict__ residual, int k, size_t H, size_t n4,
+                   float4* __restrict__ out) {
+  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const size_t t = (4 * i) / H, col = (4 * i) % H;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (residual) v = *reinterpret_cast<const float4*>(residual + 4 * i);
+  if (ys) {
+    const float4 s = *reinterpret_cast<const float4*>(ys + 4 * i);
+    v.x += s.x; v.y += s.y; v.z += s.z; v.w += s.w;
+  }
+  for (int r = 0; r < k; ++r) {
+    const float4 u = *reinterpret_cast<const float4*>(y + (t * k + r) * H + col);
+    v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+  }
+  out[i] = v;
+}
+
+// ------------------------------------------------------------- launchers
+
+template <int Q, int NMAT, int TM>
+int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
+  if (grid_y == 0) return INFERNO_OK;
+  const dim3 grid(unsigned(a.N / kTileN), grid_y);
+  gemm_kernel<Q, NMAT, TM><<<grid, 256, gemm_lds_bytes<TM>(), s>>>(a);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+template <int NMAT, int TM>
+int launch_gemm_q(hipStream_t s, int quant, const GemmArgs& a, unsigned grid_y) {
+  switch (quant) {
+    case INFERNO_Q2_K: return launch_gemm<INFERNO_Q2_K, NMAT, TM>(s, a, grid_y);
+    case INFERNO_Q3_K: return launch_gemm<INFERNO_Q3_K, NMAT, TM>(s, a, grid_y);
+    case INFERNO_Q4_K: return launch_gemm<INFERNO_Q4_K, NMAT, TM>(s, a, grid_y);
+    case INFERNO_Q8_0: return launch_gemm<INFERNO_Q8_0, NMAT, TM>(s, a, grid_y);
+  }
+  set_error("quant kind has no MFMA prefill GEMM");
+  return INFERNO_ERR_INVALID;
+}
+
+struct PlanView {
+  uint4* l128;
+  uint4* l32;
+  uint32_t* counts;
+  size_t n128, n32;
+};
+
+PlanView plan_view(uint32_t* plan, size_t A, size_t E) {
+  PlanView v;
+  v.n128 = bound128(A, E);
+  v.n32 = bound32(A, E);
+  v.l128 = reinterpret_cast<uint4*>(plan);
+  v.l32 = v.l128 + v.n128;
+  v.counts = reinterpret_cast<uint32_t*>(v.l32 + v.n32);
+  return v;
+}
+
+// The two tile-list launches of one GEMM.
+template <int NMAT>
+int launch_tiled(hipStream_t s, int quant, GemmArgs a, const PlanView& v) {
+  int st;
+  a.tiles = v.l128;
+  a.n_tiles = v.counts;
+  if ((st = launch_gemm_q<NMAT, 128>(s, quant, a, unsigned(v.n128)))) return st;
+  a.tiles = v.l32;
+  a.n_tiles = v.counts + 1;
+  return launch_gemm_q<NMAT, 32>(s, quant, a, unsigned(v.n32));
+}
+
+// Dense GEMMs: tiles of TM rows over all T rows; TM from T so that small
+// batches still spread over the chip.
+template <int NMAT>
+int launch_dense(hipStream_t s, int quant, GemmArgs a, size_t T) {
+  if (T >= 512) return launch_gemm_q<NMAT, 128>(s, quant, a, unsigned((T + 127) / 128));
+  return launch_gemm_q<NMAT, 32>(s, quant, a, unsigned((T + 31) / 32));
+}
+
+}  // namespace
+
+bool prefill_supported(int quant) {
+  return quant == INFERNO_Q2_K || quant == INFERNO_Q3_K || quant == INFERNO_Q4_K ||
+         quant == INFERNO_Q8_0;
+}
+
+bool prefill_routed_supported(int quant, int down_quant, size_t H, size_t I, size_t E) {
+  auto routed = [](int q) {
+    return q == INFERNO_Q2_K || q == INFERNO_Q3_K || q == INFERNO_Q4_K;
+  };
+  return routed(quant) && routed(down_quant) && H % kUnit == 0 && I % kUnit == 0 && E <= 256;
+}
+
+size_t prefill_plan_words(size_t A, size_t E) {
+  return 4 * (bound128(A, E) + bound32(A, E)) + 4;
+}
+
+int launch_to_f16(hipStream_t s, const void* x, int x_dtype, size_t rows, size_t K,
+                  uint16_t* out) {
+  const size_t n8 = rows * K / 8;
+  if (n8 == 0) return INFERNO_OK;
+  const unsigned grid = unsigned((n8 + 255) / 256);
+  if (x_dtype == INFERNO_BF16)
+    to_f16_kernel<uint16_t><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x), n8,
+                                                 reinterpret_cast<uint4*>(out));
+  else
+    to_f16_kernel<float><<<grid, 256, 0, s>>>(static_cast<const float*>(x), n8,
+                                              reinterpret_cast<uint4*>(out));
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+int launch_prefill_gate_up(hipStream_t s, const PrefillRouted& p) {
+  const size_t A = p.T * p.k;
+  if (A == 0) return INFERNO_OK;
+  if (!prefill_routed_supported(p.quant, p.down_quant, p.H, p.I, p.E)) {
+    set_error("MFMA prefill path does not cover this layer");
+    return INFERNO_ERR_INVALID;
+  }
+  const PlanView v = plan_view(p.plan, A, p.E);
+  plan_kernel<<<1, 256, 0, s>>>(p.offsets, p.active, v.l128, v.l32, v.counts);
+  INF_LAUNCHED();
+  GemmArgs g{};
+  g.w0 = static_cast<const uint8_t*>(p.gate);
+  g.w1 = static_cast<const uint8_t*>(p.up);
+  g.stride = p.I * (p.H / kUnit) * size_t(block_bytes(p.quant));
+  g.xin = p.x16;
+  g.in_div = uint32_t(p.k);
+  g.sorted = p.sorted;
+  g.route_w = p.weights;
+  g.N = int(p.I);
+  g.K = int(p.H);
+  g.h_out = p.h16;
+  return launch_tiled<2>(s, p.quant, g, v);
+}
+
+int launch_prefill_down(hipStream_t s, const PrefillRouted& p) {
+  const size_t A = p.T * p.k;
+  if (A == 0) return INFERNO_OK;
+  const PlanView v = plan_view(p.plan, A, p.E);
+  GemmArgs d{};
+  d.w0 = static_cast<const uint8_t*>(p.down);
+  d.stride = p.H * (p.I / kUnit) * size_t(block_bytes(p.down_quant));
+  d.xin = p.h16;
+  d.in_div = 1;
+  d.sorted = p.sorted;
+  d.N = int(p.H);
+  d.K = int(p.I);
+  d.y_out = p.y;
+  return launch_tiled<1>(s, p.down_quant, d, v);
+}
+
+int launch_prefill_dense(hipStream_t s, const void* gate, const void* up, const void* down,
+                         const uint16_t* x16, size_t T, size_t H, size_t Is, uint16_t* h16,
+                         float* ys) {
+  if (T == 0) return INFERNO_OK;
+  if (H % kUnit || Is % kUnit) {
+    set_error("MFMA prefill path needs 256-multiple dimensions");
+    return INFERNO_ERR_INVALID;
+  }
+  GemmArgs g{};
+  g.w0 = static_cast<const uint8_t*>(gate);
+  g.w1 = static_cast<const uint8_t*>(up);
+  g.xin = x16;
+  g.in_div = 1;
+  g.rows = uint32_t(T);
+  g.N = int(Is);
+  g.K = int(H);
+  g.h_out = h16;
+  int st;
+  if ((st = launch_dense<2>(s, INFERNO_Q8_0, g, T))) return st;
+  GemmArgs d{};
+  d.w0 = static_cast<const uint8_t*>(down);
+  d.xin = h16;
+  d.in_div = 1;
+  d.rows = uint32_t(T);
+  d.N = int(H);
+  d.K = int(Is);
+  d.y_out = ys;
+  return launch_dense<1>(s, INFERNO_Q8_0, d, T);
+}
+
+int launch_prefill_combine(hipStream_t s, const float* y, const float* ys, const float* residual,
+                           size_t T, size_t k, size_t H, float* out) {
+  const size_t n4 = T * H / 4;
+  if (n4 == 0) return INFERNO_OK;
+  combine_kernel<<<unsigned((n4 + 255) / 256), 256, 0, s>>>(y, ys, residual, int(k), H, n4,
+                                                             reinterpret_cast<float4*>(out));
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+}  // namespace inferno

@@ -1,0 +1,50 @@
+// Prefill (many tokens per expert): grouped dequant-GEMM on MFMA (prefill.hip).
+#pragma once
+#include "common.hpp"
+
+namespace inferno {
+
+// Weight kinds the MFMA GEMM dequantises (routed Q2_K/Q3_K/Q4_K, Q8_0 dense).
+bool prefill_supported(int quant);
+// True when the routed layer (gate/up kind, down kind, shapes) has the MFMA path.
+bool prefill_routed_supported(int quant, int down_quant, size_t H, size_t I, size_t E);
+// Assignments from which the routed layer takes the MFMA path.
+constexpr size_t kPrefillMinAssignments = 256;
+
+// 32-bit words of the routed planner's scratch (tile lists and counts).
+size_t prefill_plan_words(size_t A, size_t E);
+
+// x [rows, K] (bf16 or fp32) -> f16 [rows, K], round to nearest even.
+int launch_to_f16(hipStream_t s, const void* x, int x_dtype, size_t rows, size_t K, uint16_t* out);
+
+struct PrefillRouted {
+  int quant, down_quant;
+  const void *gate, *up, *down;  // packed experts [E][rows][blocks]
+  const uint16_t* x16;           // [T, H] f16
+  const uint32_t* offsets;       // [E+1] from the dispatch
+  const uint32_t* sorted;        // [A]
+  const uint32_t* active;        // [E+1]
+  const float* weights;          // [A] routing weights (folded into h)
+  size_t T, k, E, H, I;
+  uint16_t* h16;                 // [A, I] SwiGLU intermediate, f16
+  float* y;                      // [A, H] per-assignment down rows
+  uint32_t* plan;                // prefill_plan_words(A, E)
+};
+
+// Routed gate/up (+SwiGLU, routing weight) over the dispatch groups: plans
+// the expert tiles, then the GEMM; writes h16.
+int launch_prefill_gate_up(hipStream_t s, const PrefillRouted& p);
+// Routed down over the same tiles (after launch_prefill_gate_up): writes y.
+int launch_prefill_down(hipStream_t s, const PrefillRouted& p);
+
+// Dense Q8_0 expert over all T rows: h16 = silu(x G^T) * (x U^T); ys = h16 D^T.
+int launch_prefill_dense(hipStream_t s, const void* gate, const void* up, const void* down,
+                         const uint16_t* x16, size_t T, size_t H, size_t Is, uint16_t* h16,
+                         float* ys);
+
+// out = (residual + ys) + sum over ranks of y[t*k + r] (rank order); residual,
+// ys may be null.
+int launch_prefill_combine(hipStream_t s, const float* y, const float* ys, const float* residual,
+                           size_t T, size_t k, size_t H, float* out);
+
+}  // namespace inferno

@@ -161,6 +161,49 @@ def test_gguf_moe_matches_oracle(cuda, quant, down, T, H, I, E, k, bf16):
     assert err < ph.TOL_REL_L2
 
 
+def _skewed_ids(T, E, k, hot=(0, 1), share=(1.0, 0.8)):
+    """Routing where expert hot[i] takes a `share[i]` fraction of the tokens
+    (ranks 0, 1, ...) and the other ranks are random distinct experts."""
+    rows = []
+    for _ in range(T):
+        first = [h for h, p in zip(hot, share) if rng.random() < p]
+        rest = [e for e in rng.permutation(E) if e not in first][: k - len(first)]
+        rows.append(first + rest)
+    return np.array(rows, np.uint32).reshape(-1)
+
+
+@pytest.mark.parametrize("quant", [Q2_K, Q3_K, Q4_K])
+@pytest.mark.parametrize("T,H,I,E,k,bf16,skew", [(64, 512, 256, 16, 4, True, False),
+                                                 (96, 768, 512, 8, 4, False, True)])
+def test_gguf_moe_mfma_prefill(cuda, quant, T, H, I, E, k, bf16, skew):
+    # T * k >= 256 assignments: the MFMA grouped GEMM (f16 operands, fp32
+    # accumulation). The skewed case gives two experts >= 64 rows (128-row
+    # tiles) next to small experts (32-row tiles).
+    # weights of realistic size (N(0, 0.02) quantised): the f16 operands and
+    # the f16 intermediate, as in the reference's prefill kernels
+    # (gguf_moe_prefill_kernels.metal:50-59, :263), cover |h| < 65504 only
+    seed = 77 + quant
+    gate = ph.to_np(ops.synth_quantized(quant, seed, 0.02, E * I, H, cuda))
+    up = ph.to_np(ops.synth_quantized(quant, seed + 1, 0.02, E * I, H, cuda))
+    dn = ph.to_np(ops.synth_quantized(quant, seed + 2, 0.02, E * H, I, cuda))
+    x = torch.randn(T, H, device=cuda)
+    if bf16:
+        x = x.bfloat16()
+    ids = (_skewed_ids(T, E, k) if skew else
+           np.stack([rng.permutation(E)[:k] for _ in range(T)]).reshape(-1).astype(np.uint32))
+    w = rng.random(T * k).astype(np.float32)
+    args = (quant, quant, dev(gate, cuda), dev(up, cuda), dev(dn, cuda), x,
+            dev(ids.view(np.int32), cuda), dev(w, cuda), k, E, I)
+    out = ops.gguf_moe(*args)
+    out2 = ops.gguf_moe(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), "MFMA prefill output is not bitwise reproducible"
+    ref = orc.moe_routed(quant, quant, gate, up, dn, ph.x_f32(x), ids, w, E, k, I)
+    err = rn.rel_l2(ph.to_np(out), ref)
+    print(f"rel_l2={err:.3e}")
+    assert err < ph.TOL_REL_L2
+
+
 def test_q3_known_block(cuda):
     # gguf_moe.rs:468-514: silu(d)*d*d with d = 384/1024
     sel = kb.q3_k_block(0x1400, [33] * 16, 0xE4, 0xFF)
@@ -264,6 +307,32 @@ def test_layer_c2_glm_q2k_decode_full_size(cuda):
 
 def test_layer_c3_glm_q3k_prefill_sampled_tokens(cuda):
     _layer_parity(cuda, "c3", 512, tokens=[0, 1, 255, 511])
+
+
+def test_layer_c5_glm_q2k_prefill_zipf_sampled_tokens(cuda):
+    # full-size skewed prefill: router bias fitted so the load follows Zipf(1.1)
+    cfg = cf.CONFIGS["c5"]
+    T = 4096
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
+    x = cf.make_input(cfg, T, device=cuda)
+    logits = ops.router_logits(x, lt.router)
+    lt.bias.copy_(torch.from_numpy(cf.zipf_bias(cfg, ph.to_np(logits))).to(cuda))
+    residual = torch.randn(T, cfg.hidden, device=cuda)
+    ids = torch.empty(T * cfg.top_k, dtype=torch.int32, device=cuda)
+    w = torch.empty(T * cfg.top_k, dtype=torch.float32, device=cuda)
+    out = lt.layer.forward(x, residual, ids=ids, weights=w)
+    torch.cuda.synchronize()
+    load = np.bincount(ph.to_np(ids).astype(np.int64), minlength=cfg.experts)
+    print(f"c5 load: hottest share {load.max() / (T * cfg.top_k):.3f}, "
+          f"empty experts {(load == 0).sum()}")
+    assert load.max() >= 64  # some experts take the 128-row tiles
+    tokens = [0, 1, 2047, 4095]
+    ref, _, _, flips = ph.oracle_layer_tokens(cfg, lt, x, residual, tokens,
+                                              ph.to_np(ids).view(np.uint32), ph.to_np(w))
+    res = ph.to_np(residual)[tokens]
+    err = rn.rel_l2(ph.to_np(out)[tokens] - res, ref - res)
+    print(f"c5 T={T}: rel_l2(moe part)={err:.3e} near-tie tokens={flips}")
+    assert err < ph.TOL_REL_L2
 
 
 @pytest.mark.parametrize("T", [1, 32])
