@@ -512,7 +512,7 @@ int launch_tiled(hipStream_t s, int quant, GemmArgs a, const PlanView& v) {
 // batches still spread over the chip.
 template <int NMAT>
 int launch_dense(hipStream_t s, int quant, GemmArgs a, size_t T) {
-  if (T >= 512) return launch_gemm_q<NMAT, 128>(s, quant, a, unsigned((T + 127) / 128));
+  if (T >= 2048) return launch_gemm_q<NMAT, 128>(s, quant, a, unsigned((T + 127) / 128));
   return launch_gemm_q<NMAT, 32>(s, quant, a, unsigned((T + 31) / 32));
 }
 

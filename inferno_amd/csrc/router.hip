@@ -103,6 +103,84 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// Many tokens on the fp32 matrix cores (v_mfma_f32_16x16x4_f32: fp32 products
+// and sums, so the logits keep fp32 accuracy). A wavefront computes 16
+// experts x 16*NTB tokens; a workgroup of four covers 64 experts. Per 32-deep
+// K block, lane (row r = lane % 16, group g = lane / 16) holds
+// w[e0 + r][k0 + 8 g .. +8] and the same eight k of each of its NTB token
+// rows; MFMA step j multiplies element j of every group (k = k0 + 8 g + j).
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+template <typename XT>
+__device__ __forceinline__ void load8(const XT* p, bool ok, float v[8]);
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, bool ok, float v[8]) {
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+  if (ok) {
+    a = *reinterpret_cast<const float4*>(p);
+    b = *reinterpret_cast<const float4*>(p + 4);
+  }
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+template <>
+__device__ __forceinline__ void load8<uint16_t>(const uint16_t* p, bool ok, float v[8]) {
+  uint4 q = make_uint4(0, 0, 0, 0);
+  if (ok) q = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __builtin_bit_cast(float, w[i] << 16);
+    v[2 * i + 1] = __builtin_bit_cast(float, w[i] & 0xffff0000u);
+  }
+}
+
+template <typename XT, int NTB>
+__global__ void __launch_bounds__(256)
+    logits_mfma_kernel(const XT* __restrict__ x, const float* __restrict__ w, int T, int H, int E,
+                       float* __restrict__ logits) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int e0 = blockIdx.x * 64 + wave * 16, t0 = blockIdx.y * (16 * NTB);
+  const bool ev = e0 + r < E;
+  const float* wrow = w + size_t(ev ? e0 + r : 0) * H + 8 * g;
+  const XT* xrow[NTB];
+  bool tv[NTB];
+#pragma unroll
+  for (int b = 0; b < NTB; ++b) {
+    const int t = t0 + 16 * b + r;
+    tv[b] = t < T;
+    xrow[b] = x + size_t(tv[b] ? t : 0) * H + 8 * g;
+  }
+  float4v acc[NTB][2];
+#pragma unroll
+  for (int b = 0; b < NTB; ++b)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) acc[b][h] = float4v{0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < H; k0 += 32) {
+    float a[8];
+    load8<float>(wrow + k0, ev, a);
+#pragma unroll
+    for (int b = 0; b < NTB; ++b) {
+      float v[8];
+      load8<XT>(xrow[b] + k0, tv[b], v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        acc[b][j & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], v[j], acc[b][j & 1], 0, 0, 0);
+    }
+  }
+  // lane holds C[4 g + q][r]: expert e0 + 4 g + q, token t0 + 16 b + r
+#pragma unroll
+  for (int b = 0; b < NTB; ++b) {
+    const int t = t0 + 16 * b + r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = e0 + 4 * g + q;
+      if (t < T && e < E) logits[size_t(t) * E + e] = acc[b][0][q] + acc[b][1][q];
+    }
+  }
+}
+
 __global__ void __launch_bounds__(256)
     topk_kernel(const float* __restrict__ logits, const float* __restrict__ bias, int T, int E,
                 int k, int score_fn, int norm, float scale, uint32_t* __restrict__ ids,
@@ -127,6 +205,27 @@ int launch_router_logits(hipStream_t s, const void* x, int x_dtype, const float*
     else
       logits_small_kernel<float><<<grid, 256, 0, s>>>(static_cast<const float*>(x), w, int(T),
                                                       int(H), int(E), logits);
+  } else if (H % 32 == 0) {
+    // fp32 MFMA: 64-token wavefront tiles for large batches (router rows
+    // reused four times per load), 16-token tiles otherwise (more tiles)
+    const bool wide = T >= 2048;
+    const unsigned tt = wide ? 64u : 16u;
+    dim3 grid(unsigned((E + 63) / 64), unsigned((T + tt - 1) / tt));
+    if (x_dtype == INFERNO_BF16) {
+      if (wide)
+        logits_mfma_kernel<uint16_t, 4><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x), w,
+                                                             int(T), int(H), int(E), logits);
+      else
+        logits_mfma_kernel<uint16_t, 1><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x), w,
+                                                             int(T), int(H), int(E), logits);
+    } else {
+      if (wide)
+        logits_mfma_kernel<float, 4><<<grid, 256, 0, s>>>(static_cast<const float*>(x), w, int(T),
+                                                          int(H), int(E), logits);
+      else
+        logits_mfma_kernel<float, 1><<<grid, 256, 0, s>>>(static_cast<const float*>(x), w, int(T),
+                                                          int(H), int(E), logits);
+    }
   } else {
     dim3 grid(unsigned((E + 63) / 64), unsigned((T + 63) / 64));
     if (x_dtype == INFERNO_BF16)

@@ -58,7 +58,9 @@ def test_dequant_reference_kats(cuda):
 
 
 @pytest.mark.parametrize("T,H,E,bf16", [(1, 6144, 256, True), (16, 2048, 64, False),
-                                        (77, 4096, 128, True)])
+                                        (77, 4096, 128, True), (100, 2048, 100, False),
+                                        (2100, 1024, 256, True), (2050, 512, 72, False),
+                                        (40, 800, 64, True)])
 def test_router_logits(cuda, T, H, E, bf16):
     x = torch.randn(T, H, device=cuda)
     if bf16:
