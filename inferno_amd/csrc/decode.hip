@@ -183,9 +183,30 @@ __global__ void __launch_bounds__(1024) select_kernel(DecodeArgs p) {
 // gate/up: routed grid = max_slots * tiles_i tiles (slot = tile / tiles_i,
 // idle when slot >= active[0]); shared grid = tiles_is tiles of the Q8_0
 // shared expert. The two run as separate launches on two streams.
-template <int Q, bool XSPLIT, bool SHARED>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8)))
-    gate_up_kernel(DecodeArgs p) {
+
+// Waves per SIMD the decode kernels are compiled for: two when a wavefront
+// holds four or more columns' quant bytes at once (256 registers), else three.
+template <int KU>
+struct DecodeOcc {
+  static constexpr int value = KU >= 2 ? 2 : 3;
+};
+
+// Largest column batch per wavefront that fits 256 registers without
+// spilling, by format and activation layout (gate/up holds two matrices).
+template <int Q, bool SPLIT>
+struct GateUpMaxKU {
+  static constexpr int value = Q == INFERNO_Q2_K ? (SPLIT ? 4 : 6)
+                               : Q == INFERNO_Q4_K ? (SPLIT ? 2 : 4)
+                                                   : (SPLIT ? 1 : 2);
+};
+template <int Q>
+struct DownMaxKU {
+  static constexpr int value = Q == INFERNO_Q2_K ? 16 : 8;
+};
+
+template <int Q, bool XSPLIT, bool SHARED, int WAVES, int KU>
+__global__ void __launch_bounds__(64 * WAVES)
+    __attribute__((amdgpu_waves_per_eu(DecodeOcc<KU>::value, 8))) gate_up_kernel(DecodeArgs p) {
   extern __shared__ uint32_t smem[];
   const int tid = threadIdx.x, slot = (tid & 63) >> 2;
   const int T = p.T, H = p.H, I = p.I, Is = p.Is, k = p.k;
@@ -214,13 +235,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
   }
   uint32_t* xs = smem;
   float* part = reinterpret_cast<float*>(smem + Sx);
-  float* res = part + tile_part_floats(1);
-  TileDot<Q, 2, 1, XSPLIT> td(r0, r1, H);
+  float* res = part + tile_part_floats(1, WAVES);
+  TileDot<Q, 2, 1, XSPLIT, WAVES, KU> td(r0, r1, H);
   for (uint32_t c = lo; c < hi; ++c) {
     const uint32_t a = shared ? c : (c == lo ? first : p.sorted[c]);
     const uint32_t tok = shared ? c : a / uint32_t(k);
     td.prefetch();  // quant loads in flight while x is copied
-    copy_rows_to_lds(xs, Sx, 1, [&](int) { return p.stage_x + size_t(tok) * Sx; });
+    copy_rows_to_lds<64 * WAVES>(xs, Sx, 1, [&](int) { return p.stage_x + size_t(tok) * Sx; });
     __syncthreads();
     td.run(xs, Sx, 1, part, res);
     if (tid < 16) {
@@ -241,8 +262,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
 // out = residual + shared + routed. The four wavefronts take the
 // (rank, super-block column) pairs round robin and meet in LDS: a fixed
 // order, deterministic without float atomics.
-template <int Q>
-__global__ void __launch_bounds__(256) down_sum_kernel(DecodeArgs p) {
+template <int Q, int WAVES, int KU>
+__global__ void __launch_bounds__(64 * WAVES)
+    __attribute__((amdgpu_waves_per_eu(DecodeOcc<KU>::value, 8))) down_sum_kernel(DecodeArgs p) {
   using F = Fmt<Q>;
   extern __shared__ uint32_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -253,19 +275,19 @@ __global__ void __launch_bounds__(256) down_sum_kernel(DecodeArgs p) {
   const int t = int(blockIdx.x) / tiles_h, tile = int(blockIdx.x) % tiles_h;
   const int S = staged_stride(I, true);
   uint32_t* xs = smem;                                   // k staged h rows
-  float* part = reinterpret_cast<float*>(smem + k * S);  // 4 * kRows
+  float* part = reinterpret_cast<float*>(smem + k * S);  // WAVES * kRows
   const int bpr = I / kKBlock;
   const size_t rb = size_t(bpr) * F::kBytes;
   const uint8_t* wrow = p.down + size_t(tile * kRows + slot) * rb;
   const uint32_t* ids = p.ids + size_t(t) * k;
   const int nq = k * bpr;
-  constexpr int kU = 4;
+  constexpr int kU = KU;
   uint32_t raw[kU][F::kDw];
-  // pairs q = wave + 4 (u + kU i) -> rank q / bpr, column q % bpr
+  // pairs q = wave + WAVES (u + kU i) -> rank q / bpr, column q % bpr
   auto issue = [&](int q0) {
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      const int q = q0 + 4 * u;
+      const int q = q0 + WAVES * u;
       if (q < nq) {
         const int r = q / bpr, col = q - r * bpr;
         F::load(wrow + size_t(ids[r]) * p.down_stride + size_t(col) * F::kBytes, sub, raw[u]);
@@ -274,15 +296,15 @@ __global__ void __launch_bounds__(256) down_sum_kernel(DecodeArgs p) {
   };
   issue(wave);  // quant loads in flight while the h rows are copied
   // the token's k assignments t*k .. t*k+k-1 are consecutive rows
-  copy_to_lds<8>(reinterpret_cast<uint4*>(xs),
+  copy_to_lds<8, 64 * WAVES>(reinterpret_cast<uint4*>(xs),
               reinterpret_cast<const uint4*>(p.stage_h + size_t(t) * k * S), k * S / 4);
   __syncthreads();
   float acc = 0.f;
-  for (int q0 = wave; q0 < nq; q0 += 4 * kU) {
+  for (int q0 = wave; q0 < nq; q0 += WAVES * kU) {
     if (q0 != wave) issue(q0);
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      const int q = q0 + 4 * u;
+      const int q = q0 + WAVES * u;
       if (q < nq) {
         const int r = q / bpr, col = q - r * bpr;
         acc += F::dot(raw[u], sub, xrow_at<true>(xs + r * S, I, col));
@@ -294,8 +316,88 @@ __global__ void __launch_bounds__(256) down_sum_kernel(DecodeArgs p) {
   if (sub == 0) part[wave * kRows + slot] = acc;
   __syncthreads();
   if (tid < kRows) {
-    const float v = ((part[tid] + part[kRows + tid]) + part[2 * kRows + tid]) + part[3 * kRows + tid];
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) v += part[w * kRows + tid];
     const size_t o = size_t(t) * H + size_t(tile) * kRows + tid;
+    p.out[o] = ((p.residual ? p.residual[o] : 0.f) + (p.Is ? p.ys[o] : 0.f)) + v;
+  }
+}
+
+// Routed down with the combine folded in, 8-row output tiles: workgroup =
+// (token t, 8 output rows), which makes T * H / 8 workgroups (768 for a
+// 6144-wide token: three per CU, one round). Lane = (column parity cp, row
+// r, sub); a lane group (wavefront, cp) takes the (rank, super-block column)
+// pairs q = cp + 2 wave + 8 u, with all KU of them in flight at once. The
+// token's k SwiGLU rows are copied to LDS as their f16 high parts only
+// (plus run sums and scales): about 2^-12 relative rounding per element.
+// Lane groups meet in registers (cp) and LDS (wavefronts) in a fixed order;
+// out = (residual + shared) + routed, deterministic without float atomics.
+template <int Q, int KU>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8)))
+    down8_kernel(DecodeArgs p) {
+  using F = Fmt<Q>;
+  extern __shared__ uint32_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = (lane >> 2) & 7, sub = lane & 3, cp = lane >> 5;
+  const int H = p.H, I = p.I, k = p.k;
+  const int tiles_h = H / 8;
+  const int t = int(blockIdx.x) / tiles_h, tile = int(blockIdx.x) % tiles_h;
+  const int Ss = staged_stride(I, true), Sn = staged_stride(I, false);
+  uint32_t* xs = smem;                                    // k rows, non-split layout
+  float* part = reinterpret_cast<float*>(smem + k * Sn);  // 4 wavefronts x 8 rows
+  const int bpr = I / kKBlock;
+  const size_t rb = size_t(bpr) * F::kBytes;
+  const uint8_t* wrow = p.down + size_t(tile * 8 + r) * rb;
+  const uint32_t* ids = p.ids + size_t(t) * k;
+  const int nq = k * bpr;
+  uint32_t raw[KU][F::kDw];
+  auto issue = [&](int q0) {
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int q = q0 + 8 * u;
+      if (q < nq) {
+        const int rank = q / bpr, col = q - rank * bpr;
+        F::load(wrow + size_t(ids[rank]) * p.down_stride + size_t(col) * F::kBytes, sub, raw[u]);
+      }
+    }
+  };
+  const int q_first = cp + 2 * wave;
+  issue(q_first);  // quant loads in flight while the h rows are copied
+  // staged h rows t*k .. t*k+k-1: copy the high pairs and the run sums/scales
+  {
+    const int hi4 = I / 8, tail4 = I / 32;  // uint4 words of the two parts
+    const int per = hi4 + tail4;
+    for (int i = tid; i < k * per; i += 256) {
+      const int rank = i / per, w = i - rank * per;
+      const uint4* from = reinterpret_cast<const uint4*>(p.stage_h + size_t(t * k + rank) * Ss);
+      uint4* to = reinterpret_cast<uint4*>(xs + rank * Sn);
+      // the high pairs are the first I/2 words, the sums/scales the last I/8
+      to[w] = w < hi4 ? from[w] : from[w + hi4];
+    }
+  }
+  __syncthreads();
+  float acc = 0.f;
+  for (int q0 = q_first; q0 < nq; q0 += 8 * KU) {
+    if (q0 != q_first) issue(q0);
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int q = q0 + 8 * u;
+      if (q < nq) {
+        const int rank = q / bpr, col = q - rank * bpr;
+        acc += F::dot(raw[u], sub, xrow_at<false>(xs + rank * Sn, I, col));
+      }
+    }
+  }
+  acc += __shfl_xor(acc, 1, kWave);
+  acc += __shfl_xor(acc, 2, kWave);
+  acc += __shfl_xor(acc, 32, kWave);
+  if ((lane & 35) == 0) part[wave * 8 + r] = acc;  // sub == 0, cp == 0
+  __syncthreads();
+  if (tid < 8) {
+    const float v = ((part[tid] + part[8 + tid]) + part[16 + tid]) + part[24 + tid];
+    const size_t o = size_t(t) * H + size_t(tile) * 8 + tid;
     p.out[o] = ((p.residual ? p.residual[o] : 0.f) + (p.Is ? p.ys[o] : 0.f)) + v;
   }
 }
@@ -324,19 +426,64 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))
   }
 }
 
-size_t down_sum_lds(int k, int I) { return (size_t(k) * staged_stride(I, true) + 4 * kRows) * 4; }
+// Routed decode kernels: four wavefronts per 16-row tile, each with all of
+// its quant loads (KU columns) in flight at once; two workgroups per CU
+// overlap one's streaming with the other's arithmetic.
+constexpr int kDecodeWaves = 4;
+size_t down_sum_lds(int k, int I) {
+  return (size_t(k) * staged_stride(I, true) + kDecodeWaves * kRows) * 4;
+}
 
+template <int Q, bool XSPLIT, int KU>
+void launch_gate_up_ku(hipStream_t s, const DecodeArgs& a) {
+  const size_t tiles = size_t(a.max_slots) * (a.I / kRows);
+  const size_t lds =
+      (size_t(staged_stride(a.H, XSPLIT)) + tile_part_floats(1, kDecodeWaves) + 2 * kRows) * 4;
+  gate_up_kernel<Q, XSPLIT, false, kDecodeWaves, KU>
+      <<<unsigned(tiles), 64 * kDecodeWaves, lds, s>>>(a);
+}
+
+// columns per wavefront: ceil(H / 256 / waves), capped by the format (a
+// longer row loops over batches)
 template <int Q, bool XSPLIT>
 void launch_gate_up(hipStream_t s, const DecodeArgs& a) {
-  const size_t tiles = size_t(a.max_slots) * (a.I / kRows);
-  const size_t lds = (size_t(staged_stride(a.H, XSPLIT)) + tile_part_floats(1) + 2 * kRows) * 4;
-  gate_up_kernel<Q, XSPLIT, false><<<unsigned(tiles), 256, lds, s>>>(a);
+  constexpr int kMax = GateUpMaxKU<Q, XSPLIT>::value;
+  const int per = (a.H / kKBlock + kDecodeWaves - 1) / kDecodeWaves;
+  if (per <= 1 || kMax == 1) launch_gate_up_ku<Q, XSPLIT, 1>(s, a);
+  else if (per <= 2 || kMax == 2) launch_gate_up_ku<Q, XSPLIT, (kMax < 2 ? kMax : 2)>(s, a);
+  else if (per <= 4 || kMax == 4) launch_gate_up_ku<Q, XSPLIT, (kMax < 4 ? kMax : 4)>(s, a);
+  else launch_gate_up_ku<Q, XSPLIT, kMax>(s, a);
+}
+
+size_t down8_lds(int k, int I) { return (size_t(k) * staged_stride(I, false) + 4 * 8) * 4; }
+
+template <int Q>
+void launch_down_sum(hipStream_t s, const DecodeArgs& a) {
+  if (a.H % 8 == 0) {
+    const unsigned grid8 = unsigned(size_t(a.T) * (a.H / 8));
+    const int per8 = (a.k * (a.I / kKBlock) + 7) / 8;
+    // Q3_K holds four pairs per batch without spilling, the others eight
+    constexpr int kMax8 = Q == INFERNO_Q3_K ? 4 : 8;
+    if (per8 <= 4 || kMax8 == 4)
+      down8_kernel<Q, 4><<<grid8, 256, down8_lds(a.k, a.I), s>>>(a);
+    else
+      down8_kernel<Q, kMax8><<<grid8, 256, down8_lds(a.k, a.I), s>>>(a);
+    return;
+  }
+  const unsigned grid = unsigned(size_t(a.T) * (a.H / kRows));
+  const size_t lds = down_sum_lds(a.k, a.I);
+  constexpr int kMax = DownMaxKU<Q>::value;
+  const int per = (a.k * (a.I / kKBlock) + kDecodeWaves - 1) / kDecodeWaves;
+  if (per <= 8 || kMax == 8)
+    down_sum_kernel<Q, kDecodeWaves, 8><<<grid, 64 * kDecodeWaves, lds, s>>>(a);
+  else
+    down_sum_kernel<Q, kDecodeWaves, kMax><<<grid, 64 * kDecodeWaves, lds, s>>>(a);
 }
 
 template <bool XSPLIT>
 int launch_shared(hipStream_t s, const DecodeArgs& a) {
   const size_t gu_lds = (size_t(staged_stride(a.H, XSPLIT)) + tile_part_floats(1) + 2 * kRows) * 4;
-  gate_up_kernel<INFERNO_Q8_0, XSPLIT, true><<<unsigned(a.Is / kRows), 256, gu_lds, s>>>(a);
+  gate_up_kernel<INFERNO_Q8_0, XSPLIT, true, 4, 0><<<unsigned(a.Is / kRows), 256, gu_lds, s>>>(a);
   INF_LAUNCHED();
   const size_t dn_lds = (size_t(staged_stride(a.Is, true)) + tile_part_floats(1) + 2 * kRows) * 4;
   shared_down_kernel<<<unsigned(a.H / kRows), 256, dn_lds, s>>>(a);
@@ -380,7 +527,7 @@ bool decode_supported(size_t T, size_t k, size_t E, size_t H, size_t I, size_t I
         (quant == INFERNO_Q2_K || quant == INFERNO_Q3_K || quant == INFERNO_Q4_K)))
     return false;
   const size_t kLds = 160 * 1024;
-  const size_t tile_extra = size_t(tile_part_floats(1) + 2 * kRows) * 4;
+  const size_t tile_extra = size_t(tile_part_floats(1, kDecodeWaves) + 2 * kRows) * 4;
   const size_t gate_up = size_t(staged_stride(int(H), x_dtype == INFERNO_F32)) * 4 + tile_extra;
   const size_t shared_down = Is ? size_t(staged_stride(int(Is), true)) * 4 + tile_extra : 0;
   return gate_up <= kLds && shared_down <= kLds && down_sum_lds(int(k), int(I)) + 64 <= kLds;
@@ -443,13 +590,11 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   if (st) return st;
   // the combined down pass adds the shared expert's rows
   if (a.Is) INF_HIP(hipStreamWaitEvent(s, side->join, 0));
-  const unsigned grid = unsigned(size_t(a.T) * (a.H / kRows));
-  const size_t lds = down_sum_lds(a.k, a.I);
   return timed(s, kTimerDown, [&] {
     switch (quant) {
-      case INFERNO_Q2_K: down_sum_kernel<INFERNO_Q2_K><<<grid, 256, lds, s>>>(a); break;
-      case INFERNO_Q3_K: down_sum_kernel<INFERNO_Q3_K><<<grid, 256, lds, s>>>(a); break;
-      default: down_sum_kernel<INFERNO_Q4_K><<<grid, 256, lds, s>>>(a); break;
+      case INFERNO_Q2_K: launch_down_sum<INFERNO_Q2_K>(s, a); break;
+      case INFERNO_Q3_K: launch_down_sum<INFERNO_Q3_K>(s, a); break;
+      default: launch_down_sum<INFERNO_Q4_K>(s, a); break;
     }
     INF_LAUNCHED();
     return INFERNO_OK;

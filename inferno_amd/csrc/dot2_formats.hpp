@@ -328,20 +328,24 @@ struct Occupancy {
 
 // ------------------------------------------------------------ tile compute
 
-// LDS floats tile_dot needs for its partial sums.
-__host__ __device__ constexpr int tile_part_floats(int nt) { return 4 * kRows * nt * 2; }
+// LDS floats TileDot needs for its partial sums (two matrices, `waves` wavefronts).
+__host__ __device__ constexpr int tile_part_floats(int nt, int waves = 4) {
+  return waves * kRows * nt * 2;
+}
 
 // One 16-row tile of one (or two: gate and up) expert matrices against NT
 // staged activation rows held in LDS (`xs`, row stride S words). Lane =
-// row slot * 4 + sub; the four wavefronts split the super-block columns
+// row slot * 4 + sub; the WAVES wavefronts split the super-block columns
 // and meet in LDS. `row0`/`row1` point at this lane's row of each matrix.
-// The first batch of quant loads can be issued (prefetch) before the
-// activations are in LDS, so the two memory latencies overlap.
-template <int Q, int NMAT, int NT, bool SPLIT>
+// A wavefront loads KU columns per batch (default: the format's batch, one
+// column for split activations); the first batch can be issued (prefetch)
+// before the activations are in LDS, so the two memory latencies overlap.
+// With WAVES * KU >= the column count every quant load of the tile is in
+// flight at once.
+template <int Q, int NMAT, int NT, bool SPLIT, int WAVES = 4, int KU = 0>
 struct TileDot {
   using F = Fmt<Q>;
-  // split activations double the LDS reads per field: keep one super-block in flight
-  static constexpr int kU = SPLIT ? 1 : F::kU;
+  static constexpr int kU = KU > 0 ? KU : (SPLIT ? 1 : F::kU);
   const uint8_t* row0;
   const uint8_t* row1;
   int K, bpr, wave, sub;
@@ -357,7 +361,7 @@ struct TileDot {
   __device__ __forceinline__ void load(int cb) {
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      const int col = cb + 4 * u;
+      const int col = cb + WAVES * u;
       if (col < bpr) {
         F::load(row0 + size_t(col) * F::kBytes, sub, raw[0][u]);
         if constexpr (NMAT == 2) F::load(row1 + size_t(col) * F::kBytes, sub, raw[1][u]);
@@ -374,11 +378,11 @@ struct TileDot {
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
       for (int t = 0; t < NT; ++t) acc[m][t] = 0.f;
-    for (int cb = wave; cb < bpr; cb += 4 * kU) {
+    for (int cb = wave; cb < bpr; cb += WAVES * kU) {
       if (cb != wave) load(cb);
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
-        const int col = cb + 4 * u;
+        const int col = cb + WAVES * u;
         if (col < bpr) {
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
@@ -399,14 +403,14 @@ struct TileDot {
         float v = acc[m][t];
         v += __shfl_xor(v, 1, kWave);
         v += __shfl_xor(v, 2, kWave);
-        if (sub == 0) part[((m * 4 + wave) * kRows + slot) * NT + t] = v;
+        if (sub == 0) part[((m * WAVES + wave) * kRows + slot) * NT + t] = v;
       }
     __syncthreads();
     if (tid < NMAT * kRows * NT) {
       const int m = tid / (kRows * NT), rest = tid % (kRows * NT);
       float v = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) v += part[(m * 4 + w) * kRows * NT + rest];
+      for (int w = 0; w < WAVES; ++w) v += part[(m * WAVES + w) * kRows * NT + rest];
       res[tid] = v;
     }
     __syncthreads();
@@ -414,27 +418,28 @@ struct TileDot {
 };
 
 // Copies n 16-byte words from global memory into LDS with every thread of
-// the 256-thread workgroup, DEPTH loads in flight per thread (loads clamped
+// a THREADS-thread workgroup, DEPTH loads in flight per thread (loads clamped
 // to the last word, stores guarded, so the batch stays in registers).
-template <int DEPTH = 4>
+template <int DEPTH = 4, int THREADS = 256>
 __device__ __forceinline__ void copy_to_lds(uint4* to, const uint4* from, int n) {
   const int tid = threadIdx.x;
-  for (int base = 0; base < n; base += 256 * DEPTH) {
+  for (int base = 0; base < n; base += THREADS * DEPTH) {
     uint4 v[DEPTH];
 #pragma unroll
-    for (int j = 0; j < DEPTH; ++j) v[j] = from[min(base + j * 256 + tid, n - 1)];
+    for (int j = 0; j < DEPTH; ++j) v[j] = from[min(base + j * THREADS + tid, n - 1)];
 #pragma unroll
     for (int j = 0; j < DEPTH; ++j)
-      if (base + j * 256 + tid < n) to[base + j * 256 + tid] = v[j];
+      if (base + j * THREADS + tid < n) to[base + j * THREADS + tid] = v[j];
   }
 }
 
 // Copies `nt` staged rows (S words each, S a multiple of 4) into LDS; src(t)
 // gives the row pointer.
-template <typename SrcFn>
+template <int THREADS = 256, typename SrcFn>
 __device__ __forceinline__ void copy_rows_to_lds(uint32_t* xs, int S, int nt, SrcFn src) {
   for (int t = 0; t < nt; ++t)
-    copy_to_lds(reinterpret_cast<uint4*>(xs + t * S), reinterpret_cast<const uint4*>(src(t)), S / 4);
+    copy_to_lds<4, THREADS>(reinterpret_cast<uint4*>(xs + t * S),
+                            reinterpret_cast<const uint4*>(src(t)), S / 4);
 }
 
 // Stages one 16-value run held one value per lane by lanes 0..15 of a
