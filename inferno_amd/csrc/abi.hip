@@ -474,7 +474,7 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
     d.residual = residual; d.out = out; d.ids = ids; d.weights = wts;
     d.partials = w.partials; d.stage_x = w.moe.stage_x; d.offsets = w.moe.offsets;
     d.sorted = w.moe.sorted; d.active = w.moe.active; d.stage_h = w.moe.stage_h;
-    d.stage_hs = w.stage_hs; d.ys = w.ys; d.slots = w.slots;
+    d.stage_hs = w.stage_hs; d.slots = w.slots;
     return launch_decode_layer(s, d, L->quant);
   }
   if ((st = launch_router_logits(s, x, x_dtype, L->router, T, H, E, w.logits))) return st;

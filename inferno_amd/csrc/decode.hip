@@ -23,7 +23,6 @@
 #include "dot2_formats.hpp"
 #include "routing_dev.hpp"
 
-#include <mutex>
 
 namespace inferno {
 namespace {
@@ -199,20 +198,16 @@ struct GateUpMaxKU {
                                : Q == INFERNO_Q4_K ? (SPLIT ? 2 : 4)
                                                    : (SPLIT ? 1 : 2);
 };
-template <int Q>
-struct DownMaxKU {
-  static constexpr int value = Q == INFERNO_Q2_K ? 16 : 8;
-};
 
+// One 16-row gate/up tile: routed (tile `item` of the active slots) or the
+// Q8_0 shared expert (tile `item` of its rows).
 template <int Q, bool XSPLIT, bool SHARED, int WAVES, int KU>
-__global__ void __launch_bounds__(64 * WAVES)
-    __attribute__((amdgpu_waves_per_eu(DecodeOcc<KU>::value, 8))) gate_up_kernel(DecodeArgs p) {
+__device__ __forceinline__ void gate_up_tile(const DecodeArgs& p, uint32_t item) {
   extern __shared__ uint32_t smem[];
   const int tid = threadIdx.x, slot = (tid & 63) >> 2;
   const int T = p.T, H = p.H, I = p.I, Is = p.Is, k = p.k;
   const int Sx = staged_stride(H, XSPLIT);
   const int tiles_i = I / kRows;
-  const uint32_t item = blockIdx.x;
   constexpr bool shared = SHARED;
   uint32_t lo = 0, hi = uint32_t(T), first = 0;
   int tile = int(item);
@@ -256,72 +251,16 @@ __global__ void __launch_bounds__(64 * WAVES)
   }
 }
 
-// Routed down with the combine folded in: one workgroup per (token, 16-row
-// output tile) runs through all k ranks' experts (the token's k staged h
-// rows sit in LDS), so the sum over ranks never leaves registers; then
-// out = residual + shared + routed. The four wavefronts take the
-// (rank, super-block column) pairs round robin and meet in LDS: a fixed
-// order, deterministic without float atomics.
-template <int Q, int WAVES, int KU>
-__global__ void __launch_bounds__(64 * WAVES)
-    __attribute__((amdgpu_waves_per_eu(DecodeOcc<KU>::value, 8))) down_sum_kernel(DecodeArgs p) {
-  using F = Fmt<Q>;
-  extern __shared__ uint32_t smem[];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int slot = lane >> 2, sub = lane & 3;
-  const int H = p.H, I = p.I, k = p.k;
-  const int tiles_h = H / kRows;
-  const int t = int(blockIdx.x) / tiles_h, tile = int(blockIdx.x) % tiles_h;
-  const int S = staged_stride(I, true);
-  uint32_t* xs = smem;                                   // k staged h rows
-  float* part = reinterpret_cast<float*>(smem + k * S);  // WAVES * kRows
-  const int bpr = I / kKBlock;
-  const size_t rb = size_t(bpr) * F::kBytes;
-  const uint8_t* wrow = p.down + size_t(tile * kRows + slot) * rb;
-  const uint32_t* ids = p.ids + size_t(t) * k;
-  const int nq = k * bpr;
-  constexpr int kU = KU;
-  uint32_t raw[kU][F::kDw];
-  // pairs q = wave + WAVES (u + kU i) -> rank q / bpr, column q % bpr
-  auto issue = [&](int q0) {
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int q = q0 + WAVES * u;
-      if (q < nq) {
-        const int r = q / bpr, col = q - r * bpr;
-        F::load(wrow + size_t(ids[r]) * p.down_stride + size_t(col) * F::kBytes, sub, raw[u]);
-      }
-    }
-  };
-  issue(wave);  // quant loads in flight while the h rows are copied
-  // the token's k assignments t*k .. t*k+k-1 are consecutive rows
-  copy_to_lds<8, 64 * WAVES>(reinterpret_cast<uint4*>(xs),
-              reinterpret_cast<const uint4*>(p.stage_h + size_t(t) * k * S), k * S / 4);
-  __syncthreads();
-  float acc = 0.f;
-  for (int q0 = wave; q0 < nq; q0 += WAVES * kU) {
-    if (q0 != wave) issue(q0);
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int q = q0 + WAVES * u;
-      if (q < nq) {
-        const int r = q / bpr, col = q - r * bpr;
-        acc += F::dot(raw[u], sub, xrow_at<true>(xs + r * S, I, col));
-      }
-    }
-  }
-  acc += __shfl_xor(acc, 1, kWave);
-  acc += __shfl_xor(acc, 2, kWave);
-  if (sub == 0) part[wave * kRows + slot] = acc;
-  __syncthreads();
-  if (tid < kRows) {
-    float v = 0.f;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) v += part[w * kRows + tid];
-    const size_t o = size_t(t) * H + size_t(tile) * kRows + tid;
-    p.out[o] = ((p.residual ? p.residual[o] : 0.f) + (p.Is ? p.ys[o] : 0.f)) + v;
-  }
+// gate/up launch: the routed tiles (first routed_tiles workgroups) and the
+// shared expert's tiles in one grid.
+template <int Q, bool XSPLIT, int KU>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DecodeOcc<KU>::value, 8)))
+    gate_up_kernel(DecodeArgs p) {
+  const uint32_t item = blockIdx.x;
+  if (item < uint32_t(p.routed_tiles))
+    gate_up_tile<Q, XSPLIT, false, 4, KU>(p, item);
+  else
+    gate_up_tile<INFERNO_Q8_0, XSPLIT, true, 4, 0>(p, item - uint32_t(p.routed_tiles));
 }
 
 // Routed down with the combine folded in, 8-row output tiles: workgroup =
@@ -334,8 +273,8 @@ __global__ void __launch_bounds__(64 * WAVES)
 // Lane groups meet in registers (cp) and LDS (wavefronts) in a fixed order;
 // out = (residual + shared) + routed, deterministic without float atomics.
 template <int Q, int KU>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8)))
-    down8_kernel(DecodeArgs p) {
+__global__ void __launch_bounds__(256)
+    __attribute__((amdgpu_waves_per_eu(Q == INFERNO_Q2_K ? 3 : 2, 8))) down8_kernel(DecodeArgs p) {
   using F = Fmt<Q>;
   extern __shared__ uint32_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -345,8 +284,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
   const int tiles_h = H / 8;
   const int t = int(blockIdx.x) / tiles_h, tile = int(blockIdx.x) % tiles_h;
   const int Ss = staged_stride(I, true), Sn = staged_stride(I, false);
-  uint32_t* xs = smem;                                    // k rows, non-split layout
-  float* part = reinterpret_cast<float*>(smem + k * Sn);  // 4 wavefronts x 8 rows
+  const int Sns = p.Is ? staged_stride(p.Is, false) : 0;
+  uint32_t* xs = smem;                  // k routed rows + the shared row, non-split layout
+  uint32_t* xss = smem + k * Sn;
+  float* part = reinterpret_cast<float*>(xss + Sns);  // [2][4 wavefronts][8 rows]
   const int bpr = I / kKBlock;
   const size_t rb = size_t(bpr) * F::kBytes;
   const uint8_t* wrow = p.down + size_t(tile * 8 + r) * rb;
@@ -365,6 +306,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
   };
   const int q_first = cp + 2 * wave;
   issue(q_first);  // quant loads in flight while the h rows are copied
+  // the shared expert: 8 rows of its down matrix against the token's shared
+  // h row, one Q8_0 unit (256 values) per lane group and step
+  using FS = Fmt<INFERNO_Q8_0>;
+  const int Is = p.Is, ubs = Is / kKBlock;
+  const uint8_t* srow =
+      Is ? p.sdown + size_t(tile * 8 + r) * size_t(ubs) * FS::kBytes : nullptr;
+  uint32_t sraw[FS::kDw];
+  if (Is && q_first < ubs) FS::load(srow + size_t(q_first) * FS::kBytes, sub, sraw);
   // staged h rows t*k .. t*k+k-1: copy the high pairs and the run sums/scales
   {
     const int hi4 = I / 8, tail4 = I / 32;  // uint4 words of the two parts
@@ -375,6 +324,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
       uint4* to = reinterpret_cast<uint4*>(xs + rank * Sn);
       // the high pairs are the first I/2 words, the sums/scales the last I/8
       to[w] = w < hi4 ? from[w] : from[w + hi4];
+    }
+    if (Is) {
+      const int shi4 = Is / 8, sper = shi4 + Is / 32;
+      const uint4* from =
+          reinterpret_cast<const uint4*>(p.stage_hs + size_t(t) * staged_stride(Is, true));
+      uint4* to = reinterpret_cast<uint4*>(xss);
+      for (int w = tid; w < sper; w += 256) to[w] = w < shi4 ? from[w] : from[w + shi4];
     }
   }
   __syncthreads();
@@ -390,132 +346,70 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8))
       }
     }
   }
+  float accs = 0.f;
+  for (int q = q_first; q < ubs; q += 8) {
+    if (q != q_first) FS::load(srow + size_t(q) * FS::kBytes, sub, sraw);
+    accs += FS::dot(sraw, sub, xrow_at<false>(xss, Is, q));
+  }
   acc += __shfl_xor(acc, 1, kWave);
   acc += __shfl_xor(acc, 2, kWave);
   acc += __shfl_xor(acc, 32, kWave);
-  if ((lane & 35) == 0) part[wave * 8 + r] = acc;  // sub == 0, cp == 0
+  accs += __shfl_xor(accs, 1, kWave);
+  accs += __shfl_xor(accs, 2, kWave);
+  accs += __shfl_xor(accs, 32, kWave);
+  if ((lane & 35) == 0) {  // sub == 0, cp == 0
+    part[wave * 8 + r] = acc;
+    part[32 + wave * 8 + r] = accs;
+  }
   __syncthreads();
   if (tid < 8) {
     const float v = ((part[tid] + part[8 + tid]) + part[16 + tid]) + part[24 + tid];
+    const float vs = ((part[32 + tid] + part[40 + tid]) + part[48 + tid]) + part[56 + tid];
     const size_t o = size_t(t) * H + size_t(tile) * 8 + tid;
-    p.out[o] = ((p.residual ? p.residual[o] : 0.f) + (p.Is ? p.ys[o] : 0.f)) + v;
+    p.out[o] = ((p.residual ? p.residual[o] : 0.f) + vs) + v;
   }
 }
 
-// Shared-expert down (Q8_0): one 16-row tile per workgroup, rows of ys.
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
-    shared_down_kernel(DecodeArgs p) {
-  extern __shared__ uint32_t smem[];
-  const int tid = threadIdx.x, slot = (tid & 63) >> 2;
-  const int T = p.T, H = p.H, Is = p.Is;
-  const int tile = int(blockIdx.x);
-  const int row = tile * kRows + slot;
-  const int S = staged_stride(Is, true);
-  uint32_t* xs = smem;
-  float* part = reinterpret_cast<float*>(smem + S);  // after the staged row
-  float* res = part + tile_part_floats(1);
-  const uint8_t* r0 = p.sdown + size_t(row) * size_t(Is / kKBlock) * Fmt<INFERNO_Q8_0>::kBytes;
-  TileDot<INFERNO_Q8_0, 1, 1, true> td(r0, nullptr, Is);
-  for (int c = 0; c < T; ++c) {
-    td.prefetch();
-    copy_rows_to_lds(xs, S, 1, [&](int) { return p.stage_hs + size_t(c) * S; });
-    __syncthreads();
-    td.run(xs, S, 1, part, res);
-    if (tid < kRows) p.ys[size_t(c) * H + tile * kRows + tid] = res[tid];
-    __syncthreads();
-  }
-}
-
-// Routed decode kernels: four wavefronts per 16-row tile, each with all of
-// its quant loads (KU columns) in flight at once; two workgroups per CU
-// overlap one's streaming with the other's arithmetic.
-constexpr int kDecodeWaves = 4;
-size_t down_sum_lds(int k, int I) {
-  return (size_t(k) * staged_stride(I, true) + kDecodeWaves * kRows) * 4;
+// Routed gate/up: four wavefronts per 16-row tile, each with its quant loads
+// for KU columns in flight at once.
+size_t gate_up_lds(int H, bool xsplit) {
+  return (size_t(staged_stride(H, xsplit)) + tile_part_floats(1) + 2 * kRows) * 4;
 }
 
 template <int Q, bool XSPLIT, int KU>
 void launch_gate_up_ku(hipStream_t s, const DecodeArgs& a) {
-  const size_t tiles = size_t(a.max_slots) * (a.I / kRows);
-  const size_t lds =
-      (size_t(staged_stride(a.H, XSPLIT)) + tile_part_floats(1, kDecodeWaves) + 2 * kRows) * 4;
-  gate_up_kernel<Q, XSPLIT, false, kDecodeWaves, KU>
-      <<<unsigned(tiles), 64 * kDecodeWaves, lds, s>>>(a);
+  const size_t tiles = size_t(a.routed_tiles) + (a.Is ? size_t(a.Is / kRows) : 0);
+  gate_up_kernel<Q, XSPLIT, KU><<<unsigned(tiles), 256, gate_up_lds(a.H, XSPLIT), s>>>(a);
 }
 
-// columns per wavefront: ceil(H / 256 / waves), capped by the format (a
-// longer row loops over batches)
+// columns per wavefront: ceil(H / 256 / 4), capped by the format (a longer
+// row loops over batches)
 template <int Q, bool XSPLIT>
 void launch_gate_up(hipStream_t s, const DecodeArgs& a) {
   constexpr int kMax = GateUpMaxKU<Q, XSPLIT>::value;
-  const int per = (a.H / kKBlock + kDecodeWaves - 1) / kDecodeWaves;
+  const int per = (a.H / kKBlock + 3) / 4;
   if (per <= 1 || kMax == 1) launch_gate_up_ku<Q, XSPLIT, 1>(s, a);
   else if (per <= 2 || kMax == 2) launch_gate_up_ku<Q, XSPLIT, (kMax < 2 ? kMax : 2)>(s, a);
   else if (per <= 4 || kMax == 4) launch_gate_up_ku<Q, XSPLIT, (kMax < 4 ? kMax : 4)>(s, a);
   else launch_gate_up_ku<Q, XSPLIT, kMax>(s, a);
 }
 
-size_t down8_lds(int k, int I) { return (size_t(k) * staged_stride(I, false) + 4 * 8) * 4; }
+size_t down8_lds(int k, int I, int Is) {
+  return (size_t(k) * staged_stride(I, false) + (Is ? size_t(staged_stride(Is, false)) : 0) +
+          2 * 4 * 8) * 4;
+}
 
 template <int Q>
-void launch_down_sum(hipStream_t s, const DecodeArgs& a) {
-  if (a.H % 8 == 0) {
-    const unsigned grid8 = unsigned(size_t(a.T) * (a.H / 8));
-    const int per8 = (a.k * (a.I / kKBlock) + 7) / 8;
-    // Q3_K holds four pairs per batch without spilling, the others eight
-    constexpr int kMax8 = Q == INFERNO_Q3_K ? 4 : 8;
-    if (per8 <= 4 || kMax8 == 4)
-      down8_kernel<Q, 4><<<grid8, 256, down8_lds(a.k, a.I), s>>>(a);
-    else
-      down8_kernel<Q, kMax8><<<grid8, 256, down8_lds(a.k, a.I), s>>>(a);
-    return;
-  }
-  const unsigned grid = unsigned(size_t(a.T) * (a.H / kRows));
-  const size_t lds = down_sum_lds(a.k, a.I);
-  constexpr int kMax = DownMaxKU<Q>::value;
-  const int per = (a.k * (a.I / kKBlock) + kDecodeWaves - 1) / kDecodeWaves;
-  if (per <= 8 || kMax == 8)
-    down_sum_kernel<Q, kDecodeWaves, 8><<<grid, 64 * kDecodeWaves, lds, s>>>(a);
+void launch_down(hipStream_t s, const DecodeArgs& a) {
+  const unsigned grid = unsigned(size_t(a.T) * (a.H / 8));
+  const size_t lds = down8_lds(a.k, a.I, a.Is);
+  const int per = (a.k * (a.I / kKBlock) + 7) / 8;
+  // Q3_K holds four pairs per batch without spilling, the others eight
+  constexpr int kMax8 = Q == INFERNO_Q3_K ? 4 : 8;
+  if (per <= 4 || kMax8 == 4)
+    down8_kernel<Q, 4><<<grid, 256, lds, s>>>(a);
   else
-    down_sum_kernel<Q, kDecodeWaves, kMax><<<grid, 64 * kDecodeWaves, lds, s>>>(a);
-}
-
-template <bool XSPLIT>
-int launch_shared(hipStream_t s, const DecodeArgs& a) {
-  const size_t gu_lds = (size_t(staged_stride(a.H, XSPLIT)) + tile_part_floats(1) + 2 * kRows) * 4;
-  gate_up_kernel<INFERNO_Q8_0, XSPLIT, true, 4, 0><<<unsigned(a.Is / kRows), 256, gu_lds, s>>>(a);
-  INF_LAUNCHED();
-  const size_t dn_lds = (size_t(staged_stride(a.Is, true)) + tile_part_floats(1) + 2 * kRows) * 4;
-  shared_down_kernel<<<unsigned(a.H / kRows), 256, dn_lds, s>>>(a);
-  INF_LAUNCHED();
-  return INFERNO_OK;
-}
-
-// Second stream per device for the shared expert, plus the two events of
-// the fork/join. Created once, default priority, never destroyed.
-struct SideStream {
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-};
-
-int side_stream(SideStream** out) {
-  static std::mutex mu;
-  static SideStream per_device[64];
-  int dev = 0;
-  INF_HIP(hipGetDevice(&dev));
-  if (dev < 0 || dev >= 64) {
-    set_error("device index out of range");
-    return INFERNO_ERR_DEVICE;
-  }
-  std::lock_guard<std::mutex> lock(mu);
-  SideStream& ss = per_device[dev];
-  if (!ss.stream) {
-    INF_HIP(hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking));
-    INF_HIP(hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming));
-    INF_HIP(hipEventCreateWithFlags(&ss.join, hipEventDisableTiming));
-  }
-  *out = &ss;
-  return INFERNO_OK;
+    down8_kernel<Q, kMax8><<<grid, 256, lds, s>>>(a);
 }
 
 }  // namespace
@@ -527,10 +421,8 @@ bool decode_supported(size_t T, size_t k, size_t E, size_t H, size_t I, size_t I
         (quant == INFERNO_Q2_K || quant == INFERNO_Q3_K || quant == INFERNO_Q4_K)))
     return false;
   const size_t kLds = 160 * 1024;
-  const size_t tile_extra = size_t(tile_part_floats(1, kDecodeWaves) + 2 * kRows) * 4;
-  const size_t gate_up = size_t(staged_stride(int(H), x_dtype == INFERNO_F32)) * 4 + tile_extra;
-  const size_t shared_down = Is ? size_t(staged_stride(int(Is), true)) * 4 + tile_extra : 0;
-  return gate_up <= kLds && shared_down <= kLds && down_sum_lds(int(k), int(I)) + 64 <= kLds;
+  return gate_up_lds(int(H), x_dtype == INFERNO_F32) <= kLds &&
+         down8_lds(int(k), int(I), int(Is)) <= kLds;
 }
 
 int decode_chunk(size_t H) {
@@ -562,23 +454,15 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
       route_kernel<uint16_t><<<grid, 256, 0, s>>>(a);
     INF_LAUNCHED();
   }
-  // the shared expert only needs the staged x: fork it onto the side stream
-  SideStream* side = nullptr;
-  int st;
-  if (a.Is) {
-    if ((st = side_stream(&side))) return st;
-    INF_HIP(hipEventRecord(side->fork, s));
-    INF_HIP(hipStreamWaitEvent(side->stream, side->fork, 0));
-    if ((st = xsplit ? launch_shared<true>(side->stream, a) : launch_shared<false>(side->stream, a)))
-      return st;
-    INF_HIP(hipEventRecord(side->join, side->stream));
-  }
   if (a.T == 1)
     select1_kernel<<<1, 256, 0, s>>>(a);
   else
     select_kernel<<<1, 1024, 0, s>>>(a);
   INF_LAUNCHED();
-  st = timed(s, kTimerGateUp, [&] {
+  // routed and shared gate/up in one grid, then the routed down with the
+  // shared down and the residual folded in: one stream, no events
+  a.routed_tiles = a.max_slots * (a.I / kRows);
+  int st = timed(s, kTimerGateUp, [&] {
     switch (quant) {
       case INFERNO_Q2_K: xsplit ? launch_gate_up<INFERNO_Q2_K, true>(s, a) : launch_gate_up<INFERNO_Q2_K, false>(s, a); break;
       case INFERNO_Q3_K: xsplit ? launch_gate_up<INFERNO_Q3_K, true>(s, a) : launch_gate_up<INFERNO_Q3_K, false>(s, a); break;
@@ -588,13 +472,11 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
     return INFERNO_OK;
   });
   if (st) return st;
-  // the combined down pass adds the shared expert's rows
-  if (a.Is) INF_HIP(hipStreamWaitEvent(s, side->join, 0));
   return timed(s, kTimerDown, [&] {
     switch (quant) {
-      case INFERNO_Q2_K: launch_down_sum<INFERNO_Q2_K>(s, a); break;
-      case INFERNO_Q3_K: launch_down_sum<INFERNO_Q3_K>(s, a); break;
-      default: launch_down_sum<INFERNO_Q4_K>(s, a); break;
+      case INFERNO_Q2_K: launch_down<INFERNO_Q2_K>(s, a); break;
+      case INFERNO_Q3_K: launch_down<INFERNO_Q3_K>(s, a); break;
+      default: launch_down<INFERNO_Q4_K>(s, a); break;
     }
     INF_LAUNCHED();
     return INFERNO_OK;

@@ -35,9 +35,8 @@ struct DecodeArgs {
   uint4* slots;           // [E] per active slot: expert, lo, hi, first assignment
   uint32_t* stage_h;      // [T*k, staged_stride(I, true)]
   uint32_t* stage_hs;     // [T, staged_stride(Is, true)]
-  float* ys;              // [T, H]
   // filled by launch_decode_layer
-  int chunk, n_chunks, max_slots;
+  int chunk, n_chunks, max_slots, routed_tiles;
 };
 
 // True when the fused path covers the layer (token count, format and LDS fit).
