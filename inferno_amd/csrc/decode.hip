@@ -1,17 +1,17 @@
-// Fused decode path of one MoE layer (T <= 64 tokens), five launches on the
-// layer's stream plus two on a side stream:
+// Fused decode path of one MoE layer (T <= 64 tokens), four launches on the
+// layer's stream, no events:
 //
 //   route    router logits as per-chunk partial sums (H split over many
 //            workgroups) + staging of x into packed-f16 runs;
 //   select   logits = ordered sum of the partials, exact top-k per token
 //            (one wavefront each), stable dispatch (one wavefront for T = 1);
-//   gate/up  routed 16-row tiles, writing the SwiGLU intermediate already
-//            staged for the down pass;
-//   down     routed 16-row tiles, one output row per assignment;
-//   combine  out = residual + shared + sum over ranks in rank order,
+//   gate/up  routed and Q8_0 shared-expert 16-row tiles in one grid, writing
+//            the SwiGLU intermediate already staged for the down pass (an
+//            opt-in alternative for one token streams the tiles through an
+//            LDS ring, decode_ring.hpp);
+//   down     8-row output tiles over all ranks plus the shared expert, with
+//            out = (residual + shared) + routed summed in a fixed order,
 //            deterministic without float atomics.
-// The Q8_0 shared expert (gate/up + down) only needs the staged x and runs
-// on the side stream between route and combine.
 //
 // Reference semantics: crates/model/src/laguna/gguf_model.rs:731-860 (layer
 // order), gguf_moe_kernels.metal:340-565 (routed SwiGLU with the routing
@@ -19,6 +19,9 @@
 // (shared expert plus two residual adds), moe_kernels.metal:210-238 (rank
 // order combine).
 #include "decode.hpp"
+#include "decode_ring.hpp"
+
+#include <cstdlib>
 #include "timing.hpp"
 #include "dot2_formats.hpp"
 #include "routing_dev.hpp"
@@ -412,6 +415,86 @@ void launch_down(hipStream_t s, const DecodeArgs& a) {
     down8_kernel<Q, kMax8><<<grid, 256, lds, s>>>(a);
 }
 
+// One-token gate/up through the LDS ring (decode_ring.hpp): opt-in with
+// INFERNO_DECODE_RING=1. It measures level with the tile grid on the GLM
+// decode layer (both about 33 us for the routed + shared gate/up), so the
+// grid stays the default; the plan returns false outside what the ring
+// kernel covers (then the tile grid runs).
+bool ring_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("INFERNO_DECODE_RING");
+    return v && v[0] == '1';
+  }();
+  return on;
+}
+
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus[dev] = 0;
+  return cus[dev];
+}
+
+bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
+
+bool ring_plan(const DecodeArgs& a, int quant, ring::RingPlan& pl, unsigned& grid, size_t& lds,
+               int& pw) {
+  if (!ring_enabled() || a.T != 1 || a.x_dtype == INFERNO_F32 || quant != INFERNO_Q2_K) return false;
+  const int nsb = a.H / kKBlock;
+  if (a.I % kRows || a.Is % kRows) return false;
+  if (!ring::ring_shape_q2k(nsb, pl.routed)) return false;
+  if (a.Is) {
+    if (!ring::ring_shape_q8(nsb, pl.shared)) return false;
+  } else {
+    pl.shared = pl.routed;
+  }
+  if (!aligned16(a.gate) || !aligned16(a.up) || !aligned16(a.stage_x) ||
+      (a.Is && (!aligned16(a.sgate) || !aligned16(a.sup))))
+    return false;
+  pl.tiles_i = a.I / kRows;
+  pl.S = a.Is / kRows;
+  pl.R = a.k * pl.tiles_i;
+  pl.x_bytes = uint32_t(staged_stride(a.H, false)) * 4;
+  pl.x_pieces = int((pl.x_bytes + 1023) / 1024);
+  const int pieces = std::max(pl.routed.pieces, a.Is ? pl.shared.pieces : 0);
+  pw = (pieces + ring::kDmaWaves - 1) / ring::kDmaWaves;
+  if (pw < 4 || pw > 6) return false;
+  const int cus = device_cus();
+  if (cus <= 0) return false;
+  grid = unsigned(2 * cus);
+  if (int(grid) <= pl.S) return false;
+  lds = size_t(pl.x_pieces) * 1024 + ring::kPartFloats * 4 + size_t(ring::kDepth) * ring::kSlotBytes;
+  return lds <= 160 * 1024;
+}
+
+template <int PW>
+int launch_gate_up_ring_pw(hipStream_t s, const DecodeArgs& a, const ring::RingPlan& pl,
+                           unsigned grid, size_t lds) {
+  static bool attr = false;
+  if (!attr) {
+    if (hipFuncSetAttribute((const void*)ring::gate_up_ring_kernel<PW>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
+      set_error("gate/up ring kernel: cannot raise its LDS limit");
+      return INFERNO_ERR_DEVICE;
+    }
+    attr = true;
+  }
+  ring::gate_up_ring_kernel<PW><<<grid, 256, lds, s>>>(a, pl);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+int launch_gate_up_ring(hipStream_t s, const DecodeArgs& a, const ring::RingPlan& pl,
+                        unsigned grid, size_t lds, int pw) {
+  switch (pw) {
+    case 4: return launch_gate_up_ring_pw<4>(s, a, pl, grid, lds);
+    case 5: return launch_gate_up_ring_pw<5>(s, a, pl, grid, lds);
+    default: return launch_gate_up_ring_pw<6>(s, a, pl, grid, lds);
+  }
+}
+
 }  // namespace
 
 bool decode_supported(size_t T, size_t k, size_t E, size_t H, size_t I, size_t Is, int x_dtype,
@@ -462,7 +545,13 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   // routed and shared gate/up in one grid, then the routed down with the
   // shared down and the residual folded in: one stream, no events
   a.routed_tiles = a.max_slots * (a.I / kRows);
-  int st = timed(s, kTimerGateUp, [&] {
+  ring::RingPlan pl;
+  unsigned ring_grid = 0;
+  size_t ring_lds = 0;
+  int ring_pw = 0;
+  const bool use_ring = ring_plan(a, quant, pl, ring_grid, ring_lds, ring_pw);
+  int st = timed(s, kTimerGateUp, [&]() -> int {
+    if (use_ring) return launch_gate_up_ring(s, a, pl, ring_grid, ring_lds, ring_pw);
     switch (quant) {
       case INFERNO_Q2_K: xsplit ? launch_gate_up<INFERNO_Q2_K, true>(s, a) : launch_gate_up<INFERNO_Q2_K, false>(s, a); break;
       case INFERNO_Q3_K: xsplit ? launch_gate_up<INFERNO_Q3_K, true>(s, a) : launch_gate_up<INFERNO_Q3_K, false>(s, a); break;

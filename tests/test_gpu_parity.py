@@ -353,3 +353,17 @@ def test_layer_c4_laguna_q2k_q3k_layers(cuda, T):
         err = rn.rel_l2(ph.to_np(out)[toks], ref)
         print(f"c4 layer {layer} T={T}: rel_l2={err:.3e} near-tie tokens={flips}")
         assert err < ph.TOL_REL_L2
+
+
+def test_layer_decode_ring_opt_in(cuda):
+    """The opt-in LDS-ring gate/up (INFERNO_DECODE_RING=1) in a child process."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    env = dict(os.environ, INFERNO_DECODE_RING="1")
+    script = Path(__file__).resolve().parent / "ring_decode_check.py"
+    r = subprocess.run([sys.executable, "-u", str(script)], env=env, capture_output=True,
+                       text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and "ring ok" in r.stdout
