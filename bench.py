@@ -111,12 +111,14 @@ def main():
     ms_per_step = 1e3 * elapsed / args.steps
     tokens_per_s = T * args.steps / elapsed
 
-    # ---- dominant kernel: the routed gate/up launch -------------------------
+    # ---- dominant kernel: the gate/up launch --------------------------------
     # Same layer steps again with the event hook on: the C library brackets
-    # the routed gate/up launch (and the routed down launch) with HIP events
-    # on the layer's stream. Decode: algorithmic bytes per launch = quantised
-    # gate+up bytes of the step's unique selected experts. Prefill: flops per
-    # launch = 2 * (2 * H * I) * assignments.
+    # the gate/up launch (and the down launch) with HIP events on the layer's
+    # stream. Decode: one gate/up grid covers the routed tiles and the Q8_0
+    # shared expert's tiles, so algorithmic bytes per launch = quantised
+    # gate+up bytes of the step's unique selected experts + the shared gate+up
+    # bytes (the down launch likewise carries the shared down). Prefill: flops
+    # per launch = 2 * (2 * H * I) * assignments (routed only).
     q = cfg.quants[0]
     bb = ops.block_bytes(q)
     gu_bytes_per_expert = 2 * I * (H // 256) * bb
@@ -150,16 +152,23 @@ def main():
     router_bytes = E * H * 4
     extra = {}
     if not prefill:
-        gu_bytes = gu_bytes_per_expert * uniq_layer
+        shared_gu = 2 * cfg.shared_intermediate * (H // 32) * 34
+        shared_dn = cfg.shared_intermediate * (H // 32) * 34
+        gu_bytes = gu_bytes_per_expert * uniq_layer + shared_gu
+        dn_bytes = dn_bytes_per_expert * uniq_layer + shared_dn
         gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
-        dn_gbs = dn_bytes_per_expert * uniq_layer / (dn_us * 1e-6) / 1e9
+        dn_gbs = dn_bytes / (dn_us * 1e-6) / 1e9
         traffic = read_traffic(ROOT / "profiles" / "gate_up_q2k_c2_decode_traffic.txt")
-        roofline = {"bound": "hbm", "kernel": "gate_up_kernel<Q2_K, bf16, routed> (decode.hip)",
+        roofline = {"bound": "hbm",
+                    "kernel": "gate_up_kernel<Q2_K, bf16, KU=6>: routed + Q8_0 shared tiles (decode.hip)",
                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                    "launch_us": round(gu_us, 3), "bytes_per_launch": int(gu_bytes)}
-        extra["down_kernel"] = {"kernel": "down_sum_kernel (decode.hip)",
-                                "launch_us": round(dn_us, 3), "GBps": round(dn_gbs, 1)}
+                    "launch_us": round(gu_us, 3), "bytes_per_launch": int(gu_bytes),
+                    "routed_bytes_per_launch": int(gu_bytes_per_expert * uniq_layer),
+                    "shared_bytes_per_launch": int(shared_gu)}
+        extra["down_kernel"] = {"kernel": "down8_kernel<Q2_K>: routed + Q8_0 shared + combine (decode.hip)",
+                                "launch_us": round(dn_us, 3), "bytes_per_launch": int(dn_bytes),
+                                "GBps": round(dn_gbs, 1)}
     else:
         A = T * k
         gu_flops = 4.0 * H * I * A

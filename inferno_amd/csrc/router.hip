@@ -5,8 +5,9 @@
 // f32::total_cmp descending with the lower expert id winning ties; weights
 // are the unbiased scores in rank order, renormalised by their rank-order
 // sum, times the routed scaling factor. One wavefront per token; every lane
-// holds up to four candidates and each round is a 64-bit max-reduction of
-// (order-preserving score bits, ~expert id).
+// holds up to four candidates and each round is a DPP wavefront max of the
+// order-preserving key, then of ~expert id among the lanes holding that key
+// (routing_dev.hpp).
 #include "routing_dev.hpp"
 
 namespace inferno {
