@@ -111,23 +111,27 @@ def main():
     ms_per_step = 1e3 * elapsed / args.steps
     tokens_per_s = T * args.steps / elapsed
 
-    # ---- dominant kernel: the gate/up launch --------------------------------
+    # ---- per-kernel times and the dominant kernel ----------------------------
     # Same layer steps again with the event hook on: the C library brackets
-    # the gate/up launch (and the down launch) with HIP events on the layer's
-    # stream. Decode: one gate/up grid covers the routed tiles and the Q8_0
-    # shared expert's tiles, so algorithmic bytes per launch = quantised
-    # gate+up bytes of the step's unique selected experts + the shared gate+up
-    # bytes (the down launch likewise carries the shared down). Prefill: flops
-    # per launch = 2 * (2 * H * I) * assignments (routed only).
+    # each launch of the layer with HIP events on the layer's stream and
+    # labels what the launch covered. Decode: the routed gate/up launch streams
+    # the gate+up bytes of the step's unique selected experts, plus the Q8_0
+    # shared expert's gate+up when the label kind is "tiles"/"ring" (on the
+    # "mfma" path the shared gate/up runs in the route launch instead, label
+    # kind "route+shared"); the down launch streams the routed down bytes plus
+    # the shared down. Prefill: flops per launch = 2 * (2 * H * I) *
+    # assignments (routed only).
     q = cfg.quants[0]
     bb = ops.block_bytes(q)
     gu_bytes_per_expert = 2 * I * (H // 256) * bb
     dn_bytes_per_expert = H * (I // 256) * bb
     reps = max(args.steps, 64) if not prefill else max(args.steps, 10)
+    timers = [ops.TIMER_GATE_UP, ops.TIMER_DOWN] + ([] if prefill else
+                                                   [ops.TIMER_ROUTE, ops.TIMER_SELECT])
     ops.kernel_timing(True)
     try:
-        ops.kernel_timing_read(ops.TIMER_GATE_UP)
-        ops.kernel_timing_read(ops.TIMER_DOWN)
+        for tm in timers:
+            ops.kernel_timing_read(tm)
         uniq = 0
         loads = []
         for i in range(reps):
@@ -137,15 +141,16 @@ def main():
             if prefill and i < L:
                 loads.append(torch.bincount(ids_buf[l].long(), minlength=E).cpu())
         torch.cuda.synchronize()
-        gu_ms, gu_n = ops.kernel_timing_read(ops.TIMER_GATE_UP)
-        dn_ms, dn_n = ops.kernel_timing_read(ops.TIMER_DOWN)
+        timed = {tm: ops.kernel_timing_read(tm) for tm in timers}
+        labels = {tm: ops.kernel_timing_label(tm) for tm in timers}
     finally:
         ops.kernel_timing(False)
-    if gu_n != reps or dn_n != reps:
-        raise RuntimeError(f"kernel timers saw {gu_n}/{dn_n} launches for {reps} layer steps")
+    for tm in timers:
+        if timed[tm][1] != reps:
+            raise RuntimeError(f"kernel timer {tm} saw {timed[tm][1]} launches for {reps} steps")
+    us = {tm: 1e3 * timed[tm][0] / timed[tm][1] for tm in timers}
+    gu_us, dn_us = us[ops.TIMER_GATE_UP], us[ops.TIMER_DOWN]
     uniq_layer = uniq / reps
-    gu_us = 1e3 * gu_ms / gu_n
-    dn_us = 1e3 * dn_ms / dn_n
     layer_us = ms_per_step * 1e3
     layer_routed_bytes = (gu_bytes_per_expert + dn_bytes_per_expert) * uniq_layer
     shared_bytes = 3 * cfg.shared_intermediate * (H // 32) * 34 if cfg.shared_intermediate else 0
@@ -154,27 +159,52 @@ def main():
     if not prefill:
         shared_gu = 2 * cfg.shared_intermediate * (H // 32) * 34
         shared_dn = cfg.shared_intermediate * (H // 32) * 34
-        gu_bytes = gu_bytes_per_expert * uniq_layer + shared_gu
-        dn_bytes = dn_bytes_per_expert * uniq_layer + shared_dn
-        gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
-        dn_gbs = dn_bytes / (dn_us * 1e-6) / 1e9
-        traffic = read_traffic(ROOT / "profiles" / "gate_up_q2k_c2_decode_traffic.txt")
-        roofline = {"bound": "hbm",
-                    "kernel": "gate_up_kernel<Q2_K, bf16, KU=6>: routed + Q8_0 shared tiles (decode.hip)",
-                    "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                    "launch_us": round(gu_us, 3), "bytes_per_launch": int(gu_bytes),
-                    "routed_bytes_per_launch": int(gu_bytes_per_expert * uniq_layer),
-                    "shared_bytes_per_launch": int(shared_gu)}
-        extra["down_kernel"] = {"kernel": "down8_kernel<Q2_K>: routed + Q8_0 shared + combine (decode.hip)",
-                                "launch_us": round(dn_us, 3), "bytes_per_launch": int(dn_bytes),
-                                "GBps": round(dn_gbs, 1)}
+        gu_kind = labels[ops.TIMER_GATE_UP].split(":")[0]
+        rt_kind = labels[ops.TIMER_ROUTE].split(":")[0]
+        gu_routed = gu_bytes_per_expert * uniq_layer
+        kernels = {
+            "route": {"label": labels[ops.TIMER_ROUTE], "launch_us": us[ops.TIMER_ROUTE],
+                      "bytes_per_launch": router_bytes + (shared_gu if rt_kind == "route+shared" else 0)},
+            "select": {"label": labels[ops.TIMER_SELECT], "launch_us": us[ops.TIMER_SELECT],
+                       "bytes_per_launch": None},
+            "gate_up": {"label": labels[ops.TIMER_GATE_UP], "launch_us": gu_us,
+                        "bytes_per_launch": gu_routed + (shared_gu if gu_kind in ("tiles", "ring") else 0),
+                        "routed_bytes_per_launch": gu_routed,
+                        "traffic_file": {"mfma": "gate_up_mfma_q2k_c2_decode_traffic.txt",
+                                         "tiles": "gate_up_q2k_c2_decode_traffic.txt"}.get(gu_kind)},
+            "down": {"label": labels[ops.TIMER_DOWN], "launch_us": dn_us,
+                     "bytes_per_launch": dn_bytes_per_expert * uniq_layer + shared_dn,
+                     "routed_bytes_per_launch": dn_bytes_per_expert * uniq_layer,
+                     "traffic_file": "down8_q2k_c2_decode_traffic.txt"},
+        }
+        for kd in kernels.values():
+            b = kd["bytes_per_launch"]
+            kd["launch_us"] = round(kd["launch_us"], 3)
+            kd["GBps"] = round(b / (kd["launch_us"] * 1e-6) / 1e9, 1) if b else None
+            if b:
+                kd["bytes_per_launch"] = int(b)
+            if "routed_bytes_per_launch" in kd:
+                kd["routed_bytes_per_launch"] = int(kd["routed_bytes_per_launch"])
+        # the dominant kernel: the longer of the two expert-streaming launches
+        dom = max(("gate_up", "down"), key=lambda n: kernels[n]["launch_us"])
+        kd = kernels[dom]
+        tf = kd.pop("traffic_file", None)
+        for other in kernels.values():
+            other.pop("traffic_file", None)
+        traffic = read_traffic(ROOT / "profiles" / tf, kd["label"].split(":")[1].split("(")[0].strip()) \
+            if tf and cfg.name.startswith("c2_") else None
+        roofline = {"bound": "hbm", "kernel": kd["label"], "achieved": kd["GBps"],
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(kd["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                    "launch_us": kd["launch_us"], "bytes_per_launch": kd["bytes_per_launch"],
+                    "routed_bytes_per_launch": kd["routed_bytes_per_launch"]}
+        extra["kernels"] = kernels
     else:
         A = T * k
         gu_flops = 4.0 * H * I * A
         gu_tfs = gu_flops / (gu_us * 1e-6) / 1e12
         dn_tfs = 2.0 * H * I * A / (dn_us * 1e-6) / 1e12
-        roofline = {"bound": "mfma", "kernel": "routed gate/up launch (prefill)",
+        roofline = {"bound": "mfma", "kernel": labels[ops.TIMER_GATE_UP],
                     "achieved": round(gu_tfs, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(gu_tfs / MFMA_BF16_PEAK_TFLOPS, 4),
                     "traffic": None, "launch_us": round(gu_us, 3),
@@ -235,15 +265,20 @@ def calibrate_copy():
     print(json.dumps({"calibrate_copy_bytes": n, "launches": 10}), flush=True)
 
 
-def read_traffic(path):
+def read_traffic(path, kernel):
     """HBM bytes per launch of the roofline kernel, from the committed
-    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (null when absent)."""
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary; null when the file is absent or
+    was measured on another kernel (its "kernel:" line must name `kernel`)."""
     try:
-        for line in Path(path).read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(float(line.split(":", 1)[1]))
+        text = Path(path).read_text().splitlines()
     except OSError:
-        pass
+        return None
+    named = [l.split(":", 1)[1].strip() for l in text if l.startswith("kernel:")]
+    if not named or named[0] != kernel:
+        return None
+    for line in text:
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
     return None
 
 

@@ -253,11 +253,20 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* layer, cons
  * library waits for the second event and adds the elapsed time to a
  * process-wide accumulator. The wait serialises the host with the layer:
  * leave timing off outside measurement. */
-enum { INFERNO_TIMER_GATE_UP = 0, INFERNO_TIMER_DOWN = 1 };
+enum {
+  INFERNO_TIMER_GATE_UP = 0,
+  INFERNO_TIMER_DOWN = 1,
+  INFERNO_TIMER_ROUTE = 2,  /* fused decode: router partials (+ shared gate/up) */
+  INFERNO_TIMER_SELECT = 3  /* fused decode: top-k + dispatch */
+};
 int inferno_kernel_timing_enable(int enable);
 /* Returns the accumulated milliseconds and launch count of one timer and
  * resets it. */
 int inferno_kernel_timing_read(int which, double* total_ms, uint64_t* launches);
+/* Copies (NUL-terminated, truncated to len) the label of the last launch a
+ * timer measured: "<kind>: <kernel> (<what it streams>)", kind one of
+ * mfma, tiles, ring, route, route+shared, select, down8, prefill, stage. */
+int inferno_kernel_timing_label(int which, char* buf, size_t len);
 
 /* -------------------------------------------------------- synthetic data */
 

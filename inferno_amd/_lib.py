@@ -38,6 +38,7 @@ SIGNATURES = {
     "inferno_stream_synchronize": (_i, [_vp]),
     "inferno_kernel_timing_enable": (_i, [_i]),
     "inferno_kernel_timing_read": (_i, [_i, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
+    "inferno_kernel_timing_label": (_i, [_i, C.c_char_p, C.c_size_t]),
     "inferno_gguf_dequantize": (_i, [_vp, _i, _vp, _sz, _vp]),
     "inferno_router_logits": (_i, [_vp, _vp, _i, _vp, _sz, _sz, _sz, _vp]),
     "inferno_moe_router_topk": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, _i, _i, _f, _vp, _vp, _vp]),

@@ -130,19 +130,22 @@ int run_routed(hipStream_t s, int quant, int down_quant, const void* gate, const
     }
     PrefillRouted p{quant, down_quant, gate, up, down, x16, m.offsets, m.sorted, m.active, w,
                     T, k, E, H, I, reinterpret_cast<uint16_t*>(m.h), m.y, m.plan};
-    if ((st = timed(s, kTimerGateUp, [&] { return launch_prefill_gate_up(s, p); }))) return st;
-    return timed(s, kTimerDown, [&] { return launch_prefill_down(s, p); });
+    if ((st = timed(s, kTimerGateUp, "prefill: gemm_kernel (routed gate/up, MFMA)",
+                    [&] { return launch_prefill_gate_up(s, p); })))
+      return st;
+    return timed(s, kTimerDown, "prefill: gemm_kernel (routed down, MFMA)",
+                 [&] { return launch_prefill_down(s, p); });
   }
   // gate/up writes h already staged for the down pass (when the down kind has a
   // packed-f16 kernel; Q6_K reads the fp32 h)
   const bool h_staged = dot2_supported(down_quant);
-  if ((st = timed(s, kTimerGateUp, [&] {
+  if ((st = timed(s, kTimerGateUp, "stage: routed gate/up GEMV", [&] {
          return launch_gemv_gate_up_routed(s, quant, gate, up, x, x_dtype, m.stage_x, x_staged,
                                            m.offsets, m.sorted, m.active, w, T, k, E, H, I, m.h,
                                            h_staged ? m.stage_h : nullptr);
        })))
     return st;
-  return timed(s, kTimerDown, [&] {
+  return timed(s, kTimerDown, "stage: routed down GEMV", [&] {
     return launch_gemv_down_routed(s, down_quant, down, m.h, m.stage_h, h_staged, m.offsets,
                                    m.sorted, m.active, T, k, E, H, I, m.y);
   });
@@ -178,6 +181,20 @@ int inferno_kernel_timing_read(int which, double* total_ms, uint64_t* launches) 
   clear_error();
   INF_CHECK_ARG(total_ms && launches, "null output pointer");
   INF_CHECK_ARG(kernel_timing_read(which, total_ms, launches), "unknown timer");
+  return INFERNO_OK;
+}
+
+int inferno_kernel_timing_label(int which, char* buf, size_t len) {
+  clear_error();
+  INF_CHECK_ARG(which >= 0 && which < kNumTimers, "unknown timer");
+  INF_CHECK_ARG(buf && len > 0, "null buffer");
+  const char* l = kernel_timing_label(which);
+  size_t n = 0;
+  while (l[n] && n + 1 < len) {
+    buf[n] = l[n];
+    ++n;
+  }
+  buf[n] = '\0';
   return INFERNO_OK;
 }
 
@@ -399,6 +416,8 @@ struct LayerScratch {
   float* partials;
   float* ys;
   uint4* slots;
+  uint32_t* stage_xm;
+  float* shared_gu;
 };
 LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   LayerScratch s;
@@ -411,6 +430,10 @@ LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   s.partials = c.take<float>(size_t(L->hidden / decode_chunk(L->hidden)) * T * L->experts);
   s.ys = c.take<float>(T * L->hidden);
   s.slots = c.take<uint4>(L->experts);
+  s.stage_xm = c.take<uint32_t>(T * decode_mfma_stage_words(L->hidden));
+  s.shared_gu = c.take<float>(L->shared_intermediate
+                                  ? decode_shared_partial_floats(L->hidden, L->shared_intermediate)
+                                  : 1);
   return s;
 }
 }  // namespace
@@ -474,7 +497,8 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
     d.residual = residual; d.out = out; d.ids = ids; d.weights = wts;
     d.partials = w.partials; d.stage_x = w.moe.stage_x; d.offsets = w.moe.offsets;
     d.sorted = w.moe.sorted; d.active = w.moe.active; d.stage_h = w.moe.stage_h;
-    d.stage_hs = w.stage_hs; d.slots = w.slots;
+    d.stage_hs = w.stage_hs; d.slots = w.slots; d.stage_xm = w.stage_xm;
+    d.shared_gu = w.shared_gu;
     return launch_decode_layer(s, d, L->quant);
   }
   if ((st = launch_router_logits(s, x, x_dtype, L->router, T, H, E, w.logits))) return st;

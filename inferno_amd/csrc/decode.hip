@@ -20,6 +20,7 @@
 // order combine).
 #include "decode.hpp"
 #include "decode_ring.hpp"
+#include "decode_mfma.hpp"
 
 #include <cstdlib>
 #include "timing.hpp"
@@ -34,13 +35,59 @@ constexpr int kMaxDecodeTokens = 64;
 
 // ------------------------------------------------------------------ route
 
+// Part `part` of the Q8_0 shared expert's gate/up tile `tile` (super-block
+// columns [part * cp, part * cp + cp), cp = H / 256 / shared_parts) for the
+// one token of the MFMA path, run by a workgroup of the route launch (it
+// does not depend on the routing): that slice of x is staged into this
+// workgroup's LDS, the packed-f16 tile kernel runs over it, and the 16
+// gate and up partial sums go to shared_gu (summed in a fixed order by the
+// MFMA gate/up kernel).
 template <typename XT>
-__global__ void __launch_bounds__(256) route_kernel(DecodeArgs p) {
+__device__ __forceinline__ void shared_gate_up_part(const DecodeArgs& p, int item) {
+  extern __shared__ uint32_t smem[];
+  constexpr bool kSplit = !std::is_same<XT, uint16_t>::value;
+  const int tid = threadIdx.x, slot = (tid & 63) >> 2;
+  const int H = p.H, Is = p.Is, parts = p.shared_parts;
+  const int tile = item / parts, part = item % parts;
+  const int Kp = H / parts, c0 = part * (Kp / kKBlock);
+  const int Sx = staged_stride(Kp, kSplit);
+  const size_t rb = size_t(H / kKBlock) * Fmt<INFERNO_Q8_0>::kBytes;
+  const size_t off = size_t(tile * kRows + slot) * rb + size_t(c0) * Fmt<INFERNO_Q8_0>::kBytes;
+  uint32_t* xs = smem;
+  float* part_l = reinterpret_cast<float*>(smem + Sx);
+  float* res = part_l + tile_part_floats(1, 4);
+  TileDot<INFERNO_Q8_0, 2, 1, kSplit, 4, 0> td(p.sgate + off, p.sup + off, Kp);
+  td.prefetch();  // quant loads in flight while x is staged
+  for (int run = tid; run < Kp / 16; run += 256) {
+    const XT* src = static_cast<const XT*>(p.x) + size_t(c0) * kKBlock + run * 16;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = to_f32(src[i]);
+    stage_run<kSplit>(v, xs, Kp, run);
+  }
+  __syncthreads();
+  td.run(xs, Sx, 1, part_l, res);
+  if (tid < 32) {
+    const int m = tid >> 4, r = tid & 15;
+    p.shared_gu[(size_t(part) * 2 + m) * Is + tile * kRows + r] = res[m * kRows + r];
+  }
+}
+
+// Route launch: workgroups [0, gx * gy) compute router logit partials (and
+// stage x); on the MFMA path the following Is / 16 * shared_parts
+// workgroups run the shared expert's gate/up in K parts.
+template <typename XT>
+__global__ void __launch_bounds__(256) route_kernel(DecodeArgs p, int gx, int gy) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = p.T, H = p.H, E = p.E;
-  // staging: one thread per 16-value run of x
-  {
-    const int g = blockIdx.x + blockIdx.y * gridDim.x;
+  const int g = blockIdx.x;
+  if (g >= gx * gy) {
+    shared_gate_up_part<XT>(p, g - gx * gy);
+    return;
+  }
+  const int bx = g % gx, by = g / gx;
+  // staging for the packed-f16 kernels: one thread per 16-value run of x
+  if (p.stage_x) {
     const int run_id = g * 256 + tid;
     const int runs = H / 16;
     if (run_id < T * runs) {
@@ -53,9 +100,20 @@ __global__ void __launch_bounds__(256) route_kernel(DecodeArgs p) {
       stage_run<kSplit>(v, p.stage_x + size_t(t) * staged_stride(H, kSplit), H, run);
     }
   }
+  // staging for the MFMA gate/up: one wavefront per 256-value column
+  if constexpr (std::is_same<XT, uint16_t>::value) {
+    if (p.stage_xm) {
+      const int cols = H / kKBlock, col_id = g * 4 + wave;
+      if (col_id < T * cols) {
+        const int t = col_id / cols, col = col_id % cols;
+        mfma_decode::stage_column(static_cast<const uint16_t*>(p.x) + size_t(t) * H,
+                                  p.stage_xm + size_t(t) * mfma_decode::stage_words(H), H, col);
+      }
+    }
+  }
   // logits partial of expert e over chunk c for every token
-  const int e = blockIdx.x * 4 + wave;
-  const int c = blockIdx.y;
+  const int e = bx * 4 + wave;
+  const int c = by;
   if (e >= E || c >= p.n_chunks) return;
   const int h0 = c * p.chunk;
   const float* wrow = p.router + size_t(e) * H + h0;
@@ -254,16 +312,19 @@ __device__ __forceinline__ void gate_up_tile(const DecodeArgs& p, uint32_t item)
   }
 }
 
-// gate/up launch: the routed tiles (first routed_tiles workgroups) and the
-// shared expert's tiles in one grid.
+// gate/up launch: the shared expert's tiles and the routed tiles in one grid.
 template <int Q, bool XSPLIT, int KU>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DecodeOcc<KU>::value, 8)))
     gate_up_kernel(DecodeArgs p) {
+  // the shared expert's tiles (3.2x the bytes of a routed Q2_K tile) are
+  // dispatched first, so that the routed tiles fill in behind them instead
+  // of the big tiles forming a tail on part of the chip
   const uint32_t item = blockIdx.x;
-  if (item < uint32_t(p.routed_tiles))
-    gate_up_tile<Q, XSPLIT, false, 4, KU>(p, item);
+  const uint32_t nshared = uint32_t(p.Is / kRows);
+  if (item < nshared)
+    gate_up_tile<INFERNO_Q8_0, XSPLIT, true, 4, 0>(p, item);
   else
-    gate_up_tile<INFERNO_Q8_0, XSPLIT, true, 4, 0>(p, item - uint32_t(p.routed_tiles));
+    gate_up_tile<Q, XSPLIT, false, 4, KU>(p, item - nshared);
 }
 
 // Routed down with the combine folded in, 8-row output tiles: workgroup =
@@ -495,7 +556,72 @@ int launch_gate_up_ring(hipStream_t s, const DecodeArgs& a, const ring::RingPlan
   }
 }
 
+// Routed Q2_K gate/up for one bf16 token on the matrix cores
+// (decode_mfma.hpp); on by default, INFERNO_DECODE_MFMA=0 turns it off.
+bool mfma_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("INFERNO_DECODE_MFMA");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
+// K parts of the shared gate/up on the MFMA path: the largest of 4, 3, 2
+// dividing the super-block columns.
+int shared_parts(int H) {
+  const int cols = H / kKBlock;
+  for (int k = 4; k > 1; --k)
+    if (cols % k == 0) return k;
+  return 1;
+}
+
+bool mfma_gate_up_covers(const DecodeArgs& a, int quant) {
+  return mfma_enabled() && a.T == 1 && quant == INFERNO_Q2_K && a.x_dtype == INFERNO_BF16 &&
+         (a.Is == 0 || a.shared_gu != nullptr) &&
+         a.I % kRows == 0 && mfma_decode::covers_width(a.H) &&
+         mfma_decode::lds_bytes(a.H) <= 160 * 1024 && a.stage_xm != nullptr &&
+         device_cus() > 0;
+}
+
+template <int NB>
+int launch_gate_up_mfma_nb(hipStream_t s, const DecodeArgs& a, int ntiles) {
+  static bool attr = false;
+  if (!attr) {
+    if (hipFuncSetAttribute((const void*)mfma_decode::gate_up_q2k_kernel<NB>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
+      set_error("MFMA gate/up kernel: cannot raise its LDS limit");
+      return INFERNO_ERR_DEVICE;
+    }
+    attr = true;
+  }
+  const unsigned grid = unsigned(std::min(ntiles, device_cus()));
+  mfma_decode::gate_up_q2k_kernel<NB>
+      <<<grid, mfma_decode::kThreads, mfma_decode::lds_bytes(a.H), s>>>(a, ntiles);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+// The routed tiles of the k slots on the MFMA kernel (the shared expert's
+// gate/up already ran in the route launch).
+int launch_gate_up_mfma(hipStream_t s, const DecodeArgs& a0) {
+  const int ntiles = a0.max_slots * (a0.I / kRows);
+  switch (a0.H / kKBlock) {
+    case 4: return launch_gate_up_mfma_nb<4>(s, a0, ntiles);
+    case 8: return launch_gate_up_mfma_nb<8>(s, a0, ntiles);
+    case 12: return launch_gate_up_mfma_nb<12>(s, a0, ntiles);
+    case 16: return launch_gate_up_mfma_nb<16>(s, a0, ntiles);
+    case 20: return launch_gate_up_mfma_nb<20>(s, a0, ntiles);
+    case 24: return launch_gate_up_mfma_nb<24>(s, a0, ntiles);
+    default: return launch_gate_up_mfma_nb<28>(s, a0, ntiles);
+  }
+}
+
 }  // namespace
+
+size_t decode_mfma_stage_words(size_t H) { return size_t(mfma_decode::stage_words(int(H))); }
+size_t decode_shared_partial_floats(size_t H, size_t Is) {
+  return size_t(shared_parts(int(H))) * 2 * Is;
+}
 
 bool decode_supported(size_t T, size_t k, size_t E, size_t H, size_t I, size_t Is, int x_dtype,
                       int quant, int down_quant) {
@@ -520,6 +646,12 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   a.n_chunks = a.H / a.chunk;
   a.max_slots = std::min(a.E, a.T * a.k);
   const bool xsplit = a.x_dtype == INFERNO_F32;
+  const bool use_mfma = mfma_gate_up_covers(a, quant);
+  // with the MFMA gate/up the shared expert's gate/up runs in the route
+  // launch and stages its own x; otherwise x is staged for the tile kernels
+  a.shared_parts = shared_parts(a.H);
+  if (use_mfma) a.stage_x = nullptr;
+  else a.stage_xm = nullptr;
   if (!decode_supported(a.T, a.k, a.E, a.H, a.I, a.Is, a.x_dtype, quant, quant)) {
     set_error("fused decode path does not cover this layer shape");
     return INFERNO_ERR_INVALID;
@@ -528,29 +660,52 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   {
     const int runs = a.T * a.H / 16;
     const int gx = (a.E + 3) / 4;
-    const int need = (runs + 255) / 256;
+    const int need = std::max((runs + 255) / 256, (a.T * (a.H / kKBlock) + 3) / 4);
     const int gy = std::max(a.n_chunks, (need + gx - 1) / gx);
-    const dim3 grid((unsigned)gx, (unsigned)gy);
-    if (xsplit)
-      route_kernel<float><<<grid, 256, 0, s>>>(a);
-    else
-      route_kernel<uint16_t><<<grid, 256, 0, s>>>(a);
-    INF_LAUNCHED();
+    const int shared_wgs = use_mfma ? a.Is / kRows * a.shared_parts : 0;
+    const unsigned grid = unsigned(gx * gy + shared_wgs);
+    const size_t lds = shared_wgs ? gate_up_lds(a.H / a.shared_parts, xsplit) : 0;
+    const int st = timed(s, kTimerRoute,
+                         shared_wgs ? "route+shared: route_kernel (router logit partials, Q8_0 "
+                                      "shared gate/up in K parts)"
+                                    : "route: route_kernel (router logit partials, x staging)",
+                         [&] {
+                           if (xsplit)
+                             route_kernel<float><<<grid, 256, lds, s>>>(a, gx, gy);
+                           else
+                             route_kernel<uint16_t><<<grid, 256, lds, s>>>(a, gx, gy);
+                           INF_LAUNCHED();
+                           return INFERNO_OK;
+                         });
+    if (st) return st;
   }
-  if (a.T == 1)
-    select1_kernel<<<1, 256, 0, s>>>(a);
-  else
-    select_kernel<<<1, 1024, 0, s>>>(a);
-  INF_LAUNCHED();
-  // routed and shared gate/up in one grid, then the routed down with the
-  // shared down and the residual folded in: one stream, no events
+  {
+    const int st = timed(s, kTimerSelect, a.T == 1 ? "select: select1_kernel" : "select: select_kernel",
+                         [&] {
+                           if (a.T == 1)
+                             select1_kernel<<<1, 256, 0, s>>>(a);
+                           else
+                             select_kernel<<<1, 1024, 0, s>>>(a);
+                           INF_LAUNCHED();
+                           return INFERNO_OK;
+                         });
+    if (st) return st;
+  }
+  // gate/up (routed tiles, plus the shared tiles when they did not run in
+  // the route launch), then the routed down with the shared down and the
+  // residual folded in: one stream, no events
   a.routed_tiles = a.max_slots * (a.I / kRows);
   ring::RingPlan pl;
   unsigned ring_grid = 0;
   size_t ring_lds = 0;
   int ring_pw = 0;
   const bool use_ring = ring_plan(a, quant, pl, ring_grid, ring_lds, ring_pw);
-  int st = timed(s, kTimerGateUp, [&]() -> int {
+  const char* gu_label =
+      use_mfma ? "mfma: gate_up_q2k_kernel (routed Q2_K tiles on MFMA; shared gate/up in the route launch)"
+      : use_ring ? "ring: gate_up_ring_kernel (routed + Q8_0 shared tiles)"
+                 : "tiles: gate_up_kernel (routed + Q8_0 shared tiles)";
+  int st = timed(s, kTimerGateUp, gu_label, [&]() -> int {
+    if (use_mfma) return launch_gate_up_mfma(s, a);
     if (use_ring) return launch_gate_up_ring(s, a, pl, ring_grid, ring_lds, ring_pw);
     switch (quant) {
       case INFERNO_Q2_K: xsplit ? launch_gate_up<INFERNO_Q2_K, true>(s, a) : launch_gate_up<INFERNO_Q2_K, false>(s, a); break;
@@ -561,7 +716,7 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
     return INFERNO_OK;
   });
   if (st) return st;
-  return timed(s, kTimerDown, [&] {
+  return timed(s, kTimerDown, "down8: down8_kernel (routed + Q8_0 shared down + combine)", [&] {
     switch (quant) {
       case INFERNO_Q2_K: launch_down<INFERNO_Q2_K>(s, a); break;
       case INFERNO_Q3_K: launch_down<INFERNO_Q3_K>(s, a); break;

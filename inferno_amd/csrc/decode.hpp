@@ -35,6 +35,9 @@ struct DecodeArgs {
   uint4* slots;           // [E] per active slot: expert, lo, hi, first assignment
   uint32_t* stage_h;      // [T*k, staged_stride(I, true)]
   uint32_t* stage_hs;     // [T, staged_stride(Is, true)]
+  uint32_t* stage_xm;     // [T, decode_mfma_stage_words(H)]: x staged for the MFMA gate/up
+  float* shared_gu;       // [shared_parts][2][Is]: shared gate/up partial sums (MFMA path, T = 1)
+  int shared_parts;       // K parts of the shared gate/up in the route launch
   // filled by launch_decode_layer
   int chunk, n_chunks, max_slots, routed_tiles;
 };
@@ -43,6 +46,10 @@ struct DecodeArgs {
 bool decode_supported(size_t T, size_t k, size_t E, size_t H, size_t I, size_t Is, int x_dtype,
                       int quant, int down_quant);
 int decode_chunk(size_t H);
+// Words per token of the activation staging used by the MFMA gate/up kernel.
+size_t decode_mfma_stage_words(size_t H);
+// Floats of the shared gate/up partial-sum buffer (T = 1 MFMA path).
+size_t decode_shared_partial_floats(size_t H, size_t Is);
 int launch_decode_layer(hipStream_t s, const DecodeArgs& a, int quant);
 
 

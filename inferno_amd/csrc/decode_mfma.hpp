@@ -1,0 +1,276 @@
+// Decode gate/up of the routed Q2_K experts for one token on the matrix
+// cores (v_mfma_f32_16x16x32_f16), with every 16-row tile read from HBM as
+// one contiguous range and staged in LDS.
+//
+// The dot product of a 16-row tile over one super-block column is one
+// MFMA tile C[m][n] = sum_k A[m][k] B[k][n]:
+//   B (weights): lane (row n, k-quarter kq) holds the 16 qs bytes
+//     qs[16 kq .. 16 kq + 15] of its row's block, i.e. the 16 values i of the
+//     Q2_K groups (h = kq >> 1, s = kq & 1) at all four bit planes p. A 2-bit
+//     field masked in place out of a 32-bit word (bits 2p and 16 + 2p) is a
+//     pair of exact f16 subnormals q * 2^(2p - 24), so one v_and_b32 yields
+//     two B operand values. MFMA (p, half) takes values i in [8 half, 8 half
+//     + 8) of every lane's plane p, in the order 0 2 1 3 4 6 5 7.
+//   A (activations): row m of A is group m of the block (scale byte m,
+//     m = 8h + 2p + s). A[m][k] holds x for the k that belong to group m and
+//     zero elsewhere, so the MFMA leaves each group's 16-value dot product in
+//     its own row of C: C[m][n] = sum_i q(n, m, i) x(m, i) (scaled). Only the
+//     lane (m, kq = 2h + s) is non-zero, in MFMA (p(m), half) for both
+//     halves; every other lane reads a zero block.
+//   C: lane (kq, n) holds groups 4kq .. 4kq + 3 of row n, whose scale bytes
+//     are the kq-th dword of the block's scales. The group scale and minimum
+//     enter with v_fma_mix: the 4-bit scale and min nibbles masked in place
+//     are f16 subnormals too, so no byte-to-float conversion is needed.
+//
+// Activations are staged per 256-value column as f16 x * s_c * 4^-p(run)
+// (s_c a power of two putting the column's max|x| in [2^14, 2^15); the 4^-p
+// undoes the bit plane's 4^p, so every group of a column has the same scale),
+// plus the unscaled run sums (for the Q2_K minimum) and 2^48 / s_c per
+// column. bf16 inputs are exact in this form except for values below
+// max|x| * 2^-28 of their column.
+//
+// Reference semantics: dequantize_q2_k_block (crates/gguf/src/lib.rs:
+// 1226-1293): value = (d * (sc & 15)) * q - dmin * (sc >> 4); gate/up with
+// SwiGLU and the routing weight folded into h (gguf_moe_kernels.metal:
+// 340-455). Accumulation is fp32; the sum order differs from the reference's
+// (the parity bound is the layer tolerance, rel-L2 2e-3).
+//
+// A workgroup (16 wavefronts) is persistent over tiles t = blockIdx.x + j *
+// gridDim.x: it writes tile t (held in registers) to LDS, issues the loads of
+// tile t + gridDim.x into the same registers, and computes tile t from LDS.
+// No workgroup waits on another.
+#pragma once
+#include "decode.hpp"
+#include "dot2_formats.hpp"
+
+namespace inferno {
+namespace mfma_decode {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+constexpr int kWaves = 16;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kQ2Bytes = 84;
+constexpr int kRowPad = 16;    // LDS row padding (bytes): rows start on distinct banks
+
+// Staged row (words): [pairs K/2][run sums K/16][column factors K/256], padded to 4.
+__host__ __device__ constexpr int stage_words(int K) { return (K / 2 + K / 16 + K / 256 + 3) & ~3; }
+
+// Stages super-block column `col` of one bf16 row into `row` (the layout
+// above); one full wavefront, lane l holding values 4l .. 4l + 3.
+__device__ __forceinline__ void stage_column(const uint16_t* x, uint32_t* row, int K, int col) {
+  const int lane = threadIdx.x & 63;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = bf16_bits_to_f32(x[col * kKBlock + 4 * lane + i]);
+  float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+  float s = 1.0f;  // zero or non-finite columns keep scale 1
+  if (m > 0.f && m < 3.0e38f) {
+    int e;
+    frexpf(m, &e);
+    s = ldexpf(1.0f, 15 - e);
+  }
+  const int run = lane >> 2;                 // 16-value run of this lane
+  const int p = (run >> 1) & 3;              // its bit plane
+  const float f = s * ldexpf(1.0f, -2 * p);
+  float sum = (v[0] + v[1]) + (v[2] + v[3]);
+  sum += __shfl_xor(sum, 1, kWave);
+  sum += __shfl_xor(sum, 2, kWave);
+  // words 2u, 2u + 1 of the run (u = lane & 3): values (4u, 4u + 2), (4u + 1, 4u + 3)
+  auto pack = [&](float a, float b) {
+    const _Float16 ah = (_Float16)(a * f), bh = (_Float16)(b * f);
+    return uint32_t(__builtin_bit_cast(uint16_t, ah)) | (uint32_t(__builtin_bit_cast(uint16_t, bh)) << 16);
+  };
+  uint32_t* pairs = row + col * 128 + run * 8 + 2 * (lane & 3);
+  pairs[0] = pack(v[0], v[2]);
+  pairs[1] = pack(v[1], v[3]);
+  float* sums = reinterpret_cast<float*>(row + K / 2);
+  if ((lane & 3) == 0) sums[col * 16 + run] = sum;
+  if (lane == 0) sums[K / 16 + col] = 16777216.0f * 16777216.0f / s;
+}
+
+__device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
+
+// Loads tile t's gate and up rows (16 contiguous rows each) into registers,
+// one 16-byte chunk per thread and step.
+template <int PER>
+__device__ __forceinline__ void fetch_tile(u32x4 (&v)[PER], const DecodeArgs& p, int tiles_i,
+                                           int rb, int t, uint32_t expert) {
+  const int nv = rb;  // 16-byte chunks per matrix (16 rows of rb bytes)
+  const size_t off = size_t(expert) * p.gate_stride + size_t(t % tiles_i) * 16 * size_t(rb);
+  const u32x4* g4 = reinterpret_cast<const u32x4*>(p.gate + off);
+  const u32x4* u4 = reinterpret_cast<const u32x4*>(p.up + off);
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    int i = j * kThreads + tid;
+    i = i < 2 * nv ? i : 2 * nv - 1;  // clamped; the extra chunks are not stored
+    v[j] = i < nv ? g4[i] : u4[i - nv];
+  }
+}
+
+// Chunks per thread of a layer with NB super-block columns.
+__host__ __device__ constexpr int chunks_per_thread(int NB) {
+  return (2 * NB * kQ2Bytes + kThreads - 1) / kThreads;
+}
+
+// NB = H / 256 super-block columns (a multiple of 4, so rows are whole
+// 16-byte chunks); compile-time so that the chunk -> (matrix, row, column)
+// split and the LDS addressing use constant divisors and strides.
+template <int NB>
+__global__ void __launch_bounds__(kThreads) gate_up_q2k_kernel(DecodeArgs p, int ntiles) {
+  extern __shared__ uint32_t smem[];
+  constexpr int H = NB * kKBlock, PER = chunks_per_thread(NB);
+  constexpr int rb = NB * kQ2Bytes, RS = rb + kRowPad, nv = rb;
+  constexpr int Sm = stage_words(H);
+  const int I = p.I;
+  uint32_t* xs = smem;
+  uint32_t* zero = smem + Sm;
+  uint8_t* tl = reinterpret_cast<uint8_t*>(smem + Sm + 4);
+  float* part = reinterpret_cast<float*>(tl + 2 * 16 * RS);  // [wave][matrix][16]
+  uint32_t* slot_e = reinterpret_cast<uint32_t*>(part + kWaves * 2 * 16);  // [max_slots]
+  uint32_t* slot_a = slot_e + kMaxExperts;
+  float* slot_w = reinterpret_cast<float*>(slot_a + kMaxExperts);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, q = lane >> 4;
+  const int tiles_i = I / kRows;
+  u32x4 v[PER];
+  int t = blockIdx.x;
+  if (t < ntiles) fetch_tile<PER>(v, p, tiles_i, rb, t, p.slots[t / tiles_i].x);
+  for (int i = tid; i < Sm / 4; i += kThreads)
+    reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(p.stage_xm)[i];
+  if (tid < 4) zero[tid] = 0;
+  // per-slot expert, assignment and routing weight, read once
+  for (int j = tid; j < p.max_slots; j += kThreads) {
+    const uint4 sl = p.slots[j];
+    slot_e[j] = sl.x;
+    slot_a[j] = sl.w;
+    slot_w[j] = p.weights[sl.w];
+  }
+  // the shared expert's gate/up partial sums (split over K in the route
+  // launch) -> SwiGLU -> staged h rows, one 16-row tile per workgroup
+  if (p.Is && tid < 16) {
+    for (int st = blockIdx.x; st < p.Is / kRows; st += gridDim.x) {
+      float g = 0.f, u = 0.f;
+      for (int k = 0; k < p.shared_parts; ++k) {
+        g += p.shared_gu[(size_t(k) * 2) * p.Is + st * kRows + tid];
+        u += p.shared_gu[(size_t(k) * 2 + 1) * p.Is + st * kRows + tid];
+      }
+      stage_run_lanes(silu(g) * u, p.stage_hs, p.Is, st);
+    }
+  }
+  // A operand: lane (m = n, kq = q) is live iff kq == 2h + s of group m
+  const bool act = q == 2 * (n >> 3) + (n & 1);
+  const int pm = (n >> 1) & 3;
+  const float* sums = reinterpret_cast<const float*>(xs + H / 2);
+  const float* colf = sums + H / 16;
+  for (; t < ntiles; t += gridDim.x) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = j * kThreads + tid;
+      if (i < 2 * nv) {
+        const int mat = i >= nv, rem = i - mat * nv, row = rem / (rb / 16), c16 = rem - row * (rb / 16);
+        *reinterpret_cast<u32x4*>(tl + (mat * 16 + row) * RS + c16 * 16) = v[j];
+      }
+    }
+    __syncthreads();
+    if (t + int(gridDim.x) < ntiles)
+      fetch_tile<PER>(v, p, tiles_i, rb, t + gridDim.x, slot_e[(t + gridDim.x) / tiles_i]);
+    const int slot = t / tiles_i, tile = t - slot * tiles_i;
+    float acc[2] = {0.f, 0.f};
+    for (int c = wave; c < NB; c += kWaves) {
+      half8 A[4][2];
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const uint32_t* src = (act && pp == pm) ? xs + c * 128 + n * 8 + 4 * hf : zero;
+          A[pp][hf] = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(src));
+        }
+      const float4 xsum = *reinterpret_cast<const float4*>(sums + c * 16 + 4 * q);
+      const float kc = colf[c];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const uint8_t* blk = tl + (m * 16 + n) * RS + c * kQ2Bytes;
+        const u32x4_a4 qs = *reinterpret_cast<const u32x4_a4*>(blk + 16 + 16 * q);
+        const uint32_t scw = *reinterpret_cast<const uint32_t*>(blk + 4 * q);
+        const uint32_t dmw = *reinterpret_cast<const uint32_t*>(blk + 80);
+        floatx4 C = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const uint32_t w0 = hf ? qs.z : qs.x, w1 = hf ? qs.w : qs.y;
+          const uint32_t o0 = w0 >> 8, o1 = w1 >> 8;
+#pragma unroll
+          for (int pp = 0; pp < 4; ++pp) {
+            const uint32_t M = 0x00030003u << (2 * pp);
+            const uint4 bv = make_uint4(w0 & M, o0 & M, w1 & M, o1 & M);
+            C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[pp][hf], __builtin_bit_cast(half8, bv), C,
+                                                       0, 0, 0);
+          }
+        }
+        // scale nibbles (bytes 0, 2 | 1, 3) and min nibbles as f16 subnormal pairs
+        const uint32_t sh = scw >> 8;
+        const half2v s02 = as_h2(scw & 0x000f000fu), s13 = as_h2(sh & 0x000f000fu);
+        const half2v m02 = as_h2(scw & 0x00f000f0u), m13 = as_h2(sh & 0x00f000f0u);
+        const half2v dm = as_h2(dmw);
+        float S = fmaf((float)s02.x, C[0], 0.f);
+        S = fmaf((float)s13.x, C[1], S);
+        S = fmaf((float)s02.y, C[2], S);
+        S = fmaf((float)s13.y, C[3], S);
+        float Mn = fmaf((float)m02.x, xsum.x, 0.f);
+        Mn = fmaf((float)m13.x, xsum.y, Mn);
+        Mn = fmaf((float)m02.y, xsum.z, Mn);
+        Mn = fmaf((float)m13.y, xsum.w, Mn);
+        // value = d * sc * q - dmin * m: S carries 2^-48 s_c, Mn carries 2^-20
+        acc[m] = fmaf((float)dm.x * kc, S, acc[m]);
+        acc[m] = fmaf(-(float)dm.y * 1048576.0f, Mn, acc[m]);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      float r = acc[m];
+      r += __shfl_xor(r, 16, kWave);
+      r += __shfl_xor(r, 32, kWave);
+      if (q == 0) part[(wave * 2 + m) * 16 + n] = r;
+    }
+    __syncthreads();
+    // lanes 0..15 sum gate rows, lanes 16..31 up rows, over the wavefronts
+    // in order; no barrier follows: the next tile's LDS writes only start
+    // the next compute phase after a barrier this wavefront also reaches
+    if (tid < 32) {
+      float r = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) r += part[(w * 2 + (tid >> 4)) * 16 + (tid & 15)];
+      const float u = __shfl_down(r, 16, kWave);
+      if (tid < 16) {
+        const uint32_t a = slot_a[slot];  // the slot's (single) assignment
+        stage_run_lanes(silu(r) * u * slot_w[slot],
+                        p.stage_h + size_t(a) * staged_stride(I, true), I, tile);
+      }
+    }
+  }
+}
+
+// True when the kernel has an instance for a layer of width H: NB = H / 256
+// in {4, 8, ..., 28} (whole 16-byte chunks per row, at most five chunks per
+// thread: six spill).
+inline bool covers_width(int H) {
+  const int NB = H / kKBlock;
+  return H % kKBlock == 0 && NB % 4 == 0 && NB >= 4 && NB <= 28;
+}
+
+inline size_t lds_bytes(int H) {
+  const int rb = H / kKBlock * kQ2Bytes;
+  return size_t(stage_words(H) + 4) * 4 + size_t(2 * 16) * (rb + kRowPad) +
+         size_t(kWaves * 2 * 16) * 4 + size_t(3 * kMaxExperts) * 4;
+}
+
+}  // namespace mfma_decode
+}  // namespace inferno

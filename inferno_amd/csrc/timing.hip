@@ -11,6 +11,7 @@ struct KernelTimers {
   bool on = false;
   double ms[kNumTimers] = {};
   uint64_t n[kNumTimers] = {};
+  const char* label[kNumTimers] = {};
   hipEvent_t ev[64][2] = {};
 };
 
@@ -59,10 +60,17 @@ int kernel_timing_events(hipEvent_t* start, hipEvent_t* stop) {
   return INFERNO_OK;
 }
 
-void kernel_timing_add(int which, float ms) {
+void kernel_timing_add(int which, float ms, const char* label) {
   std::lock_guard<std::mutex> lock(timers().mu);
   timers().ms[which] += ms;
   timers().n[which] += 1;
+  timers().label[which] = label;
+}
+
+const char* kernel_timing_label(int which) {
+  if (which < 0 || which >= kNumTimers) return "";
+  std::lock_guard<std::mutex> lock(timers().mu);
+  return timers().label[which] ? timers().label[which] : "";
 }
 
 }  // namespace inferno

@@ -170,7 +170,7 @@ def rms_norm(x, w, eps):
     return out
 
 
-TIMER_GATE_UP, TIMER_DOWN = 0, 1
+TIMER_GATE_UP, TIMER_DOWN, TIMER_ROUTE, TIMER_SELECT = 0, 1, 2, 3
 
 
 def kernel_timing(enable):
@@ -184,6 +184,13 @@ def kernel_timing_read(which):
     ms, n = C.c_double(0.0), C.c_uint64(0)
     check(lib().inferno_kernel_timing_read(which, C.byref(ms), C.byref(n)))
     return ms.value, n.value
+
+
+def kernel_timing_label(which):
+    """Label of the last launch a timer measured: "<kind>: <kernel> (...)"."""
+    buf = C.create_string_buffer(256)
+    check(lib().inferno_kernel_timing_label(which, buf, len(buf)))
+    return buf.value.decode()
 
 
 def synth_normal(seed, stddev, n, dtype=torch.float32, device="cuda"):
