@@ -161,21 +161,25 @@ def main():
         shared_dn = cfg.shared_intermediate * (H // 32) * 34
         gu_kind = labels[ops.TIMER_GATE_UP].split(":")[0]
         rt_kind = labels[ops.TIMER_ROUTE].split(":")[0]
+        dn_kind = labels[ops.TIMER_DOWN].split(":")[0]
+        sl_kind = labels[ops.TIMER_SELECT].split(":")[0]
         gu_routed = gu_bytes_per_expert * uniq_layer
         kernels = {
             "route": {"label": labels[ops.TIMER_ROUTE], "launch_us": us[ops.TIMER_ROUTE],
                       "bytes_per_launch": router_bytes + (shared_gu if rt_kind == "route+shared" else 0)},
             "select": {"label": labels[ops.TIMER_SELECT], "launch_us": us[ops.TIMER_SELECT],
-                       "bytes_per_launch": None},
+                       "bytes_per_launch": shared_dn if sl_kind == "select+shared-down" else None},
             "gate_up": {"label": labels[ops.TIMER_GATE_UP], "launch_us": gu_us,
                         "bytes_per_launch": gu_routed + (shared_gu if gu_kind in ("tiles", "ring") else 0),
                         "routed_bytes_per_launch": gu_routed,
                         "traffic_file": {"mfma": "gate_up_mfma_q2k_c2_decode_traffic.txt",
                                          "tiles": "gate_up_q2k_c2_decode_traffic.txt"}.get(gu_kind)},
             "down": {"label": labels[ops.TIMER_DOWN], "launch_us": dn_us,
-                     "bytes_per_launch": dn_bytes_per_expert * uniq_layer + shared_dn,
+                     "bytes_per_launch": dn_bytes_per_expert * uniq_layer
+                     + (shared_dn if dn_kind == "down8" else 0),
                      "routed_bytes_per_launch": dn_bytes_per_expert * uniq_layer,
-                     "traffic_file": "down8_q2k_c2_decode_traffic.txt"},
+                     "traffic_file": {"down8": "down8_q2k_c2_decode_traffic.txt",
+                                      "mfma-down": "down_mfma_q2k_c2_decode_traffic.txt"}.get(dn_kind)},
         }
         for kd in kernels.values():
             b = kd["bytes_per_launch"]

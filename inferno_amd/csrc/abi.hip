@@ -499,6 +499,7 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
     d.sorted = w.moe.sorted; d.active = w.moe.active; d.stage_h = w.moe.stage_h;
     d.stage_hs = w.stage_hs; d.slots = w.slots; d.stage_xm = w.stage_xm;
     d.shared_gu = w.shared_gu;
+    d.ys = w.ys;
     return launch_decode_layer(s, d, L->quant);
   }
   if ((st = launch_router_logits(s, x, x_dtype, L->router, T, H, E, w.logits))) return st;

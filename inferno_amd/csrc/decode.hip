@@ -163,10 +163,78 @@ __device__ __forceinline__ void sum_partials(const DecodeArgs& p, int t, float* 
   }
 }
 
+// The Q8_0 shared expert's down for output rows [32 g, 32 g + 32) of the one
+// token (MFMA down path), run by a workgroup of the select launch: it only
+// needs the shared gate/up partial sums of the route launch. Each workgroup
+// forms the shared h row itself (partials summed in part order, h = silu(g)
+// * u) and stages it into its LDS, so no workgroup depends on another; then
+// four 8-row groups with the lane split and summation order of the shared
+// part of down8_kernel. Writes ys.
+constexpr int kSharedDownRows = 32;
+__device__ __forceinline__ void shared_down_rows(const DecodeArgs& p, int g) {
+  using FS = Fmt<INFERNO_Q8_0>;
+  extern __shared__ uint32_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = (lane >> 2) & 7, sub = lane & 3, cp = lane >> 5;
+  const int Is = p.Is, ubs = Is / kKBlock;
+  const int Sns = staged_stride(Is, false);
+  uint32_t* xss = smem;
+  float* part = reinterpret_cast<float*>(xss + Sns);  // [4 wavefronts][8 rows]
+  float* hrow = part + 32;                             // [Is] shared h
+  const int q_first = cp + 2 * wave;
+  constexpr int kGroups = kSharedDownRows / 8;
+  auto srow = [&](int grp) {
+    return p.sdown + size_t(g * kSharedDownRows + grp * 8 + r) * size_t(ubs) * FS::kBytes;
+  };
+  // every group's first unit in flight while h is formed
+  uint32_t sraw[kGroups][FS::kDw];
+#pragma unroll
+  for (int grp = 0; grp < kGroups; ++grp)
+    if (q_first < ubs) FS::load(srow(grp) + size_t(q_first) * FS::kBytes, sub, sraw[grp]);
+  // h = silu(sum of gate partials) * (sum of up partials), 4 values per step
+  for (int v4 = tid; v4 < Is / 4; v4 += 256) {
+    float4 gs = make_float4(0.f, 0.f, 0.f, 0.f), us = gs;
+    for (int k = 0; k < p.shared_parts; ++k) {
+      const float4 a = reinterpret_cast<const float4*>(p.shared_gu + (size_t(k) * 2) * Is)[v4];
+      const float4 b = reinterpret_cast<const float4*>(p.shared_gu + (size_t(k) * 2 + 1) * Is)[v4];
+      gs.x += a.x; gs.y += a.y; gs.z += a.z; gs.w += a.w;
+      us.x += b.x; us.y += b.y; us.z += b.z; us.w += b.w;
+    }
+    reinterpret_cast<float4*>(hrow)[v4] =
+        make_float4(silu(gs.x) * us.x, silu(gs.y) * us.y, silu(gs.z) * us.z, silu(gs.w) * us.w);
+  }
+  __syncthreads();
+  for (int run = tid; run < Is / 16; run += 256) stage_run<false>(hrow + run * 16, xss, Is, run);
+  __syncthreads();
+#pragma unroll
+  for (int grp = 0; grp < kGroups; ++grp) {
+    float accs = 0.f;
+    for (int q = q_first; q < ubs; q += 8) {
+      if (q != q_first) FS::load(srow(grp) + size_t(q) * FS::kBytes, sub, sraw[grp]);
+      accs += FS::dot(sraw[grp], sub, xrow_at<false>(xss, Is, q));
+    }
+    accs += __shfl_xor(accs, 1, kWave);
+    accs += __shfl_xor(accs, 2, kWave);
+    accs += __shfl_xor(accs, 32, kWave);
+    if ((lane & 35) == 0) part[wave * 8 + r] = accs;
+    __syncthreads();
+    if (tid < 8)
+      p.ys[size_t(g) * kSharedDownRows + grp * 8 + tid] =
+          ((part[tid] + part[8 + tid]) + part[16 + tid]) + part[24 + tid];
+    __syncthreads();
+  }
+}
+
 // T = 1: the k selected ids are distinct, so the dispatch is the k ids
 // sorted ascending (one assignment each); wavefront 0 does top-k and the
-// dispatch after the workgroup has summed the partials.
+// dispatch after the workgroup has summed the partials. On the MFMA down
+// path workgroups 1.. of this launch run the shared expert's down.
 __global__ void __launch_bounds__(256) select1_kernel(DecodeArgs p) {
+  if (blockIdx.x > 0) {
+    shared_down_rows(p, int(blockIdx.x) - 1);
+    return;
+  }
   __shared__ float logit_row[kMaxExperts];
   __shared__ float bias[kMaxExperts];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -616,6 +684,38 @@ int launch_gate_up_mfma(hipStream_t s, const DecodeArgs& a0) {
   }
 }
 
+template <int PER>
+int launch_down_mfma_per(hipStream_t s, const DecodeArgs& a) {
+  static bool attr = false;
+  auto* kern = mfma_decode::down_q2k_kernel<8, PER>;
+  if (!attr) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024) != hipSuccess) {
+      set_error("MFMA down kernel: cannot raise its LDS limit");
+      return INFERNO_ERR_DEVICE;
+    }
+    attr = true;
+  }
+  const int ntiles = a.H / kRows;
+  const unsigned grid = unsigned(std::min(ntiles, device_cus()));
+  kern<<<grid, mfma_decode::kThreads, mfma_decode::down_lds_bytes(a.I), s>>>(a, ntiles);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+// Routed down for one token on the MFMA kernel (I = 2048: 8 super-block
+// columns; k <= 8 ranks).
+int launch_down_mfma(hipStream_t s, const DecodeArgs& a) {
+  switch (mfma_decode::down_chunks_per_thread(8, a.k)) {
+    case 1: return launch_down_mfma_per<1>(s, a);
+    case 2: return launch_down_mfma_per<2>(s, a);
+    case 3: return launch_down_mfma_per<3>(s, a);
+    case 4: return launch_down_mfma_per<4>(s, a);
+    case 5: return launch_down_mfma_per<5>(s, a);
+    default: return launch_down_mfma_per<6>(s, a);
+  }
+}
+
 }  // namespace
 
 size_t decode_mfma_stage_words(size_t H) { return size_t(mfma_decode::stage_words(int(H))); }
@@ -652,6 +752,14 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   a.shared_parts = shared_parts(a.H);
   if (use_mfma) a.stage_x = nullptr;
   else a.stage_xm = nullptr;
+  // the MFMA down kernel follows the MFMA gate/up (it reads h in that
+  // kernel's layout); the shared down then runs in the select launch
+  const bool use_mfma_down = use_mfma && mfma_decode::down_covers(a.I, a.k) &&
+                             a.H % kSharedDownRows == 0 &&
+                             mfma_decode::down_lds_bytes(a.I) <= 160 * 1024 &&
+                             (a.Is == 0 || a.ys != nullptr);
+  a.h_mfma = use_mfma_down ? 1 : 0;
+  if (!use_mfma_down) a.ys = nullptr;
   if (!decode_supported(a.T, a.k, a.E, a.H, a.I, a.Is, a.x_dtype, quant, quant)) {
     set_error("fused decode path does not cover this layer shape");
     return INFERNO_ERR_INVALID;
@@ -680,15 +788,19 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
     if (st) return st;
   }
   {
-    const int st = timed(s, kTimerSelect, a.T == 1 ? "select: select1_kernel" : "select: select_kernel",
-                         [&] {
-                           if (a.T == 1)
-                             select1_kernel<<<1, 256, 0, s>>>(a);
-                           else
-                             select_kernel<<<1, 1024, 0, s>>>(a);
-                           INF_LAUNCHED();
-                           return INFERNO_OK;
-                         });
+    const int sd_wgs = (use_mfma_down && a.Is) ? a.H / kSharedDownRows : 0;
+    const size_t sd_lds = sd_wgs ? (size_t(staged_stride(a.Is, false)) + 32 + a.Is) * 4 : 0;
+    const char* label = a.T != 1 ? "select: select_kernel"
+                        : sd_wgs ? "select+shared-down: select1_kernel (top-k, dispatch; Q8_0 shared down)"
+                                 : "select: select1_kernel";
+    const int st = timed(s, kTimerSelect, label, [&] {
+      if (a.T == 1)
+        select1_kernel<<<1 + sd_wgs, 256, sd_lds, s>>>(a);
+      else
+        select_kernel<<<1, 1024, 0, s>>>(a);
+      INF_LAUNCHED();
+      return INFERNO_OK;
+    });
     if (st) return st;
   }
   // gate/up (routed tiles, plus the shared tiles when they did not run in
@@ -716,6 +828,11 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
     return INFERNO_OK;
   });
   if (st) return st;
+  if (use_mfma_down)
+    return timed(s, kTimerDown,
+                 "mfma-down: down_q2k_kernel (routed Q2_K down on MFMA + combine; shared down "
+                 "in the select launch)",
+                 [&] { return launch_down_mfma(s, a); });
   return timed(s, kTimerDown, "down8: down8_kernel (routed + Q8_0 shared down + combine)", [&] {
     switch (quant) {
       case INFERNO_Q2_K: launch_down<INFERNO_Q2_K>(s, a); break;

@@ -38,6 +38,8 @@ struct DecodeArgs {
   uint32_t* stage_xm;     // [T, decode_mfma_stage_words(H)]: x staged for the MFMA gate/up
   float* shared_gu;       // [shared_parts][2][Is]: shared gate/up partial sums (MFMA path, T = 1)
   int shared_parts;       // K parts of the shared gate/up in the route launch
+  float* ys;              // [T, H]: shared down output (MFMA down path)
+  int h_mfma;             // gate/up writes h in the MFMA down layout
   // filled by launch_decode_layer
   int chunk, n_chunks, max_slots, routed_tiles;
 };

@@ -95,6 +95,43 @@ __device__ __forceinline__ void stage_column(const uint16_t* x, uint32_t* row, i
   if (lane == 0) sums[K / 16 + col] = 16777216.0f * 16777216.0f / s;
 }
 
+// Stages one 16-value run held one value per lane by lanes 0..15 (lane i
+// holds value i; only those lanes call it) into a K-wide row of the MFMA
+// layout with a per-run scale: [pairs K/2][run sums K/16][run factors
+// K/16], factor = 2^48 / s_run. The gate/up kernel writes h this way (one
+// 16-row tile is one run of h); the down kernel reads it.
+__device__ __forceinline__ void stage_run_lanes_mfma(float v, uint32_t* row, int K, int run) {
+  const int lane = threadIdx.x & 63;
+  float m = fabsf(v), sum = v;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    m = fmaxf(m, __shfl_xor(m, o, 16));
+    sum += __shfl_xor(sum, o, 16);
+  }
+  float s = 1.0f;  // zero or non-finite runs keep scale 1
+  if (m > 0.f && m < 3.0e38f) {
+    int e;
+    frexpf(m, &e);
+    s = ldexpf(1.0f, 15 - e);
+  }
+  const int p = ((run & 15) >> 1) & 3;  // bit plane of this run's group
+  const _Float16 hv = (_Float16)(v * (s * ldexpf(1.0f, -2 * p)));
+  const uint32_t hb = __builtin_bit_cast(uint16_t, hv);
+  // pair word j holds values (base, base + 2), base = 4 (j >> 1) + (j & 1)
+  const int j = lane & 7;
+  const int base = 4 * (j >> 1) + (j & 1);
+  const uint32_t h0 = __shfl(hb, base, 16), h1 = __shfl(hb, base + 2, 16);
+  if (lane < 8) row[run * 8 + j] = h0 | (h1 << 16);
+  if (lane == 0) {
+    float* sums = reinterpret_cast<float*>(row + K / 2);
+    sums[run] = sum;
+    sums[K / 16 + run] = 16777216.0f * 16777216.0f / s;
+  }
+}
+
+// Words per row of that layout.
+__host__ __device__ constexpr int run_stage_words(int K) { return K / 2 + K / 8; }
+
 __device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
 
 // Loads tile t's gate and up rows (16 contiguous rows each) into registers,
@@ -155,8 +192,9 @@ __global__ void __launch_bounds__(kThreads) gate_up_q2k_kernel(DecodeArgs p, int
     slot_w[j] = p.weights[sl.w];
   }
   // the shared expert's gate/up partial sums (split over K in the route
-  // launch) -> SwiGLU -> staged h rows, one 16-row tile per workgroup
-  if (p.Is && tid < 16) {
+  // launch) -> SwiGLU -> staged h rows for down8_kernel, one 16-row tile per
+  // workgroup (with the MFMA down the select launch forms them itself)
+  if (p.Is && !p.h_mfma && tid < 16) {
     for (int st = blockIdx.x; st < p.Is / kRows; st += gridDim.x) {
       float g = 0.f, u = 0.f;
       for (int k = 0; k < p.shared_parts; ++k) {
@@ -251,11 +289,161 @@ __global__ void __launch_bounds__(kThreads) gate_up_q2k_kernel(DecodeArgs p, int
       const float u = __shfl_down(r, 16, kWave);
       if (tid < 16) {
         const uint32_t a = slot_a[slot];  // the slot's (single) assignment
-        stage_run_lanes(silu(r) * u * slot_w[slot],
-                        p.stage_h + size_t(a) * staged_stride(I, true), I, tile);
+        const float h = silu(r) * u * slot_w[slot];
+        if (p.h_mfma)  // the MFMA down kernel reads h
+          stage_run_lanes_mfma(h, p.stage_h + size_t(a) * run_stage_words(I), I, tile);
+        else
+          stage_run_lanes(h, p.stage_h + size_t(a) * staged_stride(I, true), I, tile);
       }
     }
   }
+}
+
+// ------------------------------------------------------------------ down
+//
+// Routed down for one token on the matrix cores: output tile = 16 rows of
+// H, all k ranks (the k selected experts' down rows [16t, 16t + 16), each
+// 16 * NB * 84 contiguous bytes, streamed into LDS as in gate/up). A block
+// (rank r, super-block column c) is one MFMA tile against h_r, whose rows
+// the gate/up kernel staged with a per-run scale (stage_run_lanes_mfma);
+// each wavefront takes the blocks b = wave + 16 j and keeps per-row sums.
+// out = (residual + shared down) + routed, with the wavefronts' sums added
+// in order: deterministic, no float atomics. The shared down (ys) was
+// computed by the select launch.
+
+constexpr int kMaxDownRanks = 8;
+
+__host__ __device__ constexpr int down_chunks_per_thread(int NB, int k) {
+  return (k * NB * kQ2Bytes + kThreads - 1) / kThreads;
+}
+
+template <int NB, int PER>
+__device__ __forceinline__ void fetch_down_tile(u32x4 (&v)[PER], const DecodeArgs& p, int k,
+                                                const uint32_t* rank_e, int t) {
+  constexpr int rb = NB * kQ2Bytes;  // bytes per row; chunks per rank tile = rb
+  const int tid = threadIdx.x, nv = k * rb;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    int i = j * kThreads + tid;
+    i = i < nv ? i : nv - 1;  // clamped; the extra chunks are not stored
+    const int r = i / rb, w = i - r * rb;
+    const u32x4* src = reinterpret_cast<const u32x4*>(p.down + size_t(rank_e[r]) * p.down_stride +
+                                                      size_t(t) * 16 * rb);
+    v[j] = src[w];
+  }
+}
+
+template <int NB, int PER>
+__global__ void __launch_bounds__(kThreads) down_q2k_kernel(DecodeArgs p, int ntiles) {
+  extern __shared__ uint32_t smem[];
+  constexpr int K = NB * kKBlock;  // the expert intermediate I
+  constexpr int rb = NB * kQ2Bytes, RS = rb + kRowPad, Sh = run_stage_words(K);
+  const int k = p.k, H = p.H;
+  uint32_t* hs = smem;                             // [k][Sh]
+  uint32_t* zero = hs + kMaxDownRanks * Sh;
+  uint8_t* tl = reinterpret_cast<uint8_t*>(zero + 4);  // [k][16 rows][RS]
+  float* part = reinterpret_cast<float*>(tl + kMaxDownRanks * 16 * RS);  // [wave][16]
+  uint32_t* rank_e = reinterpret_cast<uint32_t*>(part + kWaves * 16);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, q = lane >> 4;
+  if (tid < k) rank_e[tid] = p.ids[tid];
+  u32x4 v[PER];
+  int t = blockIdx.x;
+  __syncthreads();
+  if (t < ntiles) fetch_down_tile<NB, PER>(v, p, k, rank_e, t);
+  for (int i = tid; i < k * Sh / 4; i += kThreads)
+    reinterpret_cast<uint4*>(hs)[i] = reinterpret_cast<const uint4*>(p.stage_h)[i];
+  if (tid < 4) zero[tid] = 0;
+  const bool act = q == 2 * (n >> 3) + (n & 1);
+  const int pm = (n >> 1) & 3;
+  const int nblk = k * NB;
+  for (; t < ntiles; t += gridDim.x) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = j * kThreads + tid;
+      if (i < k * rb) {
+        const int r = i / rb, w = i - r * rb, row = w / (rb / 16), c16 = w - row * (rb / 16);
+        *reinterpret_cast<u32x4*>(tl + (r * 16 + row) * RS + c16 * 16) = v[j];
+      }
+    }
+    __syncthreads();
+    if (t + int(gridDim.x) < ntiles) fetch_down_tile<NB, PER>(v, p, k, rank_e, t + gridDim.x);
+    float acc = 0.f;
+    for (int b = wave; b < nblk; b += kWaves) {
+      const int r = b / NB, c = b - r * NB;
+      const uint32_t* hr = hs + r * Sh;
+      half8 A[4][2];
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const uint32_t* src = (act && pp == pm) ? hr + c * 128 + n * 8 + 4 * hf : zero;
+          A[pp][hf] = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(src));
+        }
+      const float* sums = reinterpret_cast<const float*>(hr + K / 2);
+      const float4 xsum = *reinterpret_cast<const float4*>(sums + c * 16 + 4 * q);
+      const float4 kk = *reinterpret_cast<const float4*>(sums + K / 16 + c * 16 + 4 * q);
+      const uint8_t* blk = tl + (r * 16 + n) * RS + c * kQ2Bytes;
+      const u32x4_a4 qs = *reinterpret_cast<const u32x4_a4*>(blk + 16 + 16 * q);
+      const uint32_t scw = *reinterpret_cast<const uint32_t*>(blk + 4 * q);
+      const uint32_t dmw = *reinterpret_cast<const uint32_t*>(blk + 80);
+      floatx4 C = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const uint32_t w0 = hf ? qs.z : qs.x, w1 = hf ? qs.w : qs.y;
+        const uint32_t o0 = w0 >> 8, o1 = w1 >> 8;
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          const uint32_t M = 0x00030003u << (2 * pp);
+          const uint4 bv = make_uint4(w0 & M, o0 & M, w1 & M, o1 & M);
+          C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[pp][hf], __builtin_bit_cast(half8, bv), C,
+                                                     0, 0, 0);
+        }
+      }
+      const uint32_t sh = scw >> 8;
+      const half2v s02 = as_h2(scw & 0x000f000fu), s13 = as_h2(sh & 0x000f000fu);
+      const half2v m02 = as_h2(scw & 0x00f000f0u), m13 = as_h2(sh & 0x00f000f0u);
+      const half2v dm = as_h2(dmw);
+      // per-run scales: group i of this lane is run 4q + i of column c
+      float S = fmaf((float)s02.x, C[0] * kk.x, 0.f);
+      S = fmaf((float)s13.x, C[1] * kk.y, S);
+      S = fmaf((float)s02.y, C[2] * kk.z, S);
+      S = fmaf((float)s13.y, C[3] * kk.w, S);
+      float Mn = fmaf((float)m02.x, xsum.x, 0.f);
+      Mn = fmaf((float)m13.x, xsum.y, Mn);
+      Mn = fmaf((float)m02.y, xsum.z, Mn);
+      Mn = fmaf((float)m13.y, xsum.w, Mn);
+      acc = fmaf((float)dm.x, S, acc);
+      acc = fmaf(-(float)dm.y * 1048576.0f, Mn, acc);
+    }
+    acc += __shfl_xor(acc, 16, kWave);
+    acc += __shfl_xor(acc, 32, kWave);
+    if (q == 0) part[wave * 16 + n] = acc;
+    __syncthreads();
+    // no barrier follows (as in gate/up): part is rewritten only after the
+    // next tile's first barrier, which these lanes also reach
+    if (tid < 16) {
+      float y = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) y += part[w * 16 + tid];
+      const size_t o = size_t(t) * 16 + tid;
+      const float base = (p.residual ? p.residual[o] : 0.f) + (p.ys ? p.ys[o] : 0.f);
+      p.out[o] = base + y;
+    }
+  }
+}
+
+inline bool down_covers(int I, int k) {
+  const int NB = I / kKBlock;
+  return I % kKBlock == 0 && NB == 8 && k >= 1 && k <= kMaxDownRanks;
+}
+
+inline size_t down_lds_bytes(int I) {
+  const int rb = I / kKBlock * kQ2Bytes;
+  return size_t(kMaxDownRanks * run_stage_words(I) + 4) * 4 +
+         size_t(kMaxDownRanks * 16) * (rb + kRowPad) + size_t(kWaves * 16) * 4 +
+         size_t(kMaxDownRanks) * 4;
 }
 
 // True when the kernel has an instance for a layer of width H: NB = H / 256
