@@ -1,10 +1,16 @@
-"""Parity of the opt-in one-token gate/up ring kernel (INFERNO_DECODE_RING=1).
+"""Parity of the non-default one-token decode variants.
 
-The switch is read once per process, so tests/test_gpu_parity.py runs this
-file in a child process with the variable set: c2 (Q2_K routed + Q8_0
-shared, H 6144) and c4 layer 0 (Q2_K, H 4096, top-10, 1536-row shared
-expert), each checked for bitwise reproducibility over three calls and
-against the oracle (same tolerance as the other layer tests).
+The decode path switches (INFERNO_DECODE_MFMA, INFERNO_DECODE_RING) are read
+once per process, so tests/test_gpu_parity.py runs this file in a child
+process per variant:
+  tiles  INFERNO_DECODE_MFMA=0: the packed-f16 tile kernels for gate/up and
+         down (the default for layers the MFMA kernels do not cover);
+  ring   INFERNO_DECODE_MFMA=0 INFERNO_DECODE_RING=1: the opt-in LDS-ring
+         gate/up.
+Each runs c2 (Q2_K routed + Q8_0 shared, H 6144) and c4 layer 0 (Q2_K, H
+4096, top-10, 1536-row shared expert), checked for bitwise reproducibility
+over three calls and against the oracle (same tolerance as the other layer
+tests).
 """
 import os
 import sys
@@ -33,17 +39,20 @@ def check(key):
     outs = [lt.layer.forward(x, residual, ids=ids, weights=w) for _ in range(3)]
     torch.cuda.synchronize()
     for o in outs[1:]:
-        assert torch.equal(outs[0], o), f"{key}: ring decode is not bitwise reproducible"
+        assert torch.equal(outs[0], o), f"{key}: {VARIANT} decode is not bitwise reproducible"
     ref, _, _, flips = ph.oracle_layer_tokens(cfg, lt, x, residual, np.arange(1),
                                               ph.to_np(ids).view(np.uint32), ph.to_np(w))
     res = ph.to_np(residual)
     err = rn.rel_l2(ph.to_np(outs[0]) - res, ref - res)
-    print(f"ring {key}: rel_l2(moe part)={err:.3e} near-tie tokens={flips}", flush=True)
+    print(f"{VARIANT} {key}: rel_l2(moe part)={err:.3e} near-tie tokens={flips}", flush=True)
     assert err < ph.TOL_REL_L2, f"{key}: rel_l2 {err}"
 
 
+VARIANT = sys.argv[1] if len(sys.argv) > 1 else "tiles"
+
 if __name__ == "__main__":
-    assert os.environ.get("INFERNO_DECODE_RING") == "1"
+    assert os.environ.get("INFERNO_DECODE_MFMA") == "0"
+    assert (os.environ.get("INFERNO_DECODE_RING") == "1") == (VARIANT == "ring")
     for key in ("c2", "c4"):
         check(key)
-    print("ring ok")
+    print(f"{VARIANT} ok")

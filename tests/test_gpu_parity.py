@@ -279,7 +279,7 @@ def test_rms_norm(cuda):
 
 
 def _layer_parity(cuda, key, T, tokens=None):
-    cfg = cf.CONFIGS[key]
+    cfg = cf.CONFIGS[key] if isinstance(key, str) else key
     lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
     x = cf.make_input(cfg, T, device=cuda)
     residual = torch.randn(T, cfg.hidden, device=cuda)
@@ -305,6 +305,17 @@ def test_layer_c1_q4k_softmax(cuda, T):
 
 def test_layer_c2_glm_q2k_decode_full_size(cuda):
     _layer_parity(cuda, "c2", 1)
+
+
+# One-token Q2_K bf16 layers of other shapes: the MFMA gate/up at 4, 8 and 12
+# super-block columns, the MFMA down (I = 2048) with 4 ranks, the tile-kernel
+# down after the MFMA gate/up (I != 2048), with and without a shared expert.
+@pytest.mark.parametrize("H,E,I,k,Is", [(1024, 16, 2048, 4, 256), (2048, 32, 512, 8, 0),
+                                        (3072, 16, 1024, 6, 512)])
+def test_layer_q2k_decode_mfma_shapes(cuda, H, E, I, k, Is):
+    cfg = cf.Config(f"q2k_decode_h{H}_e{E}_i{I}_k{k}_s{Is}", 20 + H // 1024, H, E, I, k,
+                    (cf.Q2_K,), cf.SCORE_SIGMOID, True, 2.5, 0.1, Is, torch.bfloat16, (1,))
+    _layer_parity(cuda, cfg, 1)
 
 
 def test_layer_c3_glm_q3k_prefill_sampled_tokens(cuda):
@@ -355,15 +366,22 @@ def test_layer_c4_laguna_q2k_q3k_layers(cuda, T):
         assert err < ph.TOL_REL_L2
 
 
-def test_layer_decode_ring_opt_in(cuda):
-    """The opt-in LDS-ring gate/up (INFERNO_DECODE_RING=1) in a child process."""
+@pytest.mark.parametrize("variant", ["tiles", "ring"])
+def test_layer_decode_variants(cuda, variant):
+    """The non-default one-token decode paths in a child process each (the
+    switches are read once per process): the packed-f16 tile kernels
+    (INFERNO_DECODE_MFMA=0) and the opt-in LDS-ring gate/up
+    (INFERNO_DECODE_RING=1 on top of that)."""
     import os
     import subprocess
     import sys
     from pathlib import Path
-    env = dict(os.environ, INFERNO_DECODE_RING="1")
-    script = Path(__file__).resolve().parent / "ring_decode_check.py"
-    r = subprocess.run([sys.executable, "-u", str(script)], env=env, capture_output=True,
-                       text=True, timeout=240)
+    env = dict(os.environ, INFERNO_DECODE_MFMA="0")
+    env.pop("INFERNO_DECODE_RING", None)
+    if variant == "ring":
+        env["INFERNO_DECODE_RING"] = "1"
+    script = Path(__file__).resolve().parent / "decode_variant_check.py"
+    r = subprocess.run([sys.executable, "-u", str(script), variant], env=env,
+                       capture_output=True, text=True, timeout=240)
     print(r.stdout[-2000:], r.stderr[-2000:])
-    assert r.returncode == 0 and "ring ok" in r.stdout
+    assert r.returncode == 0 and f"{variant} ok" in r.stdout
