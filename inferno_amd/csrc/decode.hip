@@ -684,10 +684,10 @@ int launch_gate_up_mfma(hipStream_t s, const DecodeArgs& a0) {
   }
 }
 
-template <int PER>
+template <int TR, int PER>
 int launch_down_mfma_per(hipStream_t s, const DecodeArgs& a) {
   static bool attr = false;
-  auto* kern = mfma_decode::down_q2k_kernel<8, PER>;
+  auto* kern = mfma_decode::down_q2k_kernel<8, TR, PER>;
   if (!attr) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                             160 * 1024) != hipSuccess) {
@@ -696,24 +696,33 @@ int launch_down_mfma_per(hipStream_t s, const DecodeArgs& a) {
     }
     attr = true;
   }
-  const int ntiles = a.H / kRows;
+  const int ntiles = a.H / TR;
   const unsigned grid = unsigned(std::min(ntiles, device_cus()));
   kern<<<grid, mfma_decode::kThreads, mfma_decode::down_lds_bytes(a.I), s>>>(a, ntiles);
   INF_LAUNCHED();
   return INFERNO_OK;
 }
 
-// Routed down for one token on the MFMA kernel (I = 2048: 8 super-block
-// columns; k <= 8 ranks).
-int launch_down_mfma(hipStream_t s, const DecodeArgs& a) {
-  switch (mfma_decode::down_chunks_per_thread(8, a.k)) {
-    case 1: return launch_down_mfma_per<1>(s, a);
-    case 2: return launch_down_mfma_per<2>(s, a);
-    case 3: return launch_down_mfma_per<3>(s, a);
-    case 4: return launch_down_mfma_per<4>(s, a);
-    case 5: return launch_down_mfma_per<5>(s, a);
-    default: return launch_down_mfma_per<6>(s, a);
+template <int TR>
+int launch_down_mfma_tr(hipStream_t s, const DecodeArgs& a) {
+  switch (mfma_decode::down_chunks_per_thread(8, a.k, TR)) {
+    case 1: return launch_down_mfma_per<TR, 1>(s, a);
+    case 2: return launch_down_mfma_per<TR, 2>(s, a);
+    case 3: return launch_down_mfma_per<TR, 3>(s, a);
+    case 4: return launch_down_mfma_per<TR, 4>(s, a);
+    case 5: return launch_down_mfma_per<TR, 5>(s, a);
+    default: return launch_down_mfma_per<TR, 6>(s, a);
   }
+}
+
+// Routed down for one token on the MFMA kernel (I = 2048: 8 super-block
+// columns; k <= 8 ranks). 12-row tiles when they split H into a whole
+// number of rounds of one tile per CU, else 16-row tiles.
+int launch_down_mfma(hipStream_t s, const DecodeArgs& a) {
+  const int cus = device_cus();
+  if (a.H % 12 == 0 && (a.H / 12) % cus == 0 && (a.H / 16) % cus != 0)
+    return launch_down_mfma_tr<12>(s, a);
+  return launch_down_mfma_tr<16>(s, a);
 }
 
 }  // namespace

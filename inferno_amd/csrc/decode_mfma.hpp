@@ -313,31 +313,36 @@ __global__ void __launch_bounds__(kThreads) gate_up_q2k_kernel(DecodeArgs p, int
 
 constexpr int kMaxDownRanks = 8;
 
-__host__ __device__ constexpr int down_chunks_per_thread(int NB, int k) {
-  return (k * NB * kQ2Bytes + kThreads - 1) / kThreads;
+__host__ __device__ constexpr int down_chunks_per_thread(int NB, int k, int TR) {
+  return (k * TR * NB * kQ2Bytes / 16 + kThreads - 1) / kThreads;
 }
 
-template <int NB, int PER>
+template <int NB, int TR, int PER>
 __device__ __forceinline__ void fetch_down_tile(u32x4 (&v)[PER], const DecodeArgs& p, int k,
                                                 const uint32_t* rank_e, int t) {
-  constexpr int rb = NB * kQ2Bytes;  // bytes per row; chunks per rank tile = rb
-  const int tid = threadIdx.x, nv = k * rb;
+  constexpr int rb = NB * kQ2Bytes;   // bytes per row
+  constexpr int cr = TR * rb / 16;    // chunks per rank tile (TR rows)
+  const int tid = threadIdx.x, nv = k * cr;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     int i = j * kThreads + tid;
     i = i < nv ? i : nv - 1;  // clamped; the extra chunks are not stored
-    const int r = i / rb, w = i - r * rb;
+    const int r = i / cr, w = i - r * cr;
     const u32x4* src = reinterpret_cast<const u32x4*>(p.down + size_t(rank_e[r]) * p.down_stride +
-                                                      size_t(t) * 16 * rb);
+                                                      size_t(t) * TR * rb);
     v[j] = src[w];
   }
 }
 
-template <int NB, int PER>
+// TR output rows per tile: 16, or 12 so that H = 6144 makes 512 tiles, two
+// per workgroup on a 256-CU part (16-row tiles leave half the CUs a second
+// round); MFMA columns n >= TR read stale LDS rows and are not written.
+template <int NB, int TR, int PER>
 __global__ void __launch_bounds__(kThreads) down_q2k_kernel(DecodeArgs p, int ntiles) {
   extern __shared__ uint32_t smem[];
   constexpr int K = NB * kKBlock;  // the expert intermediate I
   constexpr int rb = NB * kQ2Bytes, RS = rb + kRowPad, Sh = run_stage_words(K);
+  constexpr int cr = TR * rb / 16;
   const int k = p.k, H = p.H;
   uint32_t* hs = smem;                             // [k][Sh]
   uint32_t* zero = hs + kMaxDownRanks * Sh;
@@ -351,7 +356,7 @@ __global__ void __launch_bounds__(kThreads) down_q2k_kernel(DecodeArgs p, int nt
   u32x4 v[PER];
   int t = blockIdx.x;
   __syncthreads();
-  if (t < ntiles) fetch_down_tile<NB, PER>(v, p, k, rank_e, t);
+  if (t < ntiles) fetch_down_tile<NB, TR, PER>(v, p, k, rank_e, t);
   for (int i = tid; i < k * Sh / 4; i += kThreads)
     reinterpret_cast<uint4*>(hs)[i] = reinterpret_cast<const uint4*>(p.stage_h)[i];
   if (tid < 4) zero[tid] = 0;
@@ -362,13 +367,13 @@ __global__ void __launch_bounds__(kThreads) down_q2k_kernel(DecodeArgs p, int nt
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int i = j * kThreads + tid;
-      if (i < k * rb) {
-        const int r = i / rb, w = i - r * rb, row = w / (rb / 16), c16 = w - row * (rb / 16);
+      if (i < k * cr) {
+        const int r = i / cr, w = i - r * cr, row = w / (rb / 16), c16 = w - row * (rb / 16);
         *reinterpret_cast<u32x4*>(tl + (r * 16 + row) * RS + c16 * 16) = v[j];
       }
     }
     __syncthreads();
-    if (t + int(gridDim.x) < ntiles) fetch_down_tile<NB, PER>(v, p, k, rank_e, t + gridDim.x);
+    if (t + int(gridDim.x) < ntiles) fetch_down_tile<NB, TR, PER>(v, p, k, rank_e, t + gridDim.x);
     float acc = 0.f;
     for (int b = wave; b < nblk; b += kWaves) {
       const int r = b / NB, c = b - r * NB;
@@ -423,11 +428,11 @@ __global__ void __launch_bounds__(kThreads) down_q2k_kernel(DecodeArgs p, int nt
     __syncthreads();
     // no barrier follows (as in gate/up): part is rewritten only after the
     // next tile's first barrier, which these lanes also reach
-    if (tid < 16) {
+    if (tid < TR) {
       float y = 0.f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) y += part[w * 16 + tid];
-      const size_t o = size_t(t) * 16 + tid;
+      const size_t o = size_t(t) * TR + tid;
       const float base = (p.residual ? p.residual[o] : 0.f) + (p.ys ? p.ys[o] : 0.f);
       p.out[o] = base + y;
     }

@@ -289,33 +289,45 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GemmOc
       acc1[tb][v] = 0.f;
     }
   }
-  // two register sets for the quant bytes: chunk qc uses set qc & 1, while
-  // the next chunk's bytes land in the other
-  uint32_t ra0[F::kRaw], ra1[F::kRaw], rb0[F::kRaw], rb1[F::kRaw];
+  // PD + 1 register sets for the quant bytes: chunk g (= 4 kb + qc) uses
+  // set qc % (PD + 1), and the loads of chunk g + PD are in flight while it
+  // is computed. PD = 3 keeps ~3x the bytes in flight; the two formats with
+  // the most raw words per chunk would spill at 128 tokens and keep PD = 1.
+  constexpr int PD = (NMAT == 2 && TM == 128 && (Q == INFERNO_Q3_K || Q == INFERNO_Q8_0)) ? 1 : 3;
+  constexpr int NS = PD + 1;
+  uint32_t ra[NS][F::kRaw], rb[NS][F::kRaw];
   const int nkb = K / kUnit;
+  const int nch = 4 * nkb;
   load_x(0);
-  F::load(w0, 0, kg, ra0);
-  if constexpr (NMAT == 2) F::load(w1, 0, kg, ra1);
+#pragma unroll
+  for (int g = 0; g < PD; ++g) {
+    if (g < nch) {
+      F::load(w0 + size_t(g / 4) * F::kBytes, g & 3, kg, ra[g % NS]);
+      if constexpr (NMAT == 2) F::load(w1 + size_t(g / 4) * F::kBytes, g & 3, kg, rb[g % NS]);
+    }
+  }
   store_x(0);
   __syncthreads();
 
-  auto step = [&](auto qc_c, int kb, uint32_t (&c0r)[F::kRaw], uint32_t (&c1r)[F::kRaw],
-                  uint32_t (&n0r)[F::kRaw], uint32_t (&n1r)[F::kRaw]) {
+  auto step = [&](auto qc_c, int kb) __attribute__((always_inline)) {
     constexpr int QC = decltype(qc_c)::value;
     constexpr int buf = QC & 1;
+    constexpr int PQ = (QC + PD) & 3;          // chunk of chunk g + PD within its block
+    constexpr int PS = (QC + PD) % NS;         // its register set
+    constexpr int CS = QC % NS;                // this chunk's register set
     const int st = 4 * kb + QC;
-    const bool more = QC < 3 || kb + 1 < nkb;
-    if (more) {
-      load_x(st + 1);
-      const size_t boff = size_t(QC < 3 ? kb : kb + 1) * F::kBytes;
-      F::load(w0 + boff, (QC + 1) & 3, kg, n0r);
-      if constexpr (NMAT == 2) F::load(w1 + boff, (QC + 1) & 3, kg, n1r);
+    const bool more = st + 1 < nch;
+    if (more) load_x(st + 1);
+    if (st + PD < nch) {
+      const size_t boff = size_t(kb + (QC + PD) / 4) * F::kBytes;
+      F::load(w0 + boff, PQ, kg, ra[PS]);
+      if constexpr (NMAT == 2) F::load(w1 + boff, PQ, kg, rb[PS]);
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const half8 a0 = F::template get<QC>(c0r, s);
+      const half8 a0 = F::template get<QC>(ra[CS], s);
       half8 a1;
-      if constexpr (NMAT == 2) a1 = F::template get<QC>(c1r, s);
+      if constexpr (NMAT == 2) a1 = F::template get<QC>(rb[CS], s);
 #pragma unroll
       for (int tb = 0; tb < NB; ++tb) {
         const half8 b = *reinterpret_cast<const half8*>(xs(buf, tb * 32 + i) + 16 * s + 8 * kg);
@@ -328,10 +340,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GemmOc
     __syncthreads();
   };
   for (int kb = 0; kb < nkb; ++kb) {
-    step(std::integral_constant<int, 0>{}, kb, ra0, ra1, rb0, rb1);
-    step(std::integral_constant<int, 1>{}, kb, rb0, rb1, ra0, ra1);
-    step(std::integral_constant<int, 2>{}, kb, ra0, ra1, rb0, rb1);
-    step(std::integral_constant<int, 3>{}, kb, rb0, rb1, ra0, ra1);
+    step(std::integral_constant<int, 0>{}, kb);
+    step(std::integral_constant<int, 1>{}, kb);
+    step(std::integral_constant<int, 2>{}, kb);
+    step(std::integral_constant<int, 3>{}, kb);
   }
 
   // accumulator element v of lane (i, kg): weight row 8 (v / 4) + 4 kg + v % 4
