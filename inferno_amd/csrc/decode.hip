@@ -163,14 +163,14 @@ __device__ __forceinline__ void sum_partials(const DecodeArgs& p, int t, float* 
   }
 }
 
-// The Q8_0 shared expert's down for output rows [32 g, 32 g + 32) of the one
+// The Q8_0 shared expert's down for output rows [16 g, 16 g + 16) of the one
 // token (MFMA down path), run by a workgroup of the select launch: it only
 // needs the shared gate/up partial sums of the route launch. Each workgroup
 // forms the shared h row itself (partials summed in part order, h = silu(g)
 // * u) and stages it into its LDS, so no workgroup depends on another; then
-// four 8-row groups with the lane split and summation order of the shared
+// two 8-row groups with the lane split and summation order of the shared
 // part of down8_kernel. Writes ys.
-constexpr int kSharedDownRows = 32;
+constexpr int kSharedDownRows = 16;
 __device__ __forceinline__ void shared_down_rows(const DecodeArgs& p, int g) {
   using FS = Fmt<INFERNO_Q8_0>;
   extern __shared__ uint32_t smem[];

@@ -39,10 +39,11 @@ __device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
 
 // Exact top-k of one token's logits by one full wavefront (lane holds
 // experts lane, lane+64, lane+128, lane+192). `row` may live in global
-// memory or LDS. Each round takes the largest (selection key, lowest id):
-// a wavefront max of the f32 total-order key, then among the lanes holding
-// that key a max of ~id. Lane 0 stores the results; every lane also gets
-// the selected ids in rank order in `sel_id` (wave-uniform).
+// memory or LDS. The order is (selection key desc by the f32 total order,
+// id asc); the k-th best is found by a bit-serial search with ballot counts
+// and the selected k are ranked against each other. Lanes 0..k-1 store the
+// results at their ranks; every lane also gets the selected ids in rank
+// order in `sel_id` (wave-uniform).
 __device__ __forceinline__ void topk_row_wave(const float* row, const float* __restrict__ bias,
                                               int E, int k, int score_fn, int norm, float scale,
                                               int t, uint32_t* __restrict__ ids,
@@ -88,67 +89,83 @@ __device__ __forceinline__ void topk_row_wave(const float* row, const float* __r
     for (int j = 0; j < PER; ++j) part += score[j];
     denom_all = wave_sum(part);
   }
-  float sel_score[kMaxTopK];
+  // Selection without k dependent rounds. Every candidate gets a distinct
+  // 41-bit rank key: live bit 40 | selection key << 8 | (255 - id), so a
+  // larger value is a better (key desc, id asc) candidate. A bit-serial
+  // search finds the k-th largest value: for each bit from the top, keep it
+  // set if at least k candidates are at or above the prefix so far (ballot
+  // counts). The candidates at or above it are exactly the top k.
+  uint64_t rk[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t e = uint32_t(lane + j * kWave);
+    rk[j] = live[j] ? ((uint64_t(1) << 40) | (uint64_t(key[j]) << 8) | uint64_t(255u - (e & 255u)))
+                    : 0;
+  }
+  uint64_t kth = uint64_t(1) << 40;  // at least k candidates are live (k <= E)
+  for (int bit = 39; bit >= 0; --bit) {
+    const uint64_t cand = kth | (uint64_t(1) << bit);
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) cnt += uint32_t(__popcll(__ballot(rk[j] >= cand)));
+    if (cnt >= uint32_t(k)) kth = cand;
+  }
+  // the selected candidates, gathered in lane order into lanes 0..k-1
+  // (source lanes are wavefront-uniform: readlane, no LDS round trips)
+  auto rd32 = [](uint32_t v, int src) {
+    return uint32_t(__builtin_amdgcn_readlane(int(v), src));
+  };
+  uint64_t my_rk = 0;
+  uint32_t my_id = 0xffffffffu;
+  float my_score = 0.f;
+  {
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      uint64_t m = __ballot(rk[j] >= kth);
+      while (m) {
+        const int src = __builtin_ctzll(m);
+        m &= m - 1;
+        const uint64_t r = (uint64_t(rd32(uint32_t(rk[j] >> 32), src)) << 32) |
+                           rd32(uint32_t(rk[j]), src);
+        const float sc = __uint_as_float(rd32(__float_as_uint(score[j]), src));
+        if (lane == n) {
+          my_rk = r;
+          my_id = uint32_t(src + j * kWave);
+          my_score = sc;
+        }
+        ++n;
+      }
+    }
+  }
+  // rank of each selected candidate among the k (0 = best)
+  uint32_t rank = 0;
+  for (int i = 0; i < k; ++i) {
+    const uint64_t o = (uint64_t(rd32(uint32_t(my_rk >> 32), i)) << 32) | rd32(uint32_t(my_rk), i);
+    rank += o > my_rk ? 1u : 0u;
+  }
+  const bool mine = lane < k;
+  // rank order: ids for the callers, scores summed in rank order
+  float sum = 0.f;
 #pragma unroll
   for (int r = 0; r < kMaxTopK; ++r) {
     sel_id[r] = 0xffffffffu;
-    sel_score[r] = 0.f;
-  }
-#pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r) {
     if (r < k) {
-      // this lane's best live candidate: highest key, lowest id (j ascending = id ascending)
-      uint32_t bk = 0, bj = 0;
-      bool any = false;
-#pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        if (live[j] && (!any || key[j] > bk)) {
-          bk = key[j];
-          bj = uint32_t(j);
-          any = true;
-        }
-      }
-      const uint32_t mk = wave_umax(any ? bk : 0u);
-      const uint32_t my_id = uint32_t(lane) + bj * kWave;
-      const uint32_t inv = wave_umax((any && bk == mk) ? ~my_id : 0u);
-      const uint32_t id = ~inv;
-      const int owner = int(id & 63u), slot = int(id >> 6);
-      float mine = score[0];
-#pragma unroll
-      for (int j = 1; j < PER; ++j)
-        if (j == slot) mine = score[j];
-      const float s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                    __builtin_bit_cast(int, mine), owner));
-      if (lane == owner) {
-#pragma unroll
-        for (int j = 0; j < PER; ++j)
-          if (j == slot) live[j] = false;
-      }
-      sel_score[r] = s;
-      sel_id[r] = id;
+      const uint64_t at = __ballot(mine && rank == uint32_t(r));
+      const int src = __builtin_ctzll(at);
+      sel_id[r] = rd32(my_id, src);
+      if (norm) sum += __uint_as_float(rd32(__float_as_uint(my_score), src));
     }
   }
-  if (lane == 0) {
-    float sum = 0.f;
-    if (norm) {
-#pragma unroll
-      for (int r = 0; r < kMaxTopK; ++r)
-        if (r < k) sum += sel_score[r];
-    } else if (score_fn == INFERNO_SCORE_SOFTMAX) {
-      sum = denom_all;
-    }
-    const bool divide = (norm || score_fn == INFERNO_SCORE_SOFTMAX) && sum > 0.f && isfinite(sum);
-#pragma unroll
-    for (int r = 0; r < kMaxTopK; ++r) {
-      if (r < k) {
-        float wv = sel_score[r];
-        if (divide) wv /= sum;
-        const size_t a = size_t(t) * k + r;
-        ids[a] = sel_id[r];
-        weights[a] = wv * scale;
-        if (token_idx) token_idx[a] = uint32_t(t);
-      }
-    }
+  if (!norm && score_fn == INFERNO_SCORE_SOFTMAX) sum = denom_all;
+  const bool divide = (norm || score_fn == INFERNO_SCORE_SOFTMAX) && sum > 0.f && isfinite(sum);
+  if (mine) {
+    float wv = my_score;
+    if (divide) wv /= sum;
+    const size_t a = size_t(t) * k + rank;
+    ids[a] = my_id;
+    weights[a] = wv * scale;
+    if (token_idx) token_idx[a] = uint32_t(t);
   }
 }
 
