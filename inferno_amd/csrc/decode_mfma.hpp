@@ -1,33 +1,30 @@
-// Decode gate/up of the routed Q2_K experts for one token on the matrix
-// cores (v_mfma_f32_16x16x32_f16), with every 16-row tile read from HBM as
-// one contiguous range and staged in LDS.
+// Decode GEMVs of the routed Q2_K experts for one token on the matrix
+// cores, with every 16-row tile read from HBM as one contiguous range and
+// staged in LDS.
 //
-// The dot product of a 16-row tile over one super-block column is one
-// MFMA tile C[m][n] = sum_k A[m][k] B[k][n]:
-//   B (weights): lane (row n, k-quarter kq) holds the 16 qs bytes
-//     qs[16 kq .. 16 kq + 15] of its row's block, i.e. the 16 values i of the
-//     Q2_K groups (h = kq >> 1, s = kq & 1) at all four bit planes p. A 2-bit
-//     field masked in place out of a 32-bit word (bits 2p and 16 + 2p) is a
-//     pair of exact f16 subnormals q * 2^(2p - 24), so one v_and_b32 yields
-//     two B operand values. MFMA (p, half) takes values i in [8 half, 8 half
-//     + 8) of every lane's plane p, in the order 0 2 1 3 4 6 5 7.
+// gate/up (v_mfma_scale_f32_16x16x128_f8f6f4, fp8 x fp4): the dot product
+// of a 16-row tile over one super-block column is one MFMA tile C[m][n] =
+// sum_k A[m][k] B[k][n] in two K halves (the bit planes 0, 2 and 1, 3):
+//   B (weights): lane (row n, lane group kq) holds the 16 qs bytes
+//     qs[16 kq .. 16 kq + 15] of its row's block. A 2-bit field in the low
+//     two bits of a nibble is the fp4 (e2m1) value q / 2, so one v_and_b32
+//     with 0x33333333 yields eight operand values (planes 0 and 2; after a
+//     shift by 2, planes 1 and 3).
 //   A (activations): row m of A is group m of the block (scale byte m,
-//     m = 8h + 2p + s). A[m][k] holds x for the k that belong to group m and
-//     zero elsewhere, so the MFMA leaves each group's 16-value dot product in
-//     its own row of C: C[m][n] = sum_i q(n, m, i) x(m, i) (scaled). Only the
-//     lane (m, kq = 2h + s) is non-zero, in MFMA (p(m), half) for both
-//     halves; every other lane reads a zero block.
+//     m = 8h + 2p + s), holding x only in the K positions of that group, so
+//     each group's 16-value dot product lands in its own row of C. x is two
+//     e4m3 terms (two MFMAs per B, E8M0 scales 2^e1 and 2^(e1 - 4)).
+//   Operand K layout (gfx950, measured): A lane group qa holds k = 16 qa + t
+//     in bytes t < 16 and k = 64 + 16 qa + t in bytes 16 + t; B lane group q
+//     holds k = 32 q + nibble.
 //   C: lane (kq, n) holds groups 4kq .. 4kq + 3 of row n, whose scale bytes
 //     are the kq-th dword of the block's scales. The group scale and minimum
 //     enter with v_fma_mix: the 4-bit scale and min nibbles masked in place
-//     are f16 subnormals too, so no byte-to-float conversion is needed.
+//     are f16 subnormals, so no byte-to-float conversion is needed.
 //
-// Activations are staged per 256-value column as f16 x * s_c * 4^-p(run)
-// (s_c a power of two putting the column's max|x| in [2^14, 2^15); the 4^-p
-// undoes the bit plane's 4^p, so every group of a column has the same scale),
-// plus the unscaled run sums (for the Q2_K minimum) and 2^48 / s_c per
-// column. bf16 inputs are exact in this form except for values below
-// max|x| * 2^-28 of their column.
+// down (v_mfma_f32_16x16x32_f16): the same block-diagonal A with f16 h (a
+// masked 2-bit field at bits 2p and 16 + 2p is a pair of exact f16
+// subnormals q 2^(2p - 24)), per-run scales of h.
 //
 // Reference semantics: dequantize_q2_k_block (crates/gguf/src/lib.rs:
 // 1226-1293): value = (d * (sc & 15)) * q - dmin * (sc >> 4); gate/up with
@@ -51,48 +48,93 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
 
 constexpr int kWaves = 16;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kQ2Bytes = 84;
 constexpr int kRowPad = 16;    // LDS row padding (bytes): rows start on distinct banks
 
-// Staged row (words): [pairs K/2][run sums K/16][column factors K/256], padded to 4.
-__host__ __device__ constexpr int stage_words(int K) { return (K / 2 + K / 16 + K / 256 + 3) & ~3; }
+// ---------------------------------------------------------- x staging
+//
+// The gate/up kernel multiplies fp4 weights (below) by fp8 activations:
+// x = 2^e1 * (t1 + t2 / 16), t1 = e4m3(x 2^-e1), t2 = e4m3(16 (x 2^-e1 - t1)),
+// with one e1 per 256-value column putting its max|x| in [128, 256). Two
+// e4m3 terms carry a bf16 value exactly (8 significant bits) unless it lies
+// below ~max|x| 2^-17 of its column. Staged row (words), per token:
+//   [column images K/256 x 256][run sums K/16][column exponents K/256], padded to 4.
+// A column image is [term 2][group m 16][half 2] x 16 bytes laid out for the
+// A operand of v_mfma_scale_f32_16x16x128_f8f6f4 (see gate_up_q2k_kernel):
+// byte t of (m, half) holds value i = 4 j + b of group m, j = 2 half + t / 8,
+// b = (t % 8) / 2, when t % 2 == p(m) >> 1, and 0 otherwise.
+
+__host__ __device__ constexpr int stage_words(int K) { return (K + K / 16 + K / 256 + 3) & ~3; }
+
+// e4m3 (OCP, bias 7, max 448) of a float, round to nearest even; |f| here
+// stays below 256, so no saturation case arises.
+__device__ __forceinline__ uint32_t to_e4m3(float f) {
+  const uint32_t sign = f < 0.f ? 0x80u : 0u;
+  const float a = fabsf(f);
+  if (!(a >= 0.0009765625f)) return sign;  // below half the smallest subnormal (2^-9); NaN -> 0
+  int e;
+  frexpf(a, &e);  // a = f 2^e, f in [0.5, 1): a = 1.m 2^(e-1)
+  int E = e - 1;
+  if (E < -6) return sign | uint32_t(rintf(a * 512.f));  // subnormal: units of 2^-9 (8 = 0x08)
+  float mant = rintf(ldexpf(a, 3 - E));  // in [8, 16]
+  if (mant >= 16.f) {
+    mant = 8.f;
+    E += 1;
+  }
+  if (E > 8) return sign | 0x7eu;
+  return sign | (uint32_t(E + 7) << 3) | (uint32_t(mant) - 8u);
+}
+__device__ __forceinline__ float from_e4m3(uint32_t b) {
+  const float s = (b & 0x80u) ? -1.f : 1.f;
+  const uint32_t E = (b >> 3) & 15u, M = b & 7u;
+  if (E == 0) return s * float(M) * (1.f / 512.f);
+  return s * ldexpf(1.f + float(M) * 0.125f, int(E) - 7);
+}
 
 // Stages super-block column `col` of one bf16 row into `row` (the layout
-// above); one full wavefront, lane l holding values 4l .. 4l + 3.
+// above); one full wavefront, lane l holding values 4l .. 4l + 3 (group
+// m = l / 4, quarter u = l % 4 of it).
 __device__ __forceinline__ void stage_column(const uint16_t* x, uint32_t* row, int K, int col) {
   const int lane = threadIdx.x & 63;
   float v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = bf16_bits_to_f32(x[col * kKBlock + 4 * lane + i]);
-  float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
-  float s = 1.0f;  // zero or non-finite columns keep scale 1
-  if (m > 0.f && m < 3.0e38f) {
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  int e1 = 0;  // zero or non-finite columns keep exponent 0
+  if (mx > 0.f && mx < 3.0e38f) {
     int e;
-    frexpf(m, &e);
-    s = ldexpf(1.0f, 15 - e);
+    frexpf(mx, &e);
+    e1 = e - 8;
   }
-  const int run = lane >> 2;                 // 16-value run of this lane
-  const int p = (run >> 1) & 3;              // its bit plane
-  const float f = s * ldexpf(1.0f, -2 * p);
+  const int m = lane >> 2, u = lane & 3, e = (m >> 2) & 1;
+  uint32_t w[2][2] = {{0u, 0u}, {0u, 0u}};  // [term][word]: bytes 2b + e of this quarter
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const float a = ldexpf(v[b], -e1);
+    const uint32_t b1 = to_e4m3(a);
+    const uint32_t b2 = to_e4m3((a - from_e4m3(b1)) * 16.f);
+    const int sh = 16 * (b & 1) + 8 * e;
+    w[0][b >> 1] |= b1 << sh;
+    w[1][b >> 1] |= b2 << sh;
+  }
+  uint32_t* img = row + col * 256 + m * 8 + (u >> 1) * 4 + (u & 1) * 2;
+#pragma unroll
+  for (int tm = 0; tm < 2; ++tm) {
+    img[tm * 128] = w[tm][0];
+    img[tm * 128 + 1] = w[tm][1];
+  }
   float sum = (v[0] + v[1]) + (v[2] + v[3]);
   sum += __shfl_xor(sum, 1, kWave);
   sum += __shfl_xor(sum, 2, kWave);
-  // words 2u, 2u + 1 of the run (u = lane & 3): values (4u, 4u + 2), (4u + 1, 4u + 3)
-  auto pack = [&](float a, float b) {
-    const _Float16 ah = (_Float16)(a * f), bh = (_Float16)(b * f);
-    return uint32_t(__builtin_bit_cast(uint16_t, ah)) | (uint32_t(__builtin_bit_cast(uint16_t, bh)) << 16);
-  };
-  uint32_t* pairs = row + col * 128 + run * 8 + 2 * (lane & 3);
-  pairs[0] = pack(v[0], v[2]);
-  pairs[1] = pack(v[1], v[3]);
-  float* sums = reinterpret_cast<float*>(row + K / 2);
-  if ((lane & 3) == 0) sums[col * 16 + run] = sum;
-  if (lane == 0) sums[K / 16 + col] = 16777216.0f * 16777216.0f / s;
+  float* sums = reinterpret_cast<float*>(row + K);
+  if (u == 0) sums[col * 16 + m] = sum;
+  if (lane == 0) reinterpret_cast<int*>(row + K + K / 16)[col] = e1;
 }
 
 // Stages one 16-value run held one value per lane by lanes 0..15 (lane i
@@ -204,11 +246,14 @@ __global__ void __launch_bounds__(kThreads) gate_up_q2k_kernel(DecodeArgs p, int
       stage_run_lanes(silu(g) * u, p.stage_hs, p.Is, st);
     }
   }
-  // A operand: lane (m = n, kq = q) is live iff kq == 2h + s of group m
-  const bool act = q == 2 * (n >> 3) + (n & 1);
-  const int pm = (n >> 1) & 3;
-  const float* sums = reinterpret_cast<const float*>(xs + H / 2);
-  const float* colf = sums + H / 16;
+  // A operand (fp8 x): the group m of this lane's row sits in MFMA u =
+  // p(m) & 1 (the field planes 0, 2 or 1, 3 in B), in the two lanes whose K
+  // range covers B's lane group 2 (m >> 3) + (m & 1): kq >> 1 == m & 1, in
+  // operand bytes 16..31 for m >= 8; every other lane/MFMA reads zeros.
+  const bool act = (q >> 1) == (n & 1);
+  const int uact = (n >> 1) & 1, hi16 = n >> 3;
+  const float* sums = reinterpret_cast<const float*>(xs + H);
+  const int* e1s = reinterpret_cast<const int*>(xs + H + H / 16);
   for (; t < ntiles; t += gridDim.x) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
@@ -224,35 +269,40 @@ __global__ void __launch_bounds__(kThreads) gate_up_q2k_kernel(DecodeArgs p, int
     const int slot = t / tiles_i, tile = t - slot * tiles_i;
     float acc[2] = {0.f, 0.f};
     for (int c = wave; c < NB; c += kWaves) {
-      half8 A[4][2];
+      const uint32_t* img = xs + c * 256 + n * 8 + (q & 1) * 4;
+      v8i A[2][2];  // [term][u]
 #pragma unroll
-      for (int pp = 0; pp < 4; ++pp)
+      for (int tm = 0; tm < 2; ++tm)
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const uint32_t* src = (act && pp == pm) ? xs + c * 128 + n * 8 + 4 * hf : zero;
-          A[pp][hf] = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(src));
+        for (int u = 0; u < 2; ++u) {
+          const bool on = act && u == uact;
+          const uint32_t* lo = (on && !hi16) ? img + tm * 128 : zero;
+          const uint32_t* hi = (on && hi16) ? img + tm * 128 : zero;
+          const uint4 a0 = *reinterpret_cast<const uint4*>(lo);
+          const uint4 a1 = *reinterpret_cast<const uint4*>(hi);
+          A[tm][u] = v8i{int(a0.x), int(a0.y), int(a0.z), int(a0.w),
+                         int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
         }
       const float4 xsum = *reinterpret_cast<const float4*>(sums + c * 16 + 4 * q);
-      const float kc = colf[c];
+      const int sa1 = 127 + e1s[c], sa2 = sa1 - 4;  // E8M0 scales of the two x terms
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const uint8_t* blk = tl + (m * 16 + n) * RS + c * kQ2Bytes;
         const u32x4_a4 qs = *reinterpret_cast<const u32x4_a4*>(blk + 16 + 16 * q);
         const uint32_t scw = *reinterpret_cast<const uint32_t*>(blk + 4 * q);
         const uint32_t dmw = *reinterpret_cast<const uint32_t*>(blk + 80);
+        // B (fp4 weights): a 2-bit field in the low bits of a nibble is the
+        // e2m1 value q / 2; planes 0 (low nibble) and 2 (high nibble) in
+        // MFMA 0, planes 1 and 3 in MFMA 1
+        const uint32_t F = 0x33333333u;
+        const v8i B0 = v8i{int(qs.x & F), int(qs.y & F), int(qs.z & F), int(qs.w & F), 0, 0, 0, 0};
+        const v8i B1 = v8i{int((qs.x >> 2) & F), int((qs.y >> 2) & F), int((qs.z >> 2) & F),
+                           int((qs.w >> 2) & F), 0, 0, 0, 0};
         floatx4 C = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const uint32_t w0 = hf ? qs.z : qs.x, w1 = hf ? qs.w : qs.y;
-          const uint32_t o0 = w0 >> 8, o1 = w1 >> 8;
-#pragma unroll
-          for (int pp = 0; pp < 4; ++pp) {
-            const uint32_t M = 0x00030003u << (2 * pp);
-            const uint4 bv = make_uint4(w0 & M, o0 & M, w1 & M, o1 & M);
-            C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[pp][hf], __builtin_bit_cast(half8, bv), C,
-                                                       0, 0, 0);
-          }
-        }
+        C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][0], B0, C, 0, 4, 0, sa1, 0, 127);
+        C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][1], B1, C, 0, 4, 0, sa1, 0, 127);
+        C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][0], B0, C, 0, 4, 0, sa2, 0, 127);
+        C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][1], B1, C, 0, 4, 0, sa2, 0, 127);
         // scale nibbles (bytes 0, 2 | 1, 3) and min nibbles as f16 subnormal pairs
         const uint32_t sh = scw >> 8;
         const half2v s02 = as_h2(scw & 0x000f000fu), s13 = as_h2(sh & 0x000f000fu);
@@ -266,8 +316,9 @@ __global__ void __launch_bounds__(kThreads) gate_up_q2k_kernel(DecodeArgs p, int
         Mn = fmaf((float)m13.x, xsum.y, Mn);
         Mn = fmaf((float)m02.y, xsum.z, Mn);
         Mn = fmaf((float)m13.y, xsum.w, Mn);
-        // value = d * sc * q - dmin * m: S carries 2^-48 s_c, Mn carries 2^-20
-        acc[m] = fmaf((float)dm.x * kc, S, acc[m]);
+        // value = d * sc * q - dmin * m: C holds sum (q / 2) x, S carries
+        // 2^-24 (the scale nibble), Mn 2^-20 (the min nibble)
+        acc[m] = fmaf((float)dm.x * 33554432.0f, S, acc[m]);
         acc[m] = fmaf(-(float)dm.y * 1048576.0f, Mn, acc[m]);
       }
     }
