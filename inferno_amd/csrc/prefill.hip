@@ -27,6 +27,7 @@
 #include "prefill.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "gemv_common.hpp"
@@ -37,6 +38,7 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2a __attribute__((ext_vector_type(2), aligned(8)));
 
 constexpr int kUnit = 256;       // values per K unit (super-block / eight Q8_0 blocks)
 constexpr int kTileN = 128;      // weight rows per workgroup
@@ -67,6 +69,12 @@ __device__ __forceinline__ half8 dequant8(uint32_t w0, uint32_t w1, uint32_t mas
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
 
+// f16 half `hi` of w, exactly widened, times m plus c in fp32 (v_fma_mix_f32).
+__device__ __forceinline__ float mix_mul(uint32_t w, int hi, float m, float c) {
+  const half2v h = as_h2(w);
+  return __builtin_fmaf((float)h[hi], m, c);
+}
+
 // ------------------------------------------------------------- A fragments
 // A lane (row i, k half kg) dequantises, for 64-value chunk QC of a K unit
 // and k step s = 0..3, the values 64 QC + 16 s + 8 kg .. +8 of its row.
@@ -90,15 +98,21 @@ struct Frag<INFERNO_Q2_K> {
     r[4] = ld_u1(b + 4 * qc);  // scale bytes of groups 4 qc .. 4 qc + 3
     r[5] = ld_u1(b + 80);      // d | dmin
   }
+  // Group scale and min nibbles enter masked in place as f16 subnormals
+  // (n * 2^-24, byte s of r[4] in half s / 2 of the word shifted by 8 (s & 1))
+  // and one v_fma_mix_f32 each scales them by d * 2^(48 - 2p) and
+  // -dmin * 2^24: mult = sc d 2^(24 - 2p) and off = -m dmin, each rounded
+  // once as d * float(sc) is.
   template <int QC>
   __device__ static half8 get(const uint32_t r[kRaw], int s) {
     const int p = 2 * (QC & 1) + (s >> 1);
-    const uint32_t sc = byte_of(r[4], s);
+    const uint32_t sw = (s & 1) ? (r[4] >> 8) : r[4];
     const float d = f16_bits_to_f32_fast(uint16_t(r[5]));
     const float dmin = f16_bits_to_f32_fast(uint16_t(r[5] >> 16));
-    const float mult = __builtin_amdgcn_ldexpf(d * float(sc & 15u), 24 - 2 * p);
+    const float mult = mix_mul(sw & 0x000f000fu, s >> 1, __builtin_amdgcn_ldexpf(d, 48 - 2 * p), 0.0f);
+    const float off = mix_mul((sw >> 4) & 0x000f000fu, s >> 1, __builtin_amdgcn_ldexpf(-dmin, 24), 0.0f);
     return dequant8((s & 1) ? r[2] : r[0], (s & 1) ? r[3] : r[1], 0x00030003u << (2 * p), mult,
-                    -(dmin * float(sc >> 4)));
+                    off);
   }
 };
 
@@ -125,16 +139,28 @@ struct Frag<INFERNO_Q3_K> {
   __device__ static half8 get(const uint32_t r[kRaw], int s) {
     const int n = QC >> 1, jj = 2 * (QC & 1) + (s >> 1);
     const int hshift = 4 * n + jj;
-    // q + 4 hbit as a 3-bit field in every byte
-    const uint32_t w0 = ((((s & 1) ? r[2] : r[0]) >> (2 * jj)) & 0x03030303u) |
-                        (((((s & 1) ? r[6] : r[4]) >> hshift) & 0x01010101u) << 2);
-    const uint32_t w1 = ((((s & 1) ? r[3] : r[1]) >> (2 * jj)) & 0x03030303u) |
-                        (((((s & 1) ? r[7] : r[5]) >> hshift) & 0x01010101u) << 2);
-    const uint32_t lob = byte_of(r[8], s);
-    const uint32_t lo = QC < 2 ? (lob & 15u) : (lob >> 4);
-    const uint32_t hi = (byte_of(r[9], s) >> (2 * QC)) & 3u;
-    const float dl = f16_bits_to_f32_fast(uint16_t(r[10])) * float(int(lo | (hi << 4)) - 32);
-    return dequant8(w0, w1, 0x00070007u, __builtin_amdgcn_ldexpf(dl, 24), -4.0f * dl);
+    // q + 4 hbit as a 3-bit field at the bottom of every byte: bits 0-1
+    // from the shifted qs word, bit 2 (and higher bits, which the dequant
+    // mask drops) from the hmask word shifted to put bit hshift at bit 2:
+    // one bit-field insert (v_bfi_b32) per word
+    auto field3 = [&](uint32_t q, uint32_t h) {
+      const uint32_t qs = q >> (2 * jj);
+      const uint32_t hs = hshift >= 2 ? (h >> (hshift - 2)) : (h << (2 - hshift));
+      return (qs & 0x03030303u) | (hs & ~0x03030303u);
+    };
+    const uint32_t w0 = field3((s & 1) ? r[2] : r[0], (s & 1) ? r[6] : r[4]);
+    const uint32_t w1 = field3((s & 1) ? r[3] : r[1], (s & 1) ? r[7] : r[5]);
+    // the four 6-bit scales of this chunk, one per byte, then byte s as an
+    // f16 subnormal s6 * 2^-24; dl = d (s6 - 32): mult = dl 2^24 and
+    // off = -4 dl are each one v_fma_mix_f32 with an fp32 addend, rounded
+    // once as d * float(s6 - 32) is
+    const uint32_t lo = QC < 2 ? (r[8] & 0x0f0f0f0fu) : ((r[8] >> 4) & 0x0f0f0f0fu);
+    const uint32_t s6 = lo | (((r[9] >> (2 * QC)) & 0x03030303u) << 4);
+    const uint32_t f6 = ((s & 1) ? (s6 >> 8) : s6) & 0x00ff00ffu;
+    const float d = f16_bits_to_f32_fast(uint16_t(r[10]));
+    const float mult = mix_mul(f6, s >> 1, __builtin_amdgcn_ldexpf(d, 48), -32.0f * __builtin_amdgcn_ldexpf(d, 24));
+    const float off = mix_mul(f6, s >> 1, -4.0f * __builtin_amdgcn_ldexpf(d, 24), 128.0f * d);
+    return dequant8(w0, w1, 0x00070007u, mult, off);
   }
 };
 
@@ -375,6 +401,253 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GemmOc
   }
 }
 
+// ------------------------------------------------- LDS-staged weight GEMM
+// The same product for the K-quant formats whose super-block fits LDS twice
+// over at 512 rows (Q2_K, Q3_K), with two changes measured to matter more
+// than the dequantisation: (1) weights are fetched with contiguous dword
+// loads, each wavefront instruction covering whole super-blocks of two or
+// three rows, a quarter of the next K unit per 64-deep step, and stored to LDS, where every lane reads
+// its fragment; loading fragments straight from their rows touches 32 rows
+// per instruction and cost more than the token traffic; (2) a workgroup of
+// eight wavefronts covers 256 rows of each matrix, so each token tile
+// (TM x 64 f16 from LDS) feeds twice the rows of the four-wavefront kernel
+// (WAVES = 8; WAVES = 4 keeps two workgroups per CU).
+
+template <int Q>
+struct Stage;
+// Q2_K: 84 bytes = 21 words per row, rows 21 words apart in LDS (an odd
+// pitch: 32-bit fragment reads of 32 rows spread over the banks); three rows
+// per wavefront load instruction.
+template <>
+struct Stage<INFERNO_Q2_K> {
+  static constexpr int kWords = 21, kPitch = 21;
+  __device__ static int offset(int j, int& shift) {
+    shift = 0;
+    return 4 * j;
+  }
+  __device__ static void frag(const uint32_t* row, int qc, int kg, uint32_t r[6]) {
+    const int h = qc >> 1;
+    const uint32_t* a = row + 4 + 8 * h + 2 * kg;
+    r[0] = a[0]; r[1] = a[1]; r[2] = a[4]; r[3] = a[5];
+    r[4] = row[qc];
+    r[5] = row[20];
+  }
+};
+// Q3_K: 110 bytes per row; word 27 holds bytes 108..109 (d), read as the
+// dword at byte 106 shifted down 16 so no load passes the super-block.
+template <>
+struct Stage<INFERNO_Q3_K> {
+  static constexpr int kWords = 28, kPitch = 28;
+  __device__ static int offset(int j, int& shift) {
+    shift = j == 27 ? 16 : 0;
+    return j == 27 ? 106 : 4 * j;
+  }
+  __device__ static void frag(const uint32_t* row, int qc, int kg, uint32_t r[11]) {
+    const int n = qc >> 1;
+    const u32x2a qa = *reinterpret_cast<const u32x2a*>(row + 8 + 8 * n + 2 * kg);
+    const u32x2a qb = *reinterpret_cast<const u32x2a*>(row + 12 + 8 * n + 2 * kg);
+    const u32x2a ha = *reinterpret_cast<const u32x2a*>(row + 2 * kg);
+    const u32x2a hb = *reinterpret_cast<const u32x2a*>(row + 4 + 2 * kg);
+    r[0] = qa.x; r[1] = qa.y; r[2] = qb.x; r[3] = qb.y;
+    r[4] = ha.x; r[5] = ha.y; r[6] = hb.x; r[7] = hb.y;
+    r[8] = row[24 + (qc & 1)];
+    r[9] = row[26];
+    r[10] = row[27] & 0xffffu;
+  }
+};
+
+template <int Q, int NMAT, int TM, int WAVES>
+constexpr size_t gemm2_lds_bytes() {
+  return size_t(2) * TM * kLdsPitch * 2 + size_t(2) * 32 * WAVES * NMAT * Stage<Q>::kPitch * 4;
+}
+
+template <int Q, int NMAT, int TM, int PF, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
+    gemm2_kernel(GemmArgs p) {
+  using F = Frag<Q>;
+  using S = Stage<Q>;
+  constexpr int NB = TM / 32;
+  constexpr int NT = 64 * WAVES;        // threads
+  constexpr int TN = 32 * WAVES;        // weight rows per matrix
+  constexpr int R = TN * NMAT;          // staged weight rows
+  constexpr int RW = 32 * NMAT;         // rows staged by one wavefront
+  constexpr int RPI = 64 / S::kWords;   // rows per load instruction
+  constexpr int NI = (RW + RPI - 1) / RPI;
+  constexpr int XP = (TM * 8 + NT - 1) / NT;  // 16-byte token pieces per thread
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* xs_base = smem;
+  uint32_t* ws_base = reinterpret_cast<uint32_t*>(smem + 2 * TM * kLdsPitch);
+  auto xs = [&](int buf, int row) { return xs_base + (size_t(buf) * TM + row) * kLdsPitch; };
+  auto wsr = [&](int buf, int rr) { return ws_base + (size_t(buf) * R + rr) * S::kPitch; };
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, kg = lane >> 5;
+  uint32_t e = 0, c0, c1;
+  if (p.tiles) {
+    if (blockIdx.y >= *p.n_tiles) return;
+    const uint4 t = p.tiles[blockIdx.y];
+    e = t.x;
+    c0 = t.y;
+    c1 = t.z;
+  } else {
+    c0 = blockIdx.y * TM;
+    c1 = min(c0 + uint32_t(TM), p.rows);
+  }
+  const int n0 = blockIdx.x * TN;
+  const int K = p.K;
+  const size_t row_bytes = size_t(K / kUnit) * F::kBytes;
+
+  // weight staging: lane covers word j of row (lane / kWords) of each
+  // instruction's RPI rows; wavefront rows [wave RW, wave RW + RW) of the
+  // R staged rows (matrix (wave RW) / 256)
+  const int lrow = lane / S::kWords, j = lane - lrow * S::kWords;
+  int wshift;
+  const int woff = S::offset(j, wshift);
+  const bool wlane = lrow < RPI;
+  const int rr0 = wave * RW;
+  const uint8_t* wm = (NMAT == 2 && rr0 >= TN) ? p.w1 : p.w0;
+  const uint8_t* wsrc = wm + size_t(e) * p.stride + size_t(n0 + rr0 % TN + lrow) * row_bytes + woff;
+  // the next K unit is fetched in NP parts of NQ load instructions: PF = 1,
+  // a quarter per 64-deep step, stored at the end of that step; PF = 2,
+  // halves at steps 0 and 1, each stored two steps later (more registers,
+  // twice the latency covered)
+  constexpr int NP = PF == 1 ? 4 : 2;
+  constexpr int NQ = (NI + NP - 1) / NP;
+  uint32_t wv[PF][NQ];
+  auto gload_w = [&](int kb, int part, int slot) {
+    const uint8_t* b = wsrc + size_t(kb) * F::kBytes;
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int q = part * NQ + u;
+      if (q < NI && wlane && q * RPI + lrow < RW) wv[slot][u] = ld_u1(b + size_t(q * RPI) * row_bytes) >> wshift;
+    }
+  };
+  auto store_w = [&](int buf, int part, int slot) {
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int q = part * NQ + u;
+      if (q < NI && wlane && q * RPI + lrow < RW) wsr(buf, rr0 + q * RPI + lrow)[j] = wv[slot][u];
+    }
+  };
+
+  // token staging: piece c = tid + NT q -> row c / 8, 8 halfs at 8 (c % 8)
+  const uint16_t* src[XP];
+#pragma unroll
+  for (int q = 0; q < XP; ++q) {
+    const int c = tid + NT * q, row = c >> 3;
+    const uint32_t cc = c0 + uint32_t(row);
+    src[q] = nullptr;
+    if (row < TM && cc < c1) {
+      const uint32_t a = p.sorted ? p.sorted[cc] : cc;
+      src[q] = p.xin + size_t(a / p.in_div) * K + 8 * (c & 7);
+    }
+  }
+  // token pieces of step t sit in register slot t % PF until stored
+  uint4 xv[PF][XP];
+  auto load_x = [&](int st, int slot) {
+#pragma unroll
+    for (int q = 0; q < XP; ++q)
+      xv[slot][q] = src[q] ? *reinterpret_cast<const uint4*>(src[q] + 64 * st) : make_uint4(0, 0, 0, 0);
+  };
+  auto store_x = [&](int buf, int slot) {
+#pragma unroll
+    for (int q = 0; q < XP; ++q) {
+      const int c = tid + NT * q;
+      if (XP * NT == TM * 8 || c < TM * 8)
+        *reinterpret_cast<uint4*>(xs(buf, c >> 3) + 8 * (c & 7)) = xv[slot][q];
+    }
+  };
+
+  floatx16 acc0[NB], acc1[NB];
+#pragma unroll
+  for (int tb = 0; tb < NB; ++tb) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      acc0[tb][v] = 0.f;
+      acc1[tb][v] = 0.f;
+    }
+  }
+  const int nkb = K / kUnit;
+  const int nch = 4 * nkb;
+#pragma unroll
+  for (int part = 0; part < NP; ++part) {
+    gload_w(0, part, 0);
+    store_w(0, part, 0);
+  }
+  load_x(0, 0);
+  store_x(0, 0);
+  if (PF == 2 && 1 < nch) load_x(1, 1 % PF);
+  __syncthreads();
+
+  auto step = [&](auto qc_c, int kb) __attribute__((always_inline)) {
+    constexpr int QC = decltype(qc_c)::value;
+    constexpr int buf = QC & 1;
+    const int st = 4 * kb + QC;
+    const bool more = st + 1 < nch;
+    // x of step st + PF into slot (st + PF) % PF; weights of unit kb + 1
+    if (st + PF < nch) load_x(st + PF, QC % PF);
+    if (kb + 1 < nkb) {
+      if constexpr (PF == 1) gload_w(kb + 1, QC, 0);
+      else if constexpr (QC < 2) gload_w(kb + 1, QC, QC);
+    }
+    uint32_t ra[F::kRaw], rb[F::kRaw];
+    S::frag(wsr(kb & 1, 32 * wave + i), QC, kg, ra);
+    if constexpr (NMAT == 2) S::frag(wsr(kb & 1, TN + 32 * wave + i), QC, kg, rb);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const half8 a0 = F::template get<QC>(ra, s);
+      half8 a1;
+      if constexpr (NMAT == 2) a1 = F::template get<QC>(rb, s);
+#pragma unroll
+      for (int tb = 0; tb < NB; ++tb) {
+        const half8 b = *reinterpret_cast<const half8*>(xs(buf, tb * 32 + i) + 16 * s + 8 * kg);
+        acc0[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc0[tb], 0, 0, 0);
+        if constexpr (NMAT == 2)
+          acc1[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc1[tb], 0, 0, 0);
+      }
+    }
+    if (more) store_x(buf ^ 1, (QC + 1) % PF);
+    if (kb + 1 < nkb) {
+      if constexpr (PF == 1) store_w((kb + 1) & 1, QC, 0);
+      else if constexpr (QC >= 2) store_w((kb + 1) & 1, QC - 2, QC - 2);
+    }
+    __syncthreads();
+  };
+  for (int kb = 0; kb < nkb; ++kb) {
+    step(std::integral_constant<int, 0>{}, kb);
+    step(std::integral_constant<int, 1>{}, kb);
+    step(std::integral_constant<int, 2>{}, kb);
+    step(std::integral_constant<int, 3>{}, kb);
+  }
+
+  // accumulator element v of lane (i, kg): weight row 8 (v / 4) + 4 kg + v % 4
+  // of this wavefront's 32, token column i of the 32-token block
+#pragma unroll
+  for (int tb = 0; tb < NB; ++tb) {
+    const uint32_t c = c0 + uint32_t(tb * 32 + i);
+    if (c >= c1) continue;
+    const uint32_t a = p.sorted ? p.sorted[c] : c;
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int r0 = n0 + 32 * wave + 8 * g4 + 4 * kg;
+      if constexpr (NMAT == 2) {
+        const float wa = p.route_w ? p.route_w[a] : 1.0f;
+        float h[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          h[r] = silu(acc0[tb][4 * g4 + r]) * acc1[tb][4 * g4 + r] * wa;
+        const half2v lo = {(_Float16)h[0], (_Float16)h[2]};
+        const half2v hi = {(_Float16)h[1], (_Float16)h[3]};
+        *reinterpret_cast<uint2*>(p.h_out + size_t(a) * p.N + r0) = make_uint2(as_u32(lo), as_u32(hi));
+      } else {
+        *reinterpret_cast<float4*>(p.y_out + size_t(a) * p.N + r0) =
+            make_float4(acc0[tb][4 * g4], acc0[tb][4 * g4 + 1], acc0[tb][4 * g4 + 2],
+                        acc0[tb][4 * g4 + 3]);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------- planning
 
 // Tiles of one expert with n rows: full 128-row tiles, then the remainder r
@@ -470,9 +743,34 @@ __global__ void __launch_bounds__(256)
 
 // ------------------------------------------------------------- launchers
 
+// INFERNO_PREFILL_GEMM2=0 keeps the four-wavefront kernel for every format.
+bool gemm2_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("INFERNO_PREFILL_GEMM2");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
 template <int Q, int NMAT, int TM>
 int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
   if (grid_y == 0) return INFERNO_OK;
+  // staged weights (four wavefronts) where measured faster: every 32-token
+  // tile and the Q3_K down over 128 tokens; the 128-token gate/up holds too
+  // many accumulators beside the staging and stays on the fragment loads.
+  // Q3_K prefetches two steps ahead.
+  constexpr bool kStaged =
+      (Q == INFERNO_Q2_K || Q == INFERNO_Q3_K) &&
+      (TM == 32 || (NMAT == 1 && Q == INFERNO_Q3_K));
+  if constexpr (kStaged) {
+    if (a.N % 128 == 0 && gemm2_enabled()) {
+      constexpr int PF = Q == INFERNO_Q3_K ? 2 : 1;
+      const dim3 grid(unsigned(a.N / 128), grid_y);
+      gemm2_kernel<Q, NMAT, TM, PF, 4><<<grid, 256, gemm2_lds_bytes<Q, NMAT, TM, 4>(), s>>>(a);
+      INF_LAUNCHED();
+      return INFERNO_OK;
+    }
+  }
   const dim3 grid(unsigned(a.N / kTileN), grid_y);
   gemm_kernel<Q, NMAT, TM><<<grid, 256, gemm_lds_bytes<TM>(), s>>>(a);
   INF_LAUNCHED();

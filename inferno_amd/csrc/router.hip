@@ -8,6 +8,8 @@
 // holds up to four candidates and each round is a DPP wavefront max of the
 // order-preserving key, then of ~expert id among the lanes holding that key
 // (routing_dev.hpp).
+#include <cstdlib>
+
 #include "routing_dev.hpp"
 
 namespace inferno {
@@ -182,6 +184,123 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Many bf16 tokens on the bf16 matrix cores without losing fp32 accuracy:
+// every fp32 router weight is the exact sum of three bf16 terms (truncate,
+// subtract, truncate the remainder, subtract: the last remainder has at most
+// eight significant bits), a bf16 x bf16 product is exact in fp32, so
+// x . w = sum of three bf16 MFMA dots accumulated in fp32. Per 32-deep K
+// block lane (row r = lane % 16, group
+// g = lane / 16) holds w[e][k0 + 8 g .. + 8] and the same eight k of each
+// token row: v_mfma_f32_16x16x32_bf16 pairs the operands slot by slot.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void split3(const float4& a, const float4& b, u32x4v t[3]) {
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t h[3][8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v[j]);
+    const uint32_t u1 = u & 0xffff0000u;
+    const float r1 = v[j] - __builtin_bit_cast(float, u1);
+    const uint32_t u2 = __builtin_bit_cast(uint32_t, r1) & 0xffff0000u;
+    const float r2 = r1 - __builtin_bit_cast(float, u2);
+    h[0][j] = u1;
+    h[1][j] = u2;
+    h[2][j] = __builtin_bit_cast(uint32_t, r2);
+  }
+#pragma unroll
+  for (int m = 0; m < 3; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      t[m][i] = __builtin_amdgcn_perm(h[m][2 * i + 1], h[m][2 * i], 0x07060302u);
+}
+
+// A workgroup of 4 * KS wavefronts covers 64 experts x 16 * NTB tokens;
+// wavefront (s, q) takes experts e0 + 16 q and the 32-deep K blocks s,
+// s + KS, ...; the KS partial tiles are summed through LDS in split order
+// (fixed, so the logits do not depend on scheduling). Operands are loaded
+// straight in MFMA layout, two register sets in flight. (Staging 64-deep K
+// slices through LDS with whole-line loads measured no faster: the kernel is
+// bound by bytes moved into each CU, about 17 GB/s per CU, not by the access
+// pattern.) Rows past E or T read row 0 and are never stored: MFMA output
+// rows and columns are independent, so the loads need no masks.
+template <int NTB, int KS>
+__global__ void __launch_bounds__(256 * KS)
+    logits_bf16x3_kernel(const uint16_t* __restrict__ x, const float* __restrict__ w, int T,
+                         int H, int E, float* __restrict__ logits) {
+  __shared__ float4v part[KS > 1 ? KS - 1 : 1][4][NTB][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = wave & 3, s = wave >> 2;
+  const int r = lane & 15, g = lane >> 4;
+  const int e0 = blockIdx.x * 64 + q * 16, t0 = blockIdx.y * (16 * NTB);
+  const float* wrow = w + size_t(e0 + r < E ? e0 + r : 0) * H + 8 * g;
+  const uint16_t* xrow[NTB];
+#pragma unroll
+  for (int b = 0; b < NTB; ++b) {
+    const int t = t0 + 16 * b + r;
+    xrow[b] = x + size_t(t < T ? t : 0) * H + 8 * g;
+  }
+  float4v acc[NTB];
+#pragma unroll
+  for (int b = 0; b < NTB; ++b) acc[b] = float4v{0.f, 0.f, 0.f, 0.f};
+  const int nkb = H / 32;
+  struct Buf {
+    float4 wa, wb;
+    u32x4v xv[NTB];
+  };
+  // out-of-range prefetches re-read the last block (harmless, never used)
+  auto load = [&](int kb, Buf& u) {
+    const int k0 = (kb < nkb ? kb : nkb - 1) * 32;
+    u.wa = *reinterpret_cast<const float4*>(wrow + k0);
+    u.wb = *reinterpret_cast<const float4*>(wrow + k0 + 4);
+#pragma unroll
+    for (int b = 0; b < NTB; ++b) u.xv[b] = *reinterpret_cast<const u32x4v*>(xrow[b] + k0);
+  };
+  auto compute = [&](const Buf& u) {
+    u32x4v wt[3];
+    split3(u.wa, u.wb, wt);
+#pragma unroll
+    for (int m = 0; m < 3; ++m)
+#pragma unroll
+      for (int b = 0; b < NTB; ++b)
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wt[m]),
+                                                         __builtin_bit_cast(bf16x8, u.xv[b]),
+                                                         acc[b], 0, 0, 0);
+  };
+  // the host launches this kernel only when 2 * KS divides H / 32
+  Buf u0, u1;
+  load(s, u0);
+  load(s + KS, u1);
+  for (int kb = s; kb < nkb; kb += 2 * KS) {
+    compute(u0);
+    load(kb + 2 * KS, u0);
+    compute(u1);
+    load(kb + 3 * KS, u1);
+  }
+  if constexpr (KS > 1) {
+    if (s > 0)
+#pragma unroll
+      for (int b = 0; b < NTB; ++b) part[s - 1][q][b][lane] = acc[b];
+    __syncthreads();
+    if (s > 0) return;
+#pragma unroll
+    for (int j = 0; j < KS - 1; ++j)
+#pragma unroll
+      for (int b = 0; b < NTB; ++b) acc[b] += part[j][q][b][lane];
+  }
+  // lane holds C[4 g + i][r]: expert e0 + 4 g + i, token t0 + 16 b + r
+#pragma unroll
+  for (int b = 0; b < NTB; ++b) {
+    const int t = t0 + 16 * b + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = e0 + 4 * g + i;
+      if (t < T && e < E) logits[size_t(t) * E + e] = acc[b][i];
+    }
+  }
+}
+
 __global__ void __launch_bounds__(256)
     topk_kernel(const float* __restrict__ logits, const float* __restrict__ bias, int T, int E,
                 int k, int score_fn, int norm, float scale, uint32_t* __restrict__ ids,
@@ -194,6 +313,15 @@ __global__ void __launch_bounds__(256)
 }
 
 }  // namespace
+
+// INFERNO_ROUTER_BF16X3=0 keeps the fp32 matrix-core logits for bf16 tokens.
+static bool bf16x3_enabled() {
+  static const bool on = [] {
+    const char* v = getenv("INFERNO_ROUTER_BF16X3");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
 
 int launch_router_logits(hipStream_t s, const void* x, int x_dtype, const float* w, size_t T,
                          size_t H, size_t E, float* logits) {
@@ -212,7 +340,16 @@ int launch_router_logits(hipStream_t s, const void* x, int x_dtype, const float*
     const bool wide = T >= 2048;
     const unsigned tt = wide ? 64u : 16u;
     dim3 grid(unsigned((E + 63) / 64), unsigned((T + tt - 1) / tt));
-    if (x_dtype == INFERNO_BF16) {
+    if (x_dtype == INFERNO_BF16 && H % 256 == 0 && bf16x3_enabled()) {
+      // 64-token tiles, K split in two, for large batches; 16-token tiles,
+      // K split in four, otherwise (more waves for fewer tiles)
+      if (wide)
+        logits_bf16x3_kernel<4, 2><<<grid, 512, 0, s>>>(static_cast<const uint16_t*>(x), w,
+                                                        int(T), int(H), int(E), logits);
+      else
+        logits_bf16x3_kernel<1, 4><<<grid, 1024, 0, s>>>(static_cast<const uint16_t*>(x), w,
+                                                         int(T), int(H), int(E), logits);
+    } else if (x_dtype == INFERNO_BF16) {
       if (wide)
         logits_mfma_kernel<uint16_t, 4><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x), w,
                                                              int(T), int(H), int(E), logits);
