@@ -456,21 +456,29 @@ struct Stage<INFERNO_Q3_K> {
   }
 };
 
-template <int Q, int NMAT, int TM, int WAVES>
+template <int Q, int NMAT, int TM, int WR>
 constexpr size_t gemm2_lds_bytes() {
-  return size_t(2) * TM * kLdsPitch * 2 + size_t(2) * 32 * WAVES * NMAT * Stage<Q>::kPitch * 4;
+  return size_t(2) * TM * kLdsPitch * 2 + size_t(2) * 32 * WR * NMAT * Stage<Q>::kPitch * 4;
 }
 
-template <int Q, int NMAT, int TM, int PF, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// WR x WT wavefronts: wavefront (wr, wt) computes weight rows 32 wr .. + 32
+// of each matrix for token blocks wt NBW .. + NBW (NBW = TM / 32 / WT);
+// WT = 2 halves the accumulators per wavefront (each row group's fragments
+// are then dequantised by two wavefronts). OCC = waves per SIMD.
+template <int Q, int NMAT, int TM, int PF, int WR, int WT, int OCC>
+__global__ void __launch_bounds__(64 * WR * WT) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
     gemm2_kernel(GemmArgs p) {
   using F = Frag<Q>;
   using S = Stage<Q>;
+  constexpr int WAVES = WR * WT;
   constexpr int NB = TM / 32;
+  static_assert(NB % WT == 0, "token blocks split evenly over WT");
+  constexpr int NBW = NB / WT;          // token blocks per wavefront
   constexpr int NT = 64 * WAVES;        // threads
-  constexpr int TN = 32 * WAVES;        // weight rows per matrix
+  constexpr int TN = 32 * WR;           // weight rows per matrix
   constexpr int R = TN * NMAT;          // staged weight rows
-  constexpr int RW = 32 * NMAT;         // rows staged by one wavefront
+  static_assert(R % WAVES == 0, "staged rows split evenly over wavefronts");
+  constexpr int RW = R / WAVES;         // rows staged by one wavefront
   constexpr int RPI = 64 / S::kWords;   // rows per load instruction
   constexpr int NI = (RW + RPI - 1) / RPI;
   constexpr int XP = (TM * 8 + NT - 1) / NT;  // 16-byte token pieces per thread
@@ -482,6 +490,7 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, kg = lane >> 5;
+  const int wr = wave % WR, wt = wave / WR;
   uint32_t e = 0, c0, c1;
   if (p.tiles) {
     if (blockIdx.y >= *p.n_tiles) return;
@@ -558,9 +567,9 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
     }
   };
 
-  floatx16 acc0[NB], acc1[NB];
+  floatx16 acc0[NBW], acc1[NBW];
 #pragma unroll
-  for (int tb = 0; tb < NB; ++tb) {
+  for (int tb = 0; tb < NBW; ++tb) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       acc0[tb][v] = 0.f;
@@ -591,16 +600,17 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
       else if constexpr (QC < 2) gload_w(kb + 1, QC, QC);
     }
     uint32_t ra[F::kRaw], rb[F::kRaw];
-    S::frag(wsr(kb & 1, 32 * wave + i), QC, kg, ra);
-    if constexpr (NMAT == 2) S::frag(wsr(kb & 1, TN + 32 * wave + i), QC, kg, rb);
+    S::frag(wsr(kb & 1, 32 * wr + i), QC, kg, ra);
+    if constexpr (NMAT == 2) S::frag(wsr(kb & 1, TN + 32 * wr + i), QC, kg, rb);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const half8 a0 = F::template get<QC>(ra, s);
       half8 a1;
       if constexpr (NMAT == 2) a1 = F::template get<QC>(rb, s);
 #pragma unroll
-      for (int tb = 0; tb < NB; ++tb) {
-        const half8 b = *reinterpret_cast<const half8*>(xs(buf, tb * 32 + i) + 16 * s + 8 * kg);
+      for (int tb = 0; tb < NBW; ++tb) {
+        const half8 b =
+            *reinterpret_cast<const half8*>(xs(buf, (wt * NBW + tb) * 32 + i) + 16 * s + 8 * kg);
         acc0[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc0[tb], 0, 0, 0);
         if constexpr (NMAT == 2)
           acc1[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc1[tb], 0, 0, 0);
@@ -623,13 +633,13 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
   // accumulator element v of lane (i, kg): weight row 8 (v / 4) + 4 kg + v % 4
   // of this wavefront's 32, token column i of the 32-token block
 #pragma unroll
-  for (int tb = 0; tb < NB; ++tb) {
-    const uint32_t c = c0 + uint32_t(tb * 32 + i);
+  for (int tb = 0; tb < NBW; ++tb) {
+    const uint32_t c = c0 + uint32_t((wt * NBW + tb) * 32 + i);
     if (c >= c1) continue;
     const uint32_t a = p.sorted ? p.sorted[c] : c;
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      const int r0 = n0 + 32 * wave + 8 * g4 + 4 * kg;
+      const int r0 = n0 + 32 * wr + 8 * g4 + 4 * kg;
       if constexpr (NMAT == 2) {
         const float wa = p.route_w ? p.route_w[a] : 1.0f;
         float h[4];
@@ -651,29 +661,31 @@ __global__ void __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu
 // ------------------------------------------------------------- planning
 
 // Tiles of one expert with n rows: full 128-row tiles, then the remainder r
-// as one 128-row tile (r > 32) or one 32-row tile. The dequantisation cost
-// of a tile does not depend on its row count, the MFMA cost does: small
-// remainders take the cheap 32-row tile.
+// as one 128-row (r > 64), 64-row (r > 32) or 32-row tile. The
+// dequantisation cost of a tile does not depend on its row count, the MFMA
+// cost does: small remainders take the cheaper narrow tiles.
 struct TileCounts {
-  uint32_t t128, t32;
+  uint32_t t128, t64, t32;
 };
 __device__ __forceinline__ TileCounts tile_counts(uint32_t n) {
   const uint32_t r = n % 128;
-  TileCounts t{n / 128, 0};
-  if (r > 32) t.t128 += 1;
+  TileCounts t{n / 128, 0, 0};
+  if (r > 64) t.t128 += 1;
+  else if (r > 32) t.t64 = 1;
   else if (r > 0) t.t32 = 1;
   return t;
 }
 
-// One workgroup: the two tile lists of all active experts, expert order.
+// One workgroup: the three tile lists of all active experts, expert order.
 __global__ void __launch_bounds__(256)
     plan_kernel(const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ active,
-                uint4* __restrict__ l128, uint4* __restrict__ l32, uint32_t* __restrict__ counts) {
-  __shared__ uint32_t sc[2][256];
+                uint4* __restrict__ l128, uint4* __restrict__ l64, uint4* __restrict__ l32,
+                uint32_t* __restrict__ counts) {
+  __shared__ uint32_t sc[3][256];
   const int j = threadIdx.x;
   const uint32_t n_act = active[0];
   uint32_t e = 0, lo = 0, hi = 0;
-  TileCounts t{0, 0};
+  TileCounts t{0, 0, 0};
   if (uint32_t(j) < n_act) {
     e = active[1 + j];
     lo = offsets[e];
@@ -681,29 +693,34 @@ __global__ void __launch_bounds__(256)
     t = tile_counts(hi - lo);
   }
   sc[0][j] = t.t128;
-  sc[1][j] = t.t32;
+  sc[1][j] = t.t64;
+  sc[2][j] = t.t32;
   __syncthreads();
   for (int o = 1; o < 256; o <<= 1) {
-    const uint32_t v0 = j >= o ? sc[0][j - o] : 0u, v1 = j >= o ? sc[1][j - o] : 0u;
+    uint32_t v[3];
+#pragma unroll
+    for (int l = 0; l < 3; ++l) v[l] = j >= o ? sc[l][j - o] : 0u;
     __syncthreads();
-    sc[0][j] += v0;
-    sc[1][j] += v1;
+#pragma unroll
+    for (int l = 0; l < 3; ++l) sc[l][j] += v[l];
     __syncthreads();
   }
-  const uint32_t o128 = sc[0][j] - t.t128, o32 = sc[1][j] - t.t32;
+  const uint32_t o128 = sc[0][j] - t.t128, o64 = sc[1][j] - t.t64, o32 = sc[2][j] - t.t32;
   for (uint32_t q = 0; q < t.t128; ++q)
     l128[o128 + q] = make_uint4(e, lo + 128 * q, min(hi, lo + 128 * (q + 1)), 0);
+  if (t.t64) l64[o64] = make_uint4(e, lo + 128 * t.t128, hi, 0);
   if (t.t32) l32[o32] = make_uint4(e, lo + 128 * t.t128, hi, 0);
   if (j == 255) {
     counts[0] = sc[0][255];
     counts[1] = sc[1][255];
+    counts[2] = sc[2][255];
   }
 }
 
 // Upper bounds of the tile lists (grid heights): a 128-row tile covers at
-// least 33 rows, the 32-row list holds at most one tile per expert.
-size_t bound128(size_t A, size_t E) { return A / 33 + 1; }
-size_t bound32(size_t A, size_t E) { return std::min(E, A) + 1; }
+// least 65 rows, the 64- and 32-row lists hold at most one tile per expert.
+size_t bound128(size_t A, size_t E) { return A / 65 + 1; }
+size_t bound_small(size_t A, size_t E) { return std::min(E, A) + 1; }
 
 // ----------------------------------------------------------- conversions
 
@@ -755,18 +772,18 @@ bool gemm2_enabled() {
 template <int Q, int NMAT, int TM>
 int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
   if (grid_y == 0) return INFERNO_OK;
-  // staged weights (four wavefronts) where measured faster: every 32-token
-  // tile and the Q3_K down over 128 tokens; the 128-token gate/up holds too
-  // many accumulators beside the staging and stays on the fragment loads.
-  // Q3_K prefetches two steps ahead.
+  // staged weights (four wavefronts) where measured faster: 32- and
+  // 64-token tiles and the Q3_K down over 128 tokens; the 128-token gate/up
+  // holds too many accumulators beside the staging and stays on the
+  // fragment loads. Q3_K prefetches two steps ahead.
   constexpr bool kStaged =
       (Q == INFERNO_Q2_K || Q == INFERNO_Q3_K) &&
-      (TM == 32 || (NMAT == 1 && Q == INFERNO_Q3_K));
+      (TM <= 64 || (NMAT == 1 && Q == INFERNO_Q3_K));
   if constexpr (kStaged) {
     if (a.N % 128 == 0 && gemm2_enabled()) {
       constexpr int PF = Q == INFERNO_Q3_K ? 2 : 1;
       const dim3 grid(unsigned(a.N / 128), grid_y);
-      gemm2_kernel<Q, NMAT, TM, PF, 4><<<grid, 256, gemm2_lds_bytes<Q, NMAT, TM, 4>(), s>>>(a);
+      gemm2_kernel<Q, NMAT, TM, PF, 4, 1, 2><<<grid, 256, gemm2_lds_bytes<Q, NMAT, TM, 4>(), s>>>(a);
       INF_LAUNCHED();
       return INFERNO_OK;
     }
@@ -791,30 +808,36 @@ int launch_gemm_q(hipStream_t s, int quant, const GemmArgs& a, unsigned grid_y) 
 
 struct PlanView {
   uint4* l128;
+  uint4* l64;
   uint4* l32;
   uint32_t* counts;
-  size_t n128, n32;
+  size_t n128, n64, n32;
 };
 
 PlanView plan_view(uint32_t* plan, size_t A, size_t E) {
   PlanView v;
   v.n128 = bound128(A, E);
-  v.n32 = bound32(A, E);
+  v.n64 = bound_small(A, E);
+  v.n32 = bound_small(A, E);
   v.l128 = reinterpret_cast<uint4*>(plan);
-  v.l32 = v.l128 + v.n128;
+  v.l64 = v.l128 + v.n128;
+  v.l32 = v.l64 + v.n64;
   v.counts = reinterpret_cast<uint32_t*>(v.l32 + v.n32);
   return v;
 }
 
-// The two tile-list launches of one GEMM.
+// The three tile-list launches of one GEMM.
 template <int NMAT>
 int launch_tiled(hipStream_t s, int quant, GemmArgs a, const PlanView& v) {
   int st;
   a.tiles = v.l128;
   a.n_tiles = v.counts;
   if ((st = launch_gemm_q<NMAT, 128>(s, quant, a, unsigned(v.n128)))) return st;
-  a.tiles = v.l32;
+  a.tiles = v.l64;
   a.n_tiles = v.counts + 1;
+  if ((st = launch_gemm_q<NMAT, 64>(s, quant, a, unsigned(v.n64)))) return st;
+  a.tiles = v.l32;
+  a.n_tiles = v.counts + 2;
   return launch_gemm_q<NMAT, 32>(s, quant, a, unsigned(v.n32));
 }
 
@@ -841,7 +864,7 @@ bool prefill_routed_supported(int quant, int down_quant, size_t H, size_t I, siz
 }
 
 size_t prefill_plan_words(size_t A, size_t E) {
-  return 4 * (bound128(A, E) + bound32(A, E)) + 4;
+  return 4 * (bound128(A, E) + 2 * bound_small(A, E)) + 4;
 }
 
 int launch_to_f16(hipStream_t s, const void* x, int x_dtype, size_t rows, size_t K,
@@ -867,7 +890,7 @@ int launch_prefill_gate_up(hipStream_t s, const PrefillRouted& p) {
     return INFERNO_ERR_INVALID;
   }
   const PlanView v = plan_view(p.plan, A, p.E);
-  plan_kernel<<<1, 256, 0, s>>>(p.offsets, p.active, v.l128, v.l32, v.counts);
+  plan_kernel<<<1, 256, 0, s>>>(p.offsets, p.active, v.l128, v.l64, v.l32, v.counts);
   INF_LAUNCHED();
   GemmArgs g{};
   g.w0 = static_cast<const uint8_t*>(p.gate);

@@ -174,76 +174,85 @@ constexpr int kDispatchThreads = 1024;
 constexpr int kDispatchWaves = kDispatchThreads / kWave;
 
 
-// Body of the dispatch: must run on a 1024-thread workgroup; `ids` may
-// live in global memory or LDS.
-__device__ __forceinline__ void dispatch_block(const uint32_t* ids, int A, int E,
-                                               uint32_t* __restrict__ offsets,
-                                               uint32_t* __restrict__ sorted,
-                                               uint32_t* __restrict__ active) {
-  __shared__ uint32_t count[kMaxExperts];
-  __shared__ uint32_t cursor[kMaxExperts];
-  __shared__ uint32_t wcount[kDispatchWaves * kMaxExperts];  // [wave][expert], row stride E
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int e = tid; e < E; e += kDispatchThreads) count[e] = 0;
-  __syncthreads();
-  for (int a = tid; a < A; a += kDispatchThreads) {
-    uint32_t e = ids[a];
-    if (e < uint32_t(E)) atomicAdd(&count[e], 1u);
+// Lanes of this wavefront holding the same expert as this lane (ok lanes
+// only): one ballot per expert-id bit.
+__device__ __forceinline__ uint64_t expert_match(uint32_t e, bool ok, int nbits) {
+  uint64_t match = __ballot(ok);
+  for (int bit = 0; bit < nbits; ++bit) {
+    const uint64_t b = __ballot(ok && ((e >> bit) & 1u));
+    match &= ((e >> bit) & 1u) ? b : ~b;
   }
-  __syncthreads();
-  // exclusive scan of counts and of the "has assignments" flags on wave 0:
-  // each lane owns four consecutive experts (E <= 256)
-  if (wave == 0) {
-    uint32_t c4[4], f4[4], cs = 0, fs = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = 4 * lane + j;
-      c4[j] = e < E ? count[e] : 0u;
-      f4[j] = c4[j] > 0 ? 1u : 0u;
-      cs += c4[j];
-      fs += f4[j];
-    }
-    uint32_t ci = cs, fi = fs;  // inclusive wave scans
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t cu = __shfl_up(ci, o, kWave), fu = __shfl_up(fi, o, kWave);
-      if (lane >= o) {
-        ci += cu;
-        fi += fu;
-      }
-    }
-    uint32_t cex = ci - cs, fex = fi - fs;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = 4 * lane + j;
-      if (e < E) {
-        offsets[e] = cex;
-        cursor[e] = cex;
-        if (c4[j] > 0) active[1 + fex] = uint32_t(e);
-      }
-      cex += c4[j];
-      fex += f4[j];
-    }
-    if (lane == 63) {
-      offsets[E] = ci;
-      active[0] = fi;
-    }
-  }
-  __syncthreads();
+  return match;
+}
 
-  // stable scatter
+__device__ __forceinline__ int expert_bits(int E) {
   int nbits = 1;
   while ((1 << nbits) < E) ++nbits;
-  for (int base = 0; base < A; base += kDispatchThreads) {
+  return nbits;
+}
+
+// Exclusive scan of count[0..E) on wavefront 0 (each lane owns four
+// consecutive experts, E <= 256) into cursor[]; when `write`, also the
+// expert offsets (offsets[E] = total) and the compacted active list
+// (active[0] = number of experts with assignments).
+__device__ __forceinline__ void dispatch_scan(const uint32_t* count, int E, uint32_t* cursor,
+                                              bool write, uint32_t* __restrict__ offsets,
+                                              uint32_t* __restrict__ active) {
+  const int lane = threadIdx.x & 63;
+  uint32_t c4[4], f4[4], cs = 0, fs = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 4 * lane + j;
+    c4[j] = e < E ? count[e] : 0u;
+    f4[j] = c4[j] > 0 ? 1u : 0u;
+    cs += c4[j];
+    fs += f4[j];
+  }
+  uint32_t ci = cs, fi = fs;  // inclusive wave scans
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t cu = __shfl_up(ci, o, kWave), fu = __shfl_up(fi, o, kWave);
+    if (lane >= o) {
+      ci += cu;
+      fi += fu;
+    }
+  }
+  uint32_t cex = ci - cs, fex = fi - fs;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 4 * lane + j;
+    if (e < E) {
+      cursor[e] = cex;
+      if (write) {
+        offsets[e] = cex;
+        if (c4[j] > 0) active[1 + fex] = uint32_t(e);
+      }
+    }
+    cex += c4[j];
+    fex += f4[j];
+  }
+  if (write && lane == 63) {
+    offsets[E] = ci;
+    active[0] = fi;
+  }
+}
+
+// Stable scatter of assignments [a_begin, a_end) (a_begin a multiple of
+// 1024) to sorted[cursor[e]++]: inside a wavefront the rank among earlier
+// lanes with the same expert comes from the match mask; wavefront counts per
+// expert are prefix-summed across the 16 wavefronts through LDS. 1024-thread
+// workgroup; ends with a barrier.
+__device__ __forceinline__ void dispatch_scatter(const uint32_t* ids, int a_begin, int a_end, int E,
+                                                 uint32_t* cursor, uint32_t* wcount,
+                                                 uint32_t* __restrict__ sorted) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nbits = expert_bits(E);
+  for (int base = a_begin; base < a_end; base += kDispatchThreads) {
     const int a = base + tid;
-    const bool valid = a < A;
+    const bool valid = a < a_end;
     const uint32_t e = valid ? ids[a] : 0xffffffffu;
     const bool ok = valid && e < uint32_t(E);
-    uint64_t match = __ballot(ok);
-    for (int bit = 0; bit < nbits; ++bit) {
-      uint64_t b = __ballot(ok && ((e >> bit) & 1u));
-      match &= ((e >> bit) & 1u) ? b : ~b;
-    }
+    const uint64_t match = expert_match(e, ok, nbits);
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     const uint32_t rank = uint32_t(__popcll(match & lt));
     const bool leader = ok && (match & lt) == 0ull;
@@ -265,6 +274,28 @@ __device__ __forceinline__ void dispatch_block(const uint32_t* ids, int A, int E
     }
     __syncthreads();
   }
+}
+
+// Body of the dispatch: must run on a 1024-thread workgroup; `ids` may
+// live in global memory or LDS.
+__device__ __forceinline__ void dispatch_block(const uint32_t* ids, int A, int E,
+                                               uint32_t* __restrict__ offsets,
+                                               uint32_t* __restrict__ sorted,
+                                               uint32_t* __restrict__ active) {
+  __shared__ uint32_t count[kMaxExperts];
+  __shared__ uint32_t cursor[kMaxExperts];
+  __shared__ uint32_t wcount[kDispatchWaves * kMaxExperts];  // [wave][expert], row stride E
+  const int tid = threadIdx.x, wave = tid >> 6;
+  for (int e = tid; e < E; e += kDispatchThreads) count[e] = 0;
+  __syncthreads();
+  for (int a = tid; a < A; a += kDispatchThreads) {
+    uint32_t e = ids[a];
+    if (e < uint32_t(E)) atomicAdd(&count[e], 1u);
+  }
+  __syncthreads();
+  if (wave == 0) dispatch_scan(count, E, cursor, true, offsets, active);
+  __syncthreads();
+  dispatch_scatter(ids, 0, A, E, cursor, wcount, sorted);
 }
 
 

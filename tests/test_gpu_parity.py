@@ -118,7 +118,7 @@ def test_router_specialised_decode_case(cuda):
 
 
 @pytest.mark.parametrize("T,k,E", [(1, 8, 256), (16, 8, 64), (512, 8, 256), (4096, 8, 256),
-                                   (37, 10, 128), (3, 1, 1)])
+                                   (37, 10, 128), (3, 1, 1), (1111, 7, 200)])
 def test_dispatch_matches_oracle(cuda, T, k, E):
     ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).reshape(-1).astype(np.uint32)
     if T == 4096:  # heavy skew: half the tokens share experts 0..7
