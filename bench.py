@@ -227,6 +227,17 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, layers, xs, residual, T, args.cpu_seconds)
 
+    # arithmetic of the gate/up kernel that ran (decode MFMA: x as two e4m3
+    # terms times Q2_K fields as e2m1, down on f16 MFMA; prefill: f16 MFMA;
+    # packed-f16 tile kernels otherwise), always fp32 accumulation
+    gu_label = labels[ops.TIMER_GATE_UP]
+    if gu_label.startswith("mfma:"):
+        dtype = "e4m3x2*e2m1 MFMA gate/up, f16 MFMA down, f32 acc"
+    elif gu_label.startswith("prefill"):
+        dtype = "f16 MFMA, f32 acc"
+    else:
+        dtype = "f16-dot2/f32-acc"
+
     result = {
         "metric": "MoE-layer decode us/token + HBM GB/s (% of 8 TB/s); prefill tokens/s, MFMA %",
         "value": round(tokens_per_s, 3),
@@ -238,7 +249,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16-dot2/f32-acc",
+        "dtype": dtype,
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantised on device)",
         "config": {"workload": cfg.name, "tokens": T, "hidden": H, "experts": E,
                    "intermediate": I, "top_k": k, "quant": QUANT_NAMES.get(q, str(q)),
