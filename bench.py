@@ -82,13 +82,14 @@ def main():
         log(f"[bench] built layer {l + 1}/{L} ({time.time() - t0:.1f}s)")
     n_inputs = 4 if prefill else 64
     xs = [cf.make_input(cfg, T, variant=v, device=dev) for v in range(n_inputs)]
-    if cfg.zipf:
+    if cfg.zipf or cfg.balanced:
         # correction bias fitted so that the top-k load of the first input
-        # follows Zipf(s); written in place (the layer holds its pointer)
+        # follows Zipf(s) (s = 0 for the near-uniform workload); written in
+        # place (the layer holds its pointer)
         for lt in layers:
             logits = ops.router_logits(xs[0], lt.router)
             lt.bias.copy_(torch.from_numpy(cf.zipf_bias(cfg, logits.cpu().numpy())).to(dev))
-        log(f"[bench] Zipf({cfg.zipf}) bias fitted ({time.time() - t0:.1f}s)")
+        log(f"[bench] Zipf({cfg.zipf}) load bias fitted ({time.time() - t0:.1f}s)")
     residual = torch.randn(T, H, device=dev)
     out = torch.empty(T, H, device=dev)
     ids_buf = [torch.empty(T * k, dtype=torch.int32, device=dev) for _ in range(L)]

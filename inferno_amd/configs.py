@@ -30,6 +30,7 @@ class Config:
     x_dtype: torch.dtype
     tokens: tuple
     zipf: float = 0.0          # >0: bias calibrated so expert load follows Zipf(s)
+    balanced: bool = False     # bias calibrated so expert load is near-uniform (Zipf(0))
     rms_eps: float = 1e-6
     notes: str = ""
     weight_std: float = 0.02
@@ -49,7 +50,7 @@ CONFIGS = {
     "c2": Config("c2_glm_q2k_h6144_e256_top8_sigmoid_decode", 1, 6144, 256, 2048, 8, (Q2_K,),
                  SCORE_SIGMOID, True, 2.5, 0.1, 2048, torch.bfloat16, (1,)),
     "c3": Config("c3_glm_q3k_prefill_t512", 2, 6144, 256, 2048, 8, (Q3_K,), SCORE_SIGMOID, True,
-                 2.5, 0.1, 2048, torch.bfloat16, (512,)),
+                 2.5, 0.1, 2048, torch.bfloat16, (512,), balanced=True),
     "c4": Config("c4_laguna_s_4layer_q2k_q3k_top10_softmax", 3, 4096, 128, 1536, 10,
                  (Q2_K, Q2_K, Q3_K, Q3_K), SCORE_SOFTMAX, True, 1.0, 0.0, 1536, torch.bfloat16,
                  (1, 32)),
@@ -112,7 +113,8 @@ def build_layer(cfg, layer=0, device="cuda", max_tokens=1, bias=None):
 
 
 def zipf_bias(cfg, logits, iters=200):
-    """Correction bias that makes top-k load follow Zipf(cfg.zipf).
+    """Correction bias that makes top-k load follow Zipf(cfg.zipf) (cfg.zipf
+    = 0: equal load, for the near-uniform workload).
 
     Target share of rank r is r^-s normalised; an expert can take at most one
     slot per token, so targets are capped at T and the excess is spread over

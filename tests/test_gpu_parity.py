@@ -282,6 +282,9 @@ def _layer_parity(cuda, key, T, tokens=None):
     cfg = cf.CONFIGS[key] if isinstance(key, str) else key
     lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
     x = cf.make_input(cfg, T, device=cuda)
+    if cfg.balanced:  # the near-uniform load the benchmark runs (bias fitted as it does)
+        logits = ops.router_logits(x, lt.router)
+        lt.bias.copy_(torch.from_numpy(cf.zipf_bias(cfg, ph.to_np(logits))).to(cuda))
     residual = torch.randn(T, cfg.hidden, device=cuda)
     ids = torch.empty(T * cfg.top_k, dtype=torch.int32, device=cuda)
     w = torch.empty(T * cfg.top_k, dtype=torch.float32, device=cuda)
