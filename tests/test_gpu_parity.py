@@ -369,6 +369,22 @@ def test_layer_c4_laguna_q2k_q3k_layers(cuda, T):
         assert err < ph.TOL_REL_L2
 
 
+def test_layer_prefill_fragment_kernel_variant(cuda):
+    """The prefill GEMMs all on the fragment-load kernel and the fp32 router
+    logits (INFERNO_PREFILL_GEMM2=0, INFERNO_ROUTER_BF16X3=0) in a child
+    process (the switches are read once per process)."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    env = dict(os.environ, INFERNO_PREFILL_GEMM2="0", INFERNO_ROUTER_BF16X3="0")
+    script = Path(__file__).resolve().parent / "prefill_variant_check.py"
+    r = subprocess.run([sys.executable, "-u", str(script)], env=env, capture_output=True,
+                       text=True, timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and "gemm1 ok" in r.stdout
+
+
 @pytest.mark.parametrize("variant", ["tiles", "ring"])
 def test_layer_decode_variants(cuda, variant):
     """The non-default one-token decode paths in a child process each (the
