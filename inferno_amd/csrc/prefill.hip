@@ -456,16 +456,20 @@ struct Stage<INFERNO_Q3_K> {
   }
 };
 
-template <int Q, int NMAT, int TM, int WR>
+template <int Q, int NMAT, int TM, int WR, int SB = 0>
 constexpr size_t gemm2_lds_bytes() {
-  return size_t(2) * TM * kLdsPitch * 2 + size_t(2) * 32 * WR * NMAT * Stage<Q>::kPitch * 4;
+  return size_t(2) * TM * kLdsPitch * 2 + size_t(SB ? 1 : 2) * 32 * WR * NMAT * Stage<Q>::kPitch * 4;
 }
 
 // WR x WT wavefronts: wavefront (wr, wt) computes weight rows 32 wr .. + 32
 // of each matrix for token blocks wt NBW .. + NBW (NBW = TM / 32 / WT);
 // WT = 2 halves the accumulators per wavefront (each row group's fragments
-// are then dequantised by two wavefronts). OCC = waves per SIMD.
-template <int Q, int NMAT, int TM, int PF, int WR, int WT, int OCC>
+// are then dequantised by two wavefronts). OCC = waves per SIMD. SB = 1:
+// one weight buffer in LDS; the next K unit is held in registers (all four
+// quarters) and stored after an extra barrier at the end of the unit, so the
+// workgroup needs half the LDS and more of them fit on a CU (measured on the
+// Q3_K down over 32 tokens: four waves per SIMD, 0.61 vs 0.84 ms).
+template <int Q, int NMAT, int TM, int PF, int WR, int WT, int OCC, int SB = 0>
 __global__ void __launch_bounds__(64 * WR * WT) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
     gemm2_kernel(GemmArgs p) {
   using F = Frag<Q>;
@@ -486,7 +490,7 @@ __global__ void __launch_bounds__(64 * WR * WT) __attribute__((amdgpu_waves_per_
   uint16_t* xs_base = smem;
   uint32_t* ws_base = reinterpret_cast<uint32_t*>(smem + 2 * TM * kLdsPitch);
   auto xs = [&](int buf, int row) { return xs_base + (size_t(buf) * TM + row) * kLdsPitch; };
-  auto wsr = [&](int buf, int rr) { return ws_base + (size_t(buf) * R + rr) * S::kPitch; };
+  auto wsr = [&](int buf, int rr) { return ws_base + (size_t(SB ? 0 : buf) * R + rr) * S::kPitch; };
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, kg = lane >> 5;
@@ -520,9 +524,9 @@ __global__ void __launch_bounds__(64 * WR * WT) __attribute__((amdgpu_waves_per_
   // a quarter per 64-deep step, stored at the end of that step; PF = 2,
   // halves at steps 0 and 1, each stored two steps later (more registers,
   // twice the latency covered)
-  constexpr int NP = PF == 1 ? 4 : 2;
+  constexpr int NP = (PF == 1 || SB) ? 4 : 2;
   constexpr int NQ = (NI + NP - 1) / NP;
-  uint32_t wv[PF][NQ];
+  uint32_t wv[SB ? 4 : PF][NQ];
   auto gload_w = [&](int kb, int part, int slot) {
     const uint8_t* b = wsrc + size_t(kb) * F::kBytes;
 #pragma unroll
@@ -596,7 +600,8 @@ __global__ void __launch_bounds__(64 * WR * WT) __attribute__((amdgpu_waves_per_
     // x of step st + PF into slot (st + PF) % PF; weights of unit kb + 1
     if (st + PF < nch) load_x(st + PF, QC % PF);
     if (kb + 1 < nkb) {
-      if constexpr (PF == 1) gload_w(kb + 1, QC, 0);
+      if constexpr (SB) gload_w(kb + 1, QC, QC);
+      else if constexpr (PF == 1) gload_w(kb + 1, QC, 0);
       else if constexpr (QC < 2) gload_w(kb + 1, QC, QC);
     }
     uint32_t ra[F::kRaw], rb[F::kRaw];
@@ -617,7 +622,13 @@ __global__ void __launch_bounds__(64 * WR * WT) __attribute__((amdgpu_waves_per_
       }
     }
     if (more) store_x(buf ^ 1, (QC + 1) % PF);
-    if (kb + 1 < nkb) {
+    if constexpr (SB) {
+      if (QC == 3 && kb + 1 < nkb) {
+        __syncthreads();  // every wavefront is done with this unit's weights
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) store_w(0, qq, qq);
+      }
+    } else if (kb + 1 < nkb) {
       if constexpr (PF == 1) store_w((kb + 1) & 1, QC, 0);
       else if constexpr (QC >= 2) store_w((kb + 1) & 1, QC - 2, QC - 2);
     }
@@ -781,9 +792,16 @@ int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
       (TM <= 64 || (NMAT == 1 && Q == INFERNO_Q3_K));
   if constexpr (kStaged) {
     if (a.N % 128 == 0 && gemm2_enabled()) {
-      constexpr int PF = Q == INFERNO_Q3_K ? 2 : 1;
       const dim3 grid(unsigned(a.N / 128), grid_y);
-      gemm2_kernel<Q, NMAT, TM, PF, 4, 1, 2><<<grid, 256, gemm2_lds_bytes<Q, NMAT, TM, 4>(), s>>>(a);
+      if constexpr (NMAT == 1 && TM == 32) {
+        // down over few tokens: one weight buffer, four waves per SIMD (at
+        // 64 tokens the 128-register budget spills)
+        gemm2_kernel<Q, 1, TM, 2, 4, 1, 4, 1>
+            <<<grid, 256, gemm2_lds_bytes<Q, 1, TM, 4, 1>(), s>>>(a);
+      } else {
+        constexpr int PF = Q == INFERNO_Q3_K ? 2 : 1;
+        gemm2_kernel<Q, NMAT, TM, PF, 4, 1, 2><<<grid, 256, gemm2_lds_bytes<Q, NMAT, TM, 4>(), s>>>(a);
+      }
       INF_LAUNCHED();
       return INFERNO_OK;
     }
