@@ -469,12 +469,19 @@ constexpr size_t gemm2_lds_bytes() {
 // quarters) and stored after an extra barrier at the end of the unit, so the
 // workgroup needs half the LDS and more of them fit on a CU (measured on the
 // Q3_K down over 32 tokens: four waves per SIMD, 0.61 vs 0.84 ms).
-template <int Q, int NMAT, int TM, int PF, int WR, int WT, int OCC, int SB = 0>
-__global__ void __launch_bounds__(64 * WR * WT) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
-    gemm2_kernel(GemmArgs p) {
+// SPL = 1 (gate/up only): each wavefront computes one matrix (wavefronts
+// 0..WR-1 gate, WR..2WR-1 up), halving its fragment and accumulator
+// registers; after the K loop the up wavefronts pass their sums to the gate
+// wavefronts through the (then free) weight buffer for the SwiGLU.
+template <int Q, int NMAT, int TM, int PF, int WR, int WT, int OCC, int SB = 0, int SPL = 0>
+__global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
+    __attribute__((amdgpu_waves_per_eu(OCC, OCC))) gemm2_kernel(GemmArgs p) {
   using F = Frag<Q>;
   using S = Stage<Q>;
-  constexpr int WAVES = WR * WT;
+  static_assert(!SPL || (NMAT == 2 && WT == 1), "matrix split: gate/up, no token split");
+  static_assert(!SPL || WR * (TM / 32) * 16 * 64 <= (SB ? 1 : 2) * 32 * WR * NMAT * Stage<Q>::kPitch,
+                "the up sums passed through the weight buffer fit in it");
+  constexpr int WAVES = SPL ? 2 * WR : WR * WT;
   constexpr int NB = TM / 32;
   static_assert(NB % WT == 0, "token blocks split evenly over WT");
   constexpr int NBW = NB / WT;          // token blocks per wavefront
@@ -494,7 +501,8 @@ __global__ void __launch_bounds__(64 * WR * WT) __attribute__((amdgpu_waves_per_
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, kg = lane >> 5;
-  const int wr = wave % WR, wt = wave / WR;
+  const int wr = wave % WR, wt = SPL ? 0 : wave / WR;
+  const int mw = SPL ? wave / WR : 0;  // this wavefront's matrix (SPL)
   uint32_t e = 0, c0, c1;
   if (p.tiles) {
     if (blockIdx.y >= *p.n_tiles) return;
@@ -605,19 +613,23 @@ __global__ void __launch_bounds__(64 * WR * WT) __attribute__((amdgpu_waves_per_
       else if constexpr (QC < 2) gload_w(kb + 1, QC, QC);
     }
     uint32_t ra[F::kRaw], rb[F::kRaw];
-    S::frag(wsr(kb & 1, 32 * wr + i), QC, kg, ra);
-    if constexpr (NMAT == 2) S::frag(wsr(kb & 1, TN + 32 * wr + i), QC, kg, rb);
+    if constexpr (SPL) {
+      S::frag(wsr(kb & 1, mw * TN + 32 * wr + i), QC, kg, ra);
+    } else {
+      S::frag(wsr(kb & 1, 32 * wr + i), QC, kg, ra);
+      if constexpr (NMAT == 2) S::frag(wsr(kb & 1, TN + 32 * wr + i), QC, kg, rb);
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const half8 a0 = F::template get<QC>(ra, s);
       half8 a1;
-      if constexpr (NMAT == 2) a1 = F::template get<QC>(rb, s);
+      if constexpr (NMAT == 2 && !SPL) a1 = F::template get<QC>(rb, s);
 #pragma unroll
       for (int tb = 0; tb < NBW; ++tb) {
         const half8 b =
             *reinterpret_cast<const half8*>(xs(buf, (wt * NBW + tb) * 32 + i) + 16 * s + 8 * kg);
         acc0[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc0[tb], 0, 0, 0);
-        if constexpr (NMAT == 2)
+        if constexpr (NMAT == 2 && !SPL)
           acc1[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc1[tb], 0, 0, 0);
       }
     }
@@ -643,6 +655,24 @@ __global__ void __launch_bounds__(64 * WR * WT) __attribute__((amdgpu_waves_per_
 
   // accumulator element v of lane (i, kg): weight row 8 (v / 4) + 4 kg + v % 4
   // of this wavefront's 32, token column i of the 32-token block
+  if constexpr (SPL) {
+    // the up wavefronts' sums to the gate wavefronts, through the weight
+    // buffer (no wavefront reads weights any more after this barrier)
+    float* xch = reinterpret_cast<float*>(ws_base);  // [WR][NBW][16][64]
+    __syncthreads();
+    if (mw == 1) {
+#pragma unroll
+      for (int tb = 0; tb < NBW; ++tb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) xch[((wr * NBW + tb) * 16 + v) * 64 + lane] = acc0[tb][v];
+    }
+    __syncthreads();
+    if (mw == 1) return;
+#pragma unroll
+    for (int tb = 0; tb < NBW; ++tb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc1[tb][v] = xch[((wr * NBW + tb) * 16 + v) * 64 + lane];
+  }
 #pragma unroll
   for (int tb = 0; tb < NBW; ++tb) {
     const uint32_t c = c0 + uint32_t((wt * NBW + tb) * 32 + i);
@@ -798,6 +828,11 @@ int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
         // 64 tokens the 128-register budget spills)
         gemm2_kernel<Q, 1, TM, 2, 4, 1, 4, 1>
             <<<grid, 256, gemm2_lds_bytes<Q, 1, TM, 4, 1>(), s>>>(a);
+      } else if constexpr (NMAT == 2 && TM == 32) {
+        // gate/up over few tokens: one matrix per wavefront (eight), one
+        // weight buffer, four waves per SIMD
+        gemm2_kernel<Q, 2, TM, 1, 4, 1, 4, 1, 1>
+            <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 1>(), s>>>(a);
       } else {
         constexpr int PF = Q == INFERNO_Q3_K ? 2 : 1;
         gemm2_kernel<Q, NMAT, TM, PF, 4, 1, 2><<<grid, 256, gemm2_lds_bytes<Q, NMAT, TM, 4>(), s>>>(a);
