@@ -472,15 +472,15 @@ constexpr size_t gemm2_lds_bytes() {
 // SPL = 1 (gate/up only): each wavefront computes one matrix (wavefronts
 // 0..WR-1 gate, WR..2WR-1 up), halving its fragment and accumulator
 // registers; after the K loop the up wavefronts pass their sums to the gate
-// wavefronts through the (then free) weight buffer for the SwiGLU.
+// wavefronts through the (then free) LDS for the SwiGLU.
 template <int Q, int NMAT, int TM, int PF, int WR, int WT, int OCC, int SB = 0, int SPL = 0>
 __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
     __attribute__((amdgpu_waves_per_eu(OCC, OCC))) gemm2_kernel(GemmArgs p) {
   using F = Frag<Q>;
   using S = Stage<Q>;
   static_assert(!SPL || (NMAT == 2 && WT == 1), "matrix split: gate/up, no token split");
-  static_assert(!SPL || WR * (TM / 32) * 16 * 64 <= (SB ? 1 : 2) * 32 * WR * NMAT * Stage<Q>::kPitch,
-                "the up sums passed through the weight buffer fit in it");
+  static_assert(!SPL || size_t(WR) * (TM / 32) * 16 * 64 * 4 <= gemm2_lds_bytes<Q, NMAT, TM, WR, SB>(),
+                "the up sums passed through LDS fit in the workgroup's LDS");
   constexpr int WAVES = SPL ? 2 * WR : WR * WT;
   constexpr int NB = TM / 32;
   static_assert(NB % WT == 0, "token blocks split evenly over WT");
@@ -656,9 +656,10 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
   // accumulator element v of lane (i, kg): weight row 8 (v / 4) + 4 kg + v % 4
   // of this wavefront's 32, token column i of the 32-token block
   if constexpr (SPL) {
-    // the up wavefronts' sums to the gate wavefronts, through the weight
-    // buffer (no wavefront reads weights any more after this barrier)
-    float* xch = reinterpret_cast<float*>(ws_base);  // [WR][NBW][16][64]
+    // the up wavefronts' sums to the gate wavefronts, through the LDS of
+    // the token and weight buffers (no wavefront reads them after this
+    // barrier)
+    float* xch = reinterpret_cast<float*>(smem);  // [WR][NBW][16][64]
     __syncthreads();
     if (mw == 1) {
 #pragma unroll
@@ -813,13 +814,12 @@ bool gemm2_enabled() {
 template <int Q, int NMAT, int TM>
 int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
   if (grid_y == 0) return INFERNO_OK;
-  // staged weights (four wavefronts) where measured faster: 32- and
-  // 64-token tiles and the Q3_K down over 128 tokens; the 128-token gate/up
-  // holds too many accumulators beside the staging and stays on the
-  // fragment loads. Q3_K prefetches two steps ahead.
+  // staged weights where measured faster: 32- and 64-token tiles, the Q3_K
+  // down and the Q2_K gate/up over 128 tokens (the Q3_K 128-token gate/up
+  // stays on the fragment loads). Q3_K prefetches two steps ahead.
   constexpr bool kStaged =
       (Q == INFERNO_Q2_K || Q == INFERNO_Q3_K) &&
-      (TM <= 64 || (NMAT == 1 && Q == INFERNO_Q3_K));
+      (TM <= 64 || (NMAT == 1 && Q == INFERNO_Q3_K) || (NMAT == 2 && Q == INFERNO_Q2_K));
   if constexpr (kStaged) {
     if (a.N % 128 == 0 && gemm2_enabled()) {
       const dim3 grid(unsigned(a.N / 128), grid_y);
@@ -833,6 +833,13 @@ int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
         // weight buffer, four waves per SIMD
         gemm2_kernel<Q, 2, TM, 1, 4, 1, 4, 1, 1>
             <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 1>(), s>>>(a);
+      } else if constexpr (NMAT == 2 && TM == 128) {
+        // Q2_K gate/up over 128 tokens: one matrix per wavefront (64
+        // accumulators each), compiled for three waves per SIMD (lab, dense
+        // tiles: 1.81 vs 2.13 ms for the fragment-load kernel; c5 layer:
+        // 5.21 vs 5.29 ms)
+        gemm2_kernel<Q, 2, TM, 1, 4, 1, 3, 0, 1>
+            <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 0>(), s>>>(a);
       } else {
         constexpr int PF = Q == INFERNO_Q3_K ? 2 : 1;
         gemm2_kernel<Q, NMAT, TM, PF, 4, 1, 2><<<grid, 256, gemm2_lds_bytes<Q, NMAT, TM, 4>(), s>>>(a);
