@@ -249,9 +249,9 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* layer, cons
 /* Measurement hook with no counterpart in the reference (benchmarks only).
  * While enabled, the routed gate/up launch and the routed down launch of
  * inferno_moe_layer_forward / inferno_gguf_moe (fused decode kernels or the
- * stage path) are bracketed with HIP events on the caller's stream; the
- * library waits for the second event and adds the elapsed time to a
- * process-wide accumulator. The wait serialises the host with the layer:
+ * stage path) are bracketed with HIP events on the caller's stream, recorded
+ * without waiting; inferno_kernel_timing_read waits for a timer's recorded
+ * events and sums their elapsed times. The events cost a little per launch:
  * leave timing off outside measurement. */
 enum {
   INFERNO_TIMER_GATE_UP = 0,
@@ -260,8 +260,8 @@ enum {
   INFERNO_TIMER_SELECT = 3  /* fused decode: top-k + dispatch */
 };
 int inferno_kernel_timing_enable(int enable);
-/* Returns the accumulated milliseconds and launch count of one timer and
- * resets it. */
+/* Waits for the timer's recorded launches, returns their summed
+ * milliseconds and count, and resets the timer. */
 int inferno_kernel_timing_read(int which, double* total_ms, uint64_t* launches);
 /* Copies (NUL-terminated, truncated to len) the label of the last launch a
  * timer measured: "<kind>: <kernel> (<what it streams>)", kind one of

@@ -2,9 +2,18 @@
 #include "timing.hpp"
 
 #include <mutex>
+#include <vector>
 
 namespace inferno {
 namespace {
+
+// Event pairs are recorded around the timed launches without waiting (a
+// wait per launch would start every kernel on an idle device and add the
+// launch latency to its time); the pairs are summed when a timer is read.
+struct Pending {
+  int which, dev;
+  hipEvent_t e0, e1;
+};
 
 struct KernelTimers {
   std::mutex mu;
@@ -12,7 +21,8 @@ struct KernelTimers {
   double ms[kNumTimers] = {};
   uint64_t n[kNumTimers] = {};
   const char* label[kNumTimers] = {};
-  hipEvent_t ev[64][2] = {};
+  std::vector<Pending> pending;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> free_pairs[64];
 };
 
 KernelTimers& timers() {
@@ -35,14 +45,30 @@ bool kernel_timing_on() {
 bool kernel_timing_read(int which, double* ms, uint64_t* n) {
   if (which < 0 || which >= kNumTimers) return false;
   std::lock_guard<std::mutex> lock(timers().mu);
-  *ms = timers().ms[which];
-  *n = timers().n[which];
-  timers().ms[which] = 0;
-  timers().n[which] = 0;
+  KernelTimers& k = timers();
+  // settle this timer's pending pairs (in recording order)
+  std::vector<Pending> keep;
+  for (const Pending& pd : k.pending) {
+    if (pd.which != which) {
+      keep.push_back(pd);
+      continue;
+    }
+    float t = 0.f;
+    if (hipEventSynchronize(pd.e1) == hipSuccess && hipEventElapsedTime(&t, pd.e0, pd.e1) == hipSuccess) {
+      k.ms[which] += t;
+      k.n[which] += 1;
+    }
+    k.free_pairs[pd.dev].push_back({pd.e0, pd.e1});
+  }
+  k.pending.swap(keep);
+  *ms = k.ms[which];
+  *n = k.n[which];
+  k.ms[which] = 0;
+  k.n[which] = 0;
   return true;
 }
 
-int kernel_timing_events(hipEvent_t* start, hipEvent_t* stop) {
+int kernel_timing_begin(hipEvent_t* start, hipEvent_t* stop, int* dev_out) {
   int dev = 0;
   INF_HIP(hipGetDevice(&dev));
   if (dev < 0 || dev >= 64) {
@@ -50,20 +76,26 @@ int kernel_timing_events(hipEvent_t* start, hipEvent_t* stop) {
     return INFERNO_ERR_DEVICE;
   }
   std::lock_guard<std::mutex> lock(timers().mu);
-  hipEvent_t* ev = timers().ev[dev];
-  if (!ev[0]) {
-    INF_HIP(hipEventCreate(&ev[0]));
-    INF_HIP(hipEventCreate(&ev[1]));
+  auto& fp = timers().free_pairs[dev];
+  if (fp.empty()) {
+    hipEvent_t a, b;
+    // no system-scope fence when an event completes (an L2 write-back per
+    // event that the timing does not need: the events only timestamp
+    // kernels of one stream)
+    INF_HIP(hipEventCreateWithFlags(&a, hipEventDisableSystemFence));
+    INF_HIP(hipEventCreateWithFlags(&b, hipEventDisableSystemFence));
+    fp.push_back({a, b});
   }
-  *start = ev[0];
-  *stop = ev[1];
+  *start = fp.back().first;
+  *stop = fp.back().second;
+  fp.pop_back();
+  *dev_out = dev;
   return INFERNO_OK;
 }
 
-void kernel_timing_add(int which, float ms, const char* label) {
+void kernel_timing_end(int which, int dev, hipEvent_t start, hipEvent_t stop, const char* label) {
   std::lock_guard<std::mutex> lock(timers().mu);
-  timers().ms[which] += ms;
-  timers().n[which] += 1;
+  timers().pending.push_back({which, dev, start, stop});
   timers().label[which] = label;
 }
 

@@ -404,3 +404,28 @@ def test_layer_decode_variants(cuda, variant):
                        capture_output=True, text=True, timeout=240)
     print(r.stdout[-2000:], r.stderr[-2000:])
     assert r.returncode == 0 and f"{variant} ok" in r.stdout
+
+
+def test_kernel_timing_hook_counts_decode_launches(cuda):
+    """The measurement hook: events recorded around each timed launch without
+    waiting, summed when read; two decode steps give two launches per timer,
+    positive times and a label naming the kernel."""
+    cfg = cf.CONFIGS["c2"]
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=1)
+    x = cf.make_input(cfg, 1, device=cuda)
+    timers = [ops.TIMER_GATE_UP, ops.TIMER_DOWN, ops.TIMER_ROUTE, ops.TIMER_SELECT]
+    ops.kernel_timing(True)
+    try:
+        for tm in timers:
+            ops.kernel_timing_read(tm)
+        lt.layer.forward(x, None)
+        lt.layer.forward(x, None)
+        got = {tm: ops.kernel_timing_read(tm) for tm in timers}
+        labels = {tm: ops.kernel_timing_label(tm) for tm in timers}
+    finally:
+        ops.kernel_timing(False)
+    for tm in timers:
+        ms, n = got[tm]
+        assert n == 2 and ms > 0, (tm, ms, n)
+        assert ":" in labels[tm]
+    assert ops.kernel_timing_read(ops.TIMER_GATE_UP)[1] == 0  # read resets
