@@ -181,7 +181,6 @@ __device__ __forceinline__ void shared_down_rows(const DecodeArgs& p, int g) {
   const int Sns = staged_stride(Is, false);
   uint32_t* xss = smem;
   float* part = reinterpret_cast<float*>(xss + Sns);  // [4 wavefronts][8 rows]
-  float* hrow = part + 32;                             // [Is] shared h
   const int q_first = cp + 2 * wave;
   constexpr int kGroups = kSharedDownRows / 8;
   auto srow = [&](int grp) {
@@ -192,20 +191,64 @@ __device__ __forceinline__ void shared_down_rows(const DecodeArgs& p, int g) {
 #pragma unroll
   for (int grp = 0; grp < kGroups; ++grp)
     if (q_first < ubs) FS::load(srow(grp) + size_t(q_first) * FS::kBytes, sub, sraw[grp]);
-  // h = silu(sum of gate partials) * (sum of up partials), 4 values per step
-  for (int v4 = tid; v4 < Is / 4; v4 += 256) {
-    float4 gs = make_float4(0.f, 0.f, 0.f, 0.f), us = gs;
-    for (int k = 0; k < p.shared_parts; ++k) {
-      const float4 a = reinterpret_cast<const float4*>(p.shared_gu + (size_t(k) * 2) * Is)[v4];
-      const float4 b = reinterpret_cast<const float4*>(p.shared_gu + (size_t(k) * 2 + 1) * Is)[v4];
-      gs.x += a.x; gs.y += a.y; gs.z += a.z; gs.w += a.w;
-      us.x += b.x; us.y += b.y; us.z += b.z; us.w += b.w;
+  // h = silu(sum of gate partials) * (sum of up partials), formed and staged
+  // by lane quads: lane holds values 4 (v4 & 3) .. + 3 of run v4 / 4 (the
+  // parts are added in order 0, 1, ... as the gate/up kernels do); every
+  // part's loads are issued before the sums. The quad gives the run's
+  // maximum, its sum in value order (as stage_run forms it) and the hi pair
+  // words 2 (v4 & 3), + 1, which take only this lane's values.
+  const int parts = p.shared_parts;
+  constexpr int kIt = 2;  // float4 steps per thread issued together
+  for (int v0 = tid; v0 < Is / 4; v0 += 256 * kIt) {
+    float4 gv[kIt][4], uv[kIt][4];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it)
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (k < parts && v0 + 256 * it < Is / 4) {
+          gv[it][k] = reinterpret_cast<const float4*>(p.shared_gu + (size_t(k) * 2) * Is)[v0 + 256 * it];
+          uv[it][k] = reinterpret_cast<const float4*>(p.shared_gu + (size_t(k) * 2 + 1) * Is)[v0 + 256 * it];
+        }
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int v4 = v0 + 256 * it;
+      if (v4 >= Is / 4) break;  // uniform: Is / 4 is a multiple of 64
+      float4 gs = make_float4(0.f, 0.f, 0.f, 0.f), us = gs;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (k < parts) {
+          gs.x += gv[it][k].x; gs.y += gv[it][k].y; gs.z += gv[it][k].z; gs.w += gv[it][k].w;
+          us.x += uv[it][k].x; us.y += uv[it][k].y; us.z += uv[it][k].z; us.w += uv[it][k].w;
+        }
+      const float h0 = silu(gs.x) * us.x, h1 = silu(gs.y) * us.y;
+      const float h2 = silu(gs.z) * us.z, h3 = silu(gs.w) * us.w;
+      float m = fmaxf(fmaxf(fabsf(h0), fabsf(h1)), fmaxf(fabsf(h2), fabsf(h3)));
+      m = fmaxf(m, __shfl_xor(m, 1, kWave));
+      m = fmaxf(m, __shfl_xor(m, 2, kWave));
+      const int q0 = lane & ~3;
+      float sum = 0.f;
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) sum = __shfl((((sum + h0) + h1) + h2) + h3, q0 + qq, kWave);
+      float scale = 1.0f;  // zero or non-finite runs keep scale 1
+      if (m > 0.f && m < 3.0e38f) {
+        int e;
+        frexpf(m, &e);
+        scale = ldexpf(1.0f, 15 - e);
+      }
+      auto pack = [](float a, float b) {
+        const _Float16 ah = (_Float16)a, bh = (_Float16)b;
+        return uint32_t(__builtin_bit_cast(uint16_t, ah)) | (uint32_t(__builtin_bit_cast(uint16_t, bh)) << 16);
+      };
+      const int run = v4 >> 2, qi = v4 & 3;
+      *reinterpret_cast<uint2*>(xss + run * 8 + 2 * qi) =
+          make_uint2(pack(h0 * scale, h2 * scale), pack(h1 * scale, h3 * scale));
+      if (qi == 0) {
+        float* sums = reinterpret_cast<float*>(xss + Is / 2);
+        sums[run] = sum;
+        sums[Is / 16 + run] = 1.0f / scale;
+      }
     }
-    reinterpret_cast<float4*>(hrow)[v4] =
-        make_float4(silu(gs.x) * us.x, silu(gs.y) * us.y, silu(gs.z) * us.z, silu(gs.w) * us.w);
   }
-  __syncthreads();
-  for (int run = tid; run < Is / 16; run += 256) stage_run<false>(hrow + run * 16, xss, Is, run);
   __syncthreads();
 #pragma unroll
   for (int grp = 0; grp < kGroups; ++grp) {
@@ -764,7 +807,7 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   // the MFMA down kernel follows the MFMA gate/up (it reads h in that
   // kernel's layout); the shared down then runs in the select launch
   const bool use_mfma_down = use_mfma && mfma_decode::down_covers(a.I, a.k) &&
-                             a.H % kSharedDownRows == 0 &&
+                             a.H % kSharedDownRows == 0 && a.Is % kKBlock == 0 &&
                              mfma_decode::down_lds_bytes(a.I) <= 160 * 1024 &&
                              (a.Is == 0 || a.ys != nullptr);
   a.h_mfma = use_mfma_down ? 1 : 0;
@@ -798,7 +841,7 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   }
   {
     const int sd_wgs = (use_mfma_down && a.Is) ? a.H / kSharedDownRows : 0;
-    const size_t sd_lds = sd_wgs ? (size_t(staged_stride(a.Is, false)) + 32 + a.Is) * 4 : 0;
+    const size_t sd_lds = sd_wgs ? (size_t(staged_stride(a.Is, false)) + 32) * 4 : 0;
     const char* label = a.T != 1 ? "select: select_kernel"
                         : sd_wgs ? "select+shared-down: select1_kernel (top-k, dispatch; Q8_0 shared down)"
                                  : "select: select1_kernel";
