@@ -421,6 +421,9 @@ struct Stage;
 template <>
 struct Stage<INFERNO_Q2_K> {
   static constexpr int kWords = 21, kPitch = 21;
+  using Chunk = uint32_t;
+  __device__ static Chunk load(const uint8_t* b, int shift) { return ld_u1(b) >> shift; }
+  __device__ static void put(uint32_t* row, int j, Chunk v) { row[j] = v; }
   __device__ static int offset(int j, int& shift) {
     shift = 0;
     return 4 * j;
@@ -438,6 +441,9 @@ struct Stage<INFERNO_Q2_K> {
 template <>
 struct Stage<INFERNO_Q3_K> {
   static constexpr int kWords = 28, kPitch = 28;
+  using Chunk = uint32_t;
+  __device__ static Chunk load(const uint8_t* b, int shift) { return ld_u1(b) >> shift; }
+  __device__ static void put(uint32_t* row, int j, Chunk v) { row[j] = v; }
   __device__ static int offset(int j, int& shift) {
     shift = j == 27 ? 16 : 0;
     return j == 27 ? 106 : 4 * j;
@@ -453,6 +459,43 @@ struct Stage<INFERNO_Q3_K> {
     r[8] = row[24 + (qc & 1)];
     r[9] = row[26];
     r[10] = row[27] & 0xffffu;
+  }
+};
+// Q8_0: a K unit is 272 bytes (eight 34-byte blocks), fetched as 17
+// 16-byte chunks per row (three rows per wavefront load instruction) and
+// stored as dwords at an odd pitch of 69 words. The int8 codes of the even
+// blocks start 2 bytes past a word boundary and are realigned from three
+// words; those of the odd blocks are word aligned.
+template <>
+struct Stage<INFERNO_Q8_0> {
+  static constexpr int kWords = 17, kPitch = 69;
+  using Chunk = uint4;
+  __device__ static int offset(int j, int& shift) {
+    shift = 0;
+    return 16 * j;
+  }
+  __device__ static Chunk load(const uint8_t* b, int) { return ld_u4(b); }
+  __device__ static void put(uint32_t* row, int j, Chunk v) {
+    row[4 * j] = v.x; row[4 * j + 1] = v.y; row[4 * j + 2] = v.z; row[4 * j + 3] = v.w;
+  }
+  __device__ static void frag(const uint32_t* row, int qc, int kg, uint32_t r[10]) {
+    // block 2 qc: codes at byte 68 qc + 2 + 16 s + 8 kg (s = 0, 1)
+    const uint32_t* ev = row + 17 * qc + 2 * kg;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const uint32_t w0 = ev[4 * s], w1 = ev[4 * s + 1], w2 = ev[4 * s + 2];
+      r[2 * s] = __builtin_amdgcn_alignbyte(w1, w0, 2);
+      r[2 * s + 1] = __builtin_amdgcn_alignbyte(w2, w1, 2);
+    }
+    // block 2 qc + 1: codes at byte 68 qc + 36 + 16 s + 8 kg
+    const uint32_t* od = row + 17 * qc + 9 + 2 * kg;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      r[4 + 2 * s] = od[4 * s];
+      r[5 + 2 * s] = od[4 * s + 1];
+    }
+    r[8] = row[17 * qc] & 0xffffu;  // d of block 2 qc (bytes 0..1)
+    r[9] = row[17 * qc + 8] >> 16;  // d of block 2 qc + 1 (bytes 34..35)
   }
 };
 
@@ -534,20 +577,20 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
   // twice the latency covered)
   constexpr int NP = (PF == 1 || SB) ? 4 : 2;
   constexpr int NQ = (NI + NP - 1) / NP;
-  uint32_t wv[SB ? 4 : PF][NQ];
+  typename S::Chunk wv[SB ? 4 : PF][NQ];
   auto gload_w = [&](int kb, int part, int slot) {
     const uint8_t* b = wsrc + size_t(kb) * F::kBytes;
 #pragma unroll
     for (int u = 0; u < NQ; ++u) {
       const int q = part * NQ + u;
-      if (q < NI && wlane && q * RPI + lrow < RW) wv[slot][u] = ld_u1(b + size_t(q * RPI) * row_bytes) >> wshift;
+      if (q < NI && wlane && q * RPI + lrow < RW) wv[slot][u] = S::load(b + size_t(q * RPI) * row_bytes, wshift);
     }
   };
   auto store_w = [&](int buf, int part, int slot) {
 #pragma unroll
     for (int u = 0; u < NQ; ++u) {
       const int q = part * NQ + u;
-      if (q < NI && wlane && q * RPI + lrow < RW) wsr(buf, rr0 + q * RPI + lrow)[j] = wv[slot][u];
+      if (q < NI && wlane && q * RPI + lrow < RW) S::put(wsr(buf, rr0 + q * RPI + lrow), j, wv[slot][u]);
     }
   };
 
@@ -818,12 +861,22 @@ int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
   // down and the Q2_K gate/up over 128 tokens (the Q3_K 128-token gate/up
   // stays on the fragment loads). Q3_K prefetches two steps ahead.
   constexpr bool kStaged =
-      (Q == INFERNO_Q2_K || Q == INFERNO_Q3_K) &&
-      (TM <= 64 || (NMAT == 1 && Q == INFERNO_Q3_K) || (NMAT == 2 && Q == INFERNO_Q2_K));
+      ((Q == INFERNO_Q2_K || Q == INFERNO_Q3_K) &&
+       (TM <= 64 || (NMAT == 1 && Q == INFERNO_Q3_K) || (NMAT == 2 && Q == INFERNO_Q2_K))) ||
+      (Q == INFERNO_Q8_0 && (TM == 32 || TM == 128));
   if constexpr (kStaged) {
     if (a.N % 128 == 0 && gemm2_enabled()) {
       const dim3 grid(unsigned(a.N / 128), grid_y);
-      if constexpr (NMAT == 1 && TM == 32) {
+      if constexpr (Q == INFERNO_Q8_0 && TM == 128) {
+        // Q8_0 (272-byte K units): one weight buffer; gate/up with one
+        // matrix per wavefront
+        if constexpr (NMAT == 2)
+          gemm2_kernel<Q, 2, TM, 1, 4, 1, 2, 1, 1>
+              <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 1>(), s>>>(a);
+        else
+          gemm2_kernel<Q, 1, TM, 1, 4, 1, 2, 1>
+              <<<grid, 256, gemm2_lds_bytes<Q, 1, TM, 4, 1>(), s>>>(a);
+      } else if constexpr (NMAT == 1 && TM == 32) {
         // down over few tokens: one weight buffer, four waves per SIMD (at
         // 64 tokens the 128-register budget spills)
         gemm2_kernel<Q, 1, TM, 2, 4, 1, 4, 1>
