@@ -301,6 +301,16 @@ def _layer_parity(cuda, key, T, tokens=None):
     assert err < ph.TOL_REL_L2
 
 
+@pytest.mark.parametrize("T", [100, 2085])
+def test_layer_prefill_shared_ragged_tiles(cuda, T):
+    # the dense Q8_0 shared-expert GEMM over T rows: 32-row tiles below 2048
+    # tokens, 128-row tiles from 2048, the last tile partly filled (4 and 37
+    # rows); checked on the first and the last tokens
+    cfg = cf.Config("shared_ragged", 9, 1024, 16, 512, 2, (Q2_K,), SCORE_SIGMOID, True, 1.0, 0.1,
+                    512, torch.bfloat16, (T,))
+    _layer_parity(cuda, cfg, T, tokens=np.r_[0:24, T - 48:T])
+
+
 @pytest.mark.parametrize("T", [1, 16])
 def test_layer_c1_q4k_softmax(cuda, T):
     _layer_parity(cuda, "c1", T)
