@@ -858,8 +858,9 @@ template <int Q, int NMAT, int TM>
 int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
   if (grid_y == 0) return INFERNO_OK;
   // staged weights where measured faster: 32- and 64-token tiles, the Q3_K
-  // down and the Q2_K gate/up over 128 tokens (the Q3_K 128-token gate/up
-  // stays on the fragment loads). Q3_K prefetches two steps ahead.
+  // down, the Q2_K gate/up over 128 tokens and the Q8_0 shared expert (the
+  // Q3_K 128-token gate/up and the Q2_K 128-token down stay on the fragment
+  // loads). Q3_K prefetches two steps ahead.
   constexpr bool kStaged =
       ((Q == INFERNO_Q2_K || Q == INFERNO_Q3_K) &&
        (TM <= 64 || (NMAT == 1 && Q == INFERNO_Q3_K) || (NMAT == 2 && Q == INFERNO_Q2_K))) ||
