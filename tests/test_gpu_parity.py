@@ -301,6 +301,40 @@ def _layer_parity(cuda, key, T, tokens=None):
     assert err < ph.TOL_REL_L2
 
 
+@pytest.mark.parametrize("T", [1, 300])
+def test_layer_from_gguf_file(cuda, tmp_path, T):
+    # a layer written to a GGUF file (packed experts [H, I, E] / [I, H, E],
+    # f32 router [H, E], bias, Q8_0 shared expert) and loaded back through
+    # the reader gives bit-identical outputs to the same tensors passed
+    # directly (decode at T = 1, prefill at T = 300)
+    from inferno_amd import gguf as G
+    cfg = cf.Config("gguf_file", 10, 1024, 16, 512, 4, (Q2_K,), SCORE_SIGMOID, True, 2.5, 0.1,
+                    512, torch.bfloat16, (T,))
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
+    H, E, I, Is = cfg.hidden, cfg.experts, cfg.intermediate, cfg.shared_intermediate
+    sg, su, sd = lt.shared
+    ts = [("blk.5.ffn_gate_inp.weight", (H, E), G.GGML_F32, ph.to_np(lt.router).tobytes()),
+          ("blk.5.exp_probs_b.bias", (E,), G.GGML_F32, ph.to_np(lt.bias).tobytes()),
+          ("blk.5.ffn_gate_exps.weight", (H, I, E), Q2_K, ph.to_np(lt.gate).tobytes()),
+          ("blk.5.ffn_up_exps.weight", (H, I, E), Q2_K, ph.to_np(lt.up).tobytes()),
+          ("blk.5.ffn_down_exps.weight", (I, H, E), Q2_K, ph.to_np(lt.down).tobytes()),
+          ("blk.5.ffn_gate_shexp.weight", (H, Is), Q8_0, ph.to_np(sg).tobytes()),
+          ("blk.5.ffn_up_shexp.weight", (H, Is), Q8_0, ph.to_np(su).tobytes()),
+          ("blk.5.ffn_down_shexp.weight", (Is, H), Q8_0, ph.to_np(sd).tobytes())]
+    path = tmp_path / "layer.gguf"
+    G.write_gguf(path, [("general.architecture", G.MT_STRING, "glm")], ts)
+    with G.GGUFFile(path) as g:
+        layer = G.moe_layer_from_gguf(g, 5, top_k=cfg.top_k, score_fn=cfg.score_fn,
+                                      norm_topk_prob=cfg.norm, routed_scaling_factor=cfg.scale,
+                                      device=cuda, max_tokens=T)
+    x = cf.make_input(cfg, T, device=cuda)
+    residual = torch.randn(T, H, device=cuda)
+    got = layer.forward(x, residual)
+    want = lt.layer.forward(x, residual)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("T", [100, 2085])
 def test_layer_prefill_shared_ragged_tiles(cuda, T):
     # the dense Q8_0 shared-expert GEMM over T rows: 32-row tiles below 2048
