@@ -301,23 +301,24 @@ def _layer_parity(cuda, key, T, tokens=None):
     assert err < ph.TOL_REL_L2
 
 
+@pytest.mark.parametrize("quant", [Q2_K, Q3_K, Q4_K])
 @pytest.mark.parametrize("T", [1, 300])
-def test_layer_from_gguf_file(cuda, tmp_path, T):
+def test_layer_from_gguf_file(cuda, tmp_path, T, quant):
     # a layer written to a GGUF file (packed experts [H, I, E] / [I, H, E],
     # f32 router [H, E], bias, Q8_0 shared expert) and loaded back through
     # the reader gives bit-identical outputs to the same tensors passed
     # directly (decode at T = 1, prefill at T = 300)
     from inferno_amd import gguf as G
-    cfg = cf.Config("gguf_file", 10, 1024, 16, 512, 4, (Q2_K,), SCORE_SIGMOID, True, 2.5, 0.1,
+    cfg = cf.Config("gguf_file", 10, 1024, 16, 512, 4, (quant,), SCORE_SIGMOID, True, 2.5, 0.1,
                     512, torch.bfloat16, (T,))
     lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
     H, E, I, Is = cfg.hidden, cfg.experts, cfg.intermediate, cfg.shared_intermediate
     sg, su, sd = lt.shared
     ts = [("blk.5.ffn_gate_inp.weight", (H, E), G.GGML_F32, ph.to_np(lt.router).tobytes()),
           ("blk.5.exp_probs_b.bias", (E,), G.GGML_F32, ph.to_np(lt.bias).tobytes()),
-          ("blk.5.ffn_gate_exps.weight", (H, I, E), Q2_K, ph.to_np(lt.gate).tobytes()),
-          ("blk.5.ffn_up_exps.weight", (H, I, E), Q2_K, ph.to_np(lt.up).tobytes()),
-          ("blk.5.ffn_down_exps.weight", (I, H, E), Q2_K, ph.to_np(lt.down).tobytes()),
+          ("blk.5.ffn_gate_exps.weight", (H, I, E), quant, ph.to_np(lt.gate).tobytes()),
+          ("blk.5.ffn_up_exps.weight", (H, I, E), quant, ph.to_np(lt.up).tobytes()),
+          ("blk.5.ffn_down_exps.weight", (I, H, E), quant, ph.to_np(lt.down).tobytes()),
           ("blk.5.ffn_gate_shexp.weight", (H, Is), Q8_0, ph.to_np(sg).tobytes()),
           ("blk.5.ffn_up_shexp.weight", (H, Is), Q8_0, ph.to_np(su).tobytes()),
           ("blk.5.ffn_down_shexp.weight", (Is, H), Q8_0, ph.to_np(sd).tobytes())]
