@@ -174,8 +174,9 @@ TIMER_GATE_UP, TIMER_DOWN, TIMER_ROUTE, TIMER_SELECT = 0, 1, 2, 3
 
 
 def kernel_timing(enable):
-    """Turns the event timing of the fused decode path's routed gate/up and
-    down kernels on or off (measurement only: it waits on every launch)."""
+    """Turns the event timing of the layer's launches (route, select, gate/up,
+    down) on or off. Events are recorded around each launch without a wait;
+    ``kernel_timing_read`` settles and sums them (measurement only)."""
     check(lib().inferno_kernel_timing_enable(1 if enable else 0))
 
 
