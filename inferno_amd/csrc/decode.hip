@@ -282,9 +282,11 @@ __global__ void __launch_bounds__(256) select1_kernel(DecodeArgs p) {
   __shared__ float bias[kMaxExperts];
   const int tid = threadIdx.x, lane = tid & 63;
   const int E = p.E, k = p.k;
-  if (p.bias)
-    for (int e = tid; e < E; e += 256) bias[e] = p.bias[e];
+  // the bias load is issued before the partials' loads and stored after
+  // them, so the two round trips overlap (E <= 256: one expert per thread)
+  const float bv = (p.bias && tid < E) ? p.bias[tid] : 0.f;
   sum_partials(p, 0, logit_row, tid, 256);
+  if (p.bias && tid < E) bias[tid] = bv;
   __syncthreads();
   if (tid >= 64) return;
   uint32_t all[kMaxTopK];  // the k selected ids, held by every lane
