@@ -150,6 +150,13 @@ class GGUFFile:
         self.path = str(path)
         with open(self.path, "rb") as f:
             self._map = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+        try:
+            self._parse()
+        except Exception:
+            self.close()  # unmapped now, or once the traceback's views are gone
+            raise
+
+    def _parse(self):
         self.file_size = len(self._map)
         r = _Reader(memoryview(self._map))
         if bytes(r.take(4)) != MAGIC:
