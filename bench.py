@@ -70,36 +70,48 @@ def main():
     dev = torch.device("cuda:0")
     cfg = cf.CONFIGS[args.config]
     T = args.tokens or cfg.tokens[0]
-    L = args.layers or (8 if T <= 64 else 2)
+    L = args.layers or (2 if T > 64 or cfg.layers > 1 else 8)
     H, E, I, k = cfg.hidden, cfg.experts, cfg.intermediate, cfg.top_k
 
     prefill = T > 64
+    stacked = cfg.layers > 1
+    n_sub = cfg.layers  # MoE layers per step (a stack runs all of the config's layers)
     t0 = time.time()
-    layers = []
+    units = []  # resident copies: one layer, or one whole stack
     for l in range(L):
         c = cf.Config(**{**cfg.__dict__, "index": cfg.index + 100 * l}) if l else cfg
-        layers.append(cf.build_layer(c, 0, dev, max_tokens=T))
-        log(f"[bench] built layer {l + 1}/{L} ({time.time() - t0:.1f}s)")
+        if stacked:
+            units.append(cf.build_stack(c, dev, max_tokens=T))
+        else:
+            lt = cf.build_layer(c, 0, dev, max_tokens=T)
+            units.append(([lt], None))
+        log(f"[bench] built {'stack' if stacked else 'layer'} {l + 1}/{L} ({time.time() - t0:.1f}s)")
     n_inputs = 4 if prefill else 64
     xs = [cf.make_input(cfg, T, variant=v, device=dev) for v in range(n_inputs)]
+    hiddens = [x.float() for x in xs] if stacked else None
     if cfg.zipf or cfg.balanced:
         # correction bias fitted so that the top-k load of the first input
         # follows Zipf(s) (s = 0 for the near-uniform workload); written in
         # place (the layer holds its pointer)
-        for lt in layers:
+        for lts, _ in units:
+            lt = lts[0]
             logits = ops.router_logits(xs[0], lt.router)
             lt.bias.copy_(torch.from_numpy(cf.zipf_bias(cfg, logits.cpu().numpy())).to(dev))
         log(f"[bench] Zipf({cfg.zipf}) load bias fitted ({time.time() - t0:.1f}s)")
     residual = torch.randn(T, H, device=dev)
     out = torch.empty(T, H, device=dev)
-    ids_buf = [torch.empty(T * k, dtype=torch.int32, device=dev) for _ in range(L)]
+    ids_buf = [torch.empty(n_sub * T * k, dtype=torch.int32, device=dev) for _ in range(L)]
     w_buf = [torch.empty(T * k, device=dev) for _ in range(L)]
     torch.cuda.synchronize()
 
     def step(i):
-        l = i % L
-        layers[l].layer.forward(xs[i % n_inputs], residual, out=out, ids=ids_buf[l],
-                                weights=w_buf[l])
+        u = i % L
+        lts, stack = units[u]
+        if stacked:
+            stack.forward(hiddens[i % n_inputs], out=out, ids=ids_buf[u])
+        else:
+            lts[0].layer.forward(xs[i % n_inputs], residual, out=out, ids=ids_buf[u],
+                                 weights=w_buf[u])
 
     for i in range(args.warmup):
         step(i)
@@ -113,61 +125,65 @@ def main():
     tokens_per_s = T * args.steps / elapsed
 
     # ---- per-kernel times and the dominant kernel ----------------------------
-    # Same layer steps again with the event hook on: the C library brackets
-    # each launch of the layer with HIP events on the layer's stream and
-    # labels what the launch covered. Decode: the routed gate/up launch streams
-    # the gate+up bytes of the step's unique selected experts, plus the Q8_0
-    # shared expert's gate+up when the label kind is "tiles"/"ring" (on the
-    # "mfma" path the shared gate/up runs in the route launch instead, label
-    # kind "route+shared"); the down launch streams the routed down bytes plus
-    # the shared down. Prefill: flops per launch = 2 * (2 * H * I) *
+    # Same steps again with the event hook on: the C library brackets each
+    # launch of a layer with HIP events on the layer's stream and labels what
+    # the launch covered (a stack step makes one launch per layer and timer).
+    # Decode: the routed gate/up launch streams the gate+up bytes of the
+    # layer's unique selected experts, plus the Q8_0 shared expert's gate+up
+    # when the label kind is "tiles"/"ring" (on the "mfma" path the shared
+    # gate/up runs in the route launch instead, label kind "route+shared");
+    # the down launch streams the routed down bytes plus the shared down when
+    # the kind is "down8". Prefill: flops per launch = 2 * (2 * H * I) *
     # assignments (routed only).
-    q = cfg.quants[0]
-    bb = ops.block_bytes(q)
-    gu_bytes_per_expert = 2 * I * (H // 256) * bb
-    dn_bytes_per_expert = H * (I // 256) * bb
+    quants = list(cfg.quants)
+    gu_per_expert = [2 * I * (H // 256) * ops.block_bytes(q) for q in quants]
+    dn_per_expert = [H * (I // 256) * ops.block_bytes(q) for q in quants]
     reps = max(args.steps, 64) if not prefill else max(args.steps, 10)
     timers = [ops.TIMER_GATE_UP, ops.TIMER_DOWN] + ([] if prefill else
                                                    [ops.TIMER_ROUTE, ops.TIMER_SELECT])
+    uniq = [0] * n_sub
     ops.kernel_timing(True)
     try:
         for tm in timers:
             ops.kernel_timing_read(tm)
-        uniq = 0
         loads = []
         for i in range(reps):
             step(i)
-            l = i % L
-            uniq += int(torch.unique(ids_buf[l]).numel())
+            u = i % L
+            for j in range(n_sub):
+                uniq[j] += int(torch.unique(ids_buf[u][j * T * k:(j + 1) * T * k]).numel())
             if prefill and i < L:
-                loads.append(torch.bincount(ids_buf[l].long(), minlength=E).cpu())
+                loads.append(torch.bincount(ids_buf[u][:T * k].long(), minlength=E).cpu())
         torch.cuda.synchronize()
         timed = {tm: ops.kernel_timing_read(tm) for tm in timers}
         labels = {tm: ops.kernel_timing_label(tm) for tm in timers}
     finally:
         ops.kernel_timing(False)
+    launches = reps * n_sub
     for tm in timers:
-        if timed[tm][1] != reps:
-            raise RuntimeError(f"kernel timer {tm} saw {timed[tm][1]} launches for {reps} steps")
-    us = {tm: 1e3 * timed[tm][0] / timed[tm][1] for tm in timers}
+        if timed[tm][1] != launches:
+            raise RuntimeError(f"kernel timer {tm} saw {timed[tm][1]} launches for {launches}")
+    us = {tm: 1e3 * timed[tm][0] / timed[tm][1] for tm in timers}  # per launch
     gu_us, dn_us = us[ops.TIMER_GATE_UP], us[ops.TIMER_DOWN]
-    uniq_layer = uniq / reps
+    uniq_sub = [u / reps for u in uniq]  # unique experts per step, per layer of the step
     layer_us = ms_per_step * 1e3
-    layer_routed_bytes = (gu_bytes_per_expert + dn_bytes_per_expert) * uniq_layer
-    shared_bytes = 3 * cfg.shared_intermediate * (H // 32) * 34 if cfg.shared_intermediate else 0
-    router_bytes = E * H * 4
+    gu_routed = sum(g * u for g, u in zip(gu_per_expert, uniq_sub)) / n_sub  # per launch
+    dn_routed = sum(d * u for d, u in zip(dn_per_expert, uniq_sub)) / n_sub
+    layer_routed_bytes = (gu_routed + dn_routed) * n_sub
+    shared_bytes = n_sub * 3 * cfg.shared_intermediate * (H // 32) * 34 if cfg.shared_intermediate else 0
+    router_bytes = n_sub * E * H * 4
     extra = {}
     if not prefill:
         shared_gu = 2 * cfg.shared_intermediate * (H // 32) * 34
         shared_dn = cfg.shared_intermediate * (H // 32) * 34
-        gu_kind = labels[ops.TIMER_GATE_UP].split(":")[0]
-        rt_kind = labels[ops.TIMER_ROUTE].split(":")[0]
-        dn_kind = labels[ops.TIMER_DOWN].split(":")[0]
-        sl_kind = labels[ops.TIMER_SELECT].split(":")[0]
-        gu_routed = gu_bytes_per_expert * uniq_layer
+        kinds = {tm: labels[tm].split(":")[0] for tm in timers}
+        # a stack mixes formats: the label is the last layer's, so the shared
+        # bytes follow the kind of each layer's launch, read per layer below
+        gu_kind, dn_kind = kinds[ops.TIMER_GATE_UP], kinds[ops.TIMER_DOWN]
+        rt_kind, sl_kind = kinds[ops.TIMER_ROUTE], kinds[ops.TIMER_SELECT]
         kernels = {
             "route": {"label": labels[ops.TIMER_ROUTE], "launch_us": us[ops.TIMER_ROUTE],
-                      "bytes_per_launch": router_bytes + (shared_gu if rt_kind == "route+shared" else 0)},
+                      "bytes_per_launch": E * H * 4 + (shared_gu if rt_kind == "route+shared" else 0)},
             "select": {"label": labels[ops.TIMER_SELECT], "launch_us": us[ops.TIMER_SELECT],
                        "bytes_per_launch": shared_dn if sl_kind == "select+shared-down" else None},
             "gate_up": {"label": labels[ops.TIMER_GATE_UP], "launch_us": gu_us,
@@ -176,12 +192,14 @@ def main():
                         "traffic_file": {"mfma": "gate_up_mfma_q2k_c2_decode_traffic.txt",
                                          "tiles": "gate_up_q2k_c2_decode_traffic.txt"}.get(gu_kind)},
             "down": {"label": labels[ops.TIMER_DOWN], "launch_us": dn_us,
-                     "bytes_per_launch": dn_bytes_per_expert * uniq_layer
-                     + (shared_dn if dn_kind == "down8" else 0),
-                     "routed_bytes_per_launch": dn_bytes_per_expert * uniq_layer,
+                     "bytes_per_launch": dn_routed + (shared_dn if dn_kind == "down8" else 0),
+                     "routed_bytes_per_launch": dn_routed,
                      "traffic_file": {"down8": "down8_q2k_c2_decode_traffic.txt",
                                       "mfma-down": "down_mfma_q2k_c2_decode_traffic.txt"}.get(dn_kind)},
         }
+        if stacked:
+            for kd in kernels.values():
+                kd["label"] = f"{kd['label']} [last of {n_sub} layers; times and bytes averaged per launch]"
         for kd in kernels.values():
             b = kd["bytes_per_launch"]
             kd["launch_us"] = round(kd["launch_us"], 3)
@@ -204,6 +222,8 @@ def main():
                     "launch_us": kd["launch_us"], "bytes_per_launch": kd["bytes_per_launch"],
                     "routed_bytes_per_launch": kd["routed_bytes_per_launch"]}
         extra["kernels"] = kernels
+        if stacked:
+            extra["unique_experts_per_layer"] = [round(u, 3) for u in uniq_sub]
     else:
         A = T * k
         gu_flops = 4.0 * H * I * A
@@ -214,9 +234,9 @@ def main():
                     "unit": "TFLOP/s", "frac": round(gu_tfs / MFMA_BF16_PEAK_TFLOPS, 4),
                     "traffic": None, "launch_us": round(gu_us, 3),
                     "flops_per_launch": gu_flops,
-                    "routed_bytes_per_launch": int(gu_bytes_per_expert * uniq_layer)}
+                    "routed_bytes_per_launch": int(gu_routed)}
         extra["down_launch"] = {"launch_us": round(dn_us, 3), "TFLOPs": round(dn_tfs, 2)}
-        extra["layer_mfma_frac"] = round(6.0 * H * I * A / (layer_us * 1e-6) / 1e12
+        extra["layer_mfma_frac"] = round(6.0 * H * I * A * n_sub / (layer_us * 1e-6) / 1e12
                                          / MFMA_BF16_PEAK_TFLOPS, 4)
         load = torch.stack(loads).float().mean(0)
         extra["expert_load"] = {"active": int((load > 0).sum()), "hottest_share":
@@ -226,7 +246,7 @@ def main():
     # ---- CPU baseline: oracle on the host cores -------------------------
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(cfg, layers, xs, residual, T, args.cpu_seconds)
+        cpu = cpu_baseline(cfg, units, xs, residual, T, args.cpu_seconds)
 
     # arithmetic of the gate/up kernel that ran (decode MFMA: x as two e4m3
     # terms times Q2_K fields as e2m1, down on f16 MFMA; prefill: f16 MFMA;
@@ -253,9 +273,13 @@ def main():
         "dtype": dtype,
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantised on device)",
         "config": {"workload": cfg.name, "tokens": T, "hidden": H, "experts": E,
-                   "intermediate": I, "top_k": k, "quant": QUANT_NAMES.get(q, str(q)),
-                   "shared_intermediate": cfg.shared_intermediate, "layers_resident": L},
+                   "intermediate": I, "top_k": k, "quant": QUANT_NAMES.get(quants[0], str(quants[0])),
+                   "shared_intermediate": cfg.shared_intermediate,
+                   "layers_per_step": n_sub, "quants": [QUANT_NAMES.get(x, str(x)) for x in quants],
+                   "rms_norm_eps": cfg.rms_eps if stacked else None,
+                   "copies_resident": L},
         "us_per_token": round(layer_us / T, 3),
+        "us_per_token_per_layer": round(layer_us / T / n_sub, 3),
         "layer_routed_bytes": int(layer_routed_bytes),
         "layer_routed_GBps": round(layer_routed_bytes / (layer_us * 1e-6) / 1e9, 1),
         "layer_total_bytes": int(layer_routed_bytes + shared_bytes + router_bytes),
@@ -298,57 +322,70 @@ def read_traffic(path, kernel):
     return None
 
 
-def cpu_baseline(cfg, layers, xs, residual, T, seconds):
+def cpu_baseline(cfg, units, xs, residual, T, seconds):
     """Times the C++ oracle on a bounded sample of the workload's tokens:
-    decode one token per layer call, prefill chunks of 4 consecutive tokens
-    of the batch, cycling layers. Only the oracle calls are timed; copying
-    the selected experts' bytes to the host is not."""
+    decode one token per step, prefill chunks of 4 consecutive tokens of the
+    batch, cycling the resident copies; a stack step runs every layer (RMSNorm,
+    bf16 rounding, router, routed and shared experts). Only the oracle calls
+    are timed; copying the selected experts' bytes to the host is not."""
     import numpy as np
     import torch
 
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_lib as orc  # test-infrastructure checker, used here only as the CPU baseline
+    import parity_helpers as ph
 
     try:
-        cores = len(os.sched_getaffinity(0))
+        host_cores = len(os.sched_getaffinity(0))
     except AttributeError:
-        cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
-    orc.THREADS = cores
+        host_cores = os.cpu_count() or 1
+    threads = max(1, min(host_cores, 16))
+    orc.THREADS = threads
     k, E = cfg.top_k, cfg.experts
     chunk = 1 if T <= 64 else 4
+    stacked = cfg.layers > 1
     busy, n = 0.0, 0
     while busy < seconds and n < 2048:
-        lt = layers[n % len(layers)]
+        lts, _ = units[n % len(units)]
         j = (n * chunk) % T
         x = xs[n % len(xs)][j:j + chunk].float().cpu().numpy()
-        router = lt.router.cpu().numpy()
-        bias = None if lt.bias is None else lt.bias.cpu().numpy()
-        t0 = time.perf_counter()
-        logits = orc.linear(x, router)
-        ids, w = orc.router_topk(logits, bias, k, cfg.score_fn, cfg.norm, cfg.scale)
-        busy += time.perf_counter() - t0
-        experts = np.unique(ids)
-        sel = torch.as_tensor(experts.astype(np.int64), device=lt.gate.device)
-        g = lt.gate.view(E, -1)[sel].cpu().numpy().reshape(-1)
-        u = lt.up.view(E, -1)[sel].cpu().numpy().reshape(-1)
-        d = lt.down.view(E, -1)[sel].cpu().numpy().reshape(-1)
-        remap = {int(e): i for i, e in enumerate(experts)}
-        ids_c = np.array([remap[int(e)] for e in ids], np.uint32)
-        shared = [s.cpu().numpy() for s in lt.shared] if lt.shared else None
-        res = residual[j:j + chunk].cpu().numpy()
-        t0 = time.perf_counter()
-        routed = orc.moe_routed(lt.quant, lt.quant, g, u, d, x, ids_c, w, len(experts), k,
-                                cfg.intermediate)
-        if shared:
-            orc.shared_q8_0(*shared, x, cfg.shared_intermediate, routed=routed, residual=res)
-        busy += time.perf_counter() - t0
+        r = x.copy() if stacked else residual[j:j + chunk].cpu().numpy()
+        for lt in lts:
+            router = lt.router.cpu().numpy()
+            bias = None if lt.bias is None else lt.bias.cpu().numpy()
+            t0 = time.perf_counter()
+            if stacked:
+                x = orc.rms_norm(r, lt.norm_w.cpu().numpy(), cfg.rms_eps)
+                if cfg.x_dtype == torch.bfloat16:
+                    x = ph.bf16_round(x)
+            logits = orc.linear(x, router)
+            ids, w = orc.router_topk(logits, bias, k, cfg.score_fn, cfg.norm, cfg.scale)
+            busy += time.perf_counter() - t0
+            experts = np.unique(ids)
+            sel = torch.as_tensor(experts.astype(np.int64), device=lt.gate.device)
+            g = lt.gate.view(E, -1)[sel].cpu().numpy().reshape(-1)
+            u = lt.up.view(E, -1)[sel].cpu().numpy().reshape(-1)
+            d = lt.down.view(E, -1)[sel].cpu().numpy().reshape(-1)
+            remap = {int(e): i for i, e in enumerate(experts)}
+            ids_c = np.array([remap[int(e)] for e in ids], np.uint32)
+            shared = [s.cpu().numpy() for s in lt.shared] if lt.shared else None
+            t0 = time.perf_counter()
+            routed = orc.moe_routed(lt.quant, lt.quant, g, u, d, x, ids_c, w, len(experts), k,
+                                    cfg.intermediate)
+            if shared:
+                r = orc.shared_q8_0(*shared, x, cfg.shared_intermediate, routed=routed, residual=r)
+            else:
+                r = routed + r
+            busy += time.perf_counter() - t0
         n += 1
-    what = "decode tokens (T=1 layer forwards" if chunk == 1 else \
-        f"prefill tokens (layer forwards over chunks of {chunk} tokens"
-    return {"value": round(n * chunk / busy, 4), "unit": "tokens/s", "cores": cores,
-            "kind": "port",
-            "sample": f"{n * chunk} {what} incl. router, routed experts and shared expert) "
+    what = ("decode tokens (T=1 forwards" if chunk == 1 else
+            f"prefill tokens (forwards over chunks of {chunk} tokens")
+    what += f" of all {cfg.layers} layers with RMSNorm" if stacked else " of the layer"
+    return {"value": round(n * chunk / busy, 4), "unit": "tokens/s", "cores": threads,
+            "host_cores": host_cores, "kind": "port",
+            "threads_note": "oracle worker threads = min(host cores in this process's "
+                            "affinity, 16); threads are spawned per oracle call",
+            "sample": f"{n * chunk} {what}, incl. router, routed experts and shared expert) "
                       f"in {busy:.1f}s of oracle time"}
 
 

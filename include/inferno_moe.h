@@ -244,6 +244,26 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* layer, cons
                               uint32_t* expert_ids_out, float* expert_weights_out,
                               void* workspace, size_t workspace_bytes);
 
+/* ---------------------------------------------------------- layer stack */
+
+/* n_layers consecutive MoE layers on one residual stream, as the reference
+ * decoder runs its MoE blocks (crates/model/src/laguna/gguf_model.rs:612-657,
+ * attention left out): for each layer l,
+ *   a_l     = rms_norm(r_l, norm_weights[l], eps)   (backend.rs:10211-10257),
+ *             rounded to act_dtype (BF16: nearest even; F32: as is);
+ *   r_{l+1} = r_l + routed_l(a_l) + shared_l(a_l)   (inferno_moe_layer_forward,
+ *             residual = r_l).
+ * hidden = r_0, fp32 [T,H]; out = r_n, fp32 [T,H] (must not alias hidden).
+ * norm_weights is a HOST array of n_layers device pointers to fp32 [H].
+ * expert_ids_out (may be NULL) receives each layer's routing, layer after
+ * layer: [T*k_0] then [T*k_1] ... Every layer must have the same hidden size. */
+size_t inferno_moe_stack_workspace_bytes(const inferno_moe_layer* layers, size_t n_layers,
+                                         size_t T);
+int inferno_moe_stack_forward(void* stream, const inferno_moe_layer* layers, size_t n_layers,
+                              const float* const* norm_weights, float eps, int act_dtype,
+                              const float* hidden, size_t T, float* out,
+                              uint32_t* expert_ids_out, void* workspace, size_t workspace_bytes);
+
 /* ------------------------------------------------------- kernel timing */
 
 /* Measurement hook with no counterpart in the reference (benchmarks only).

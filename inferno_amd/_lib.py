@@ -62,6 +62,9 @@ SIGNATURES = {
     "inferno_moe_layer_workspace_bytes": (_sz, [C.POINTER(LayerDesc), _sz]),
     "inferno_moe_layer_forward": (_i, [_vp, C.POINTER(LayerDesc), _vp, _i, _vp, _sz, _vp, _vp,
                                        _vp, _vp, _sz]),
+    "inferno_moe_stack_workspace_bytes": (_sz, [C.POINTER(LayerDesc), _sz, _sz]),
+    "inferno_moe_stack_forward": (_i, [_vp, C.POINTER(LayerDesc), _sz, C.POINTER(_vp), _f, _i,
+                                       _vp, _sz, _vp, _vp, _vp, _sz]),
     "inferno_synth_normal": (_i, [_vp, _u64, _f, _sz, _i, _vp]),
     "inferno_synth_normal_host": (_i, [_u64, _f, _sz, _vp]),
     "inferno_quantize_rows_host": (_i, [_i, _vp, _sz, _sz, _vp]),

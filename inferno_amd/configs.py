@@ -146,3 +146,18 @@ def zipf_bias(cfg, logits, iters=200):
         live = target > 0
         bias[live] += 0.05 * (np.log(target[live] + 1) - np.log(count[live] + 1))
     return bias.astype(np.float32)
+
+
+def build_stack(cfg, device="cuda", max_tokens=1):
+    """The config's consecutive layers (one per entry of cfg.quants), each
+    with its own seeded tensors and RMSNorm weight, as an ops.MoEStack."""
+    lts = [build_layer(cfg, l, device, max_tokens=max_tokens) for l in range(cfg.layers)]
+    stack = ops.MoEStack([lt.layer for lt in lts], [lt.norm_w for lt in lts], eps=cfg.rms_eps,
+                         act_dtype=cfg.x_dtype, max_tokens=max_tokens)
+    return lts, stack
+
+
+def make_hidden(cfg, T, variant=0, device="cuda"):
+    """fp32 residual stream entering the stack: the config's N(0, 1)
+    activations (bf16 values for bf16 configs) held as fp32."""
+    return make_input(cfg, T, variant, device).float()

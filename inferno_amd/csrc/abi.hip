@@ -399,7 +399,7 @@ int inferno_rms_norm(void* stream, const float* x, const float* w, size_t rows, 
   clear_error();
   INF_CHECK_ARG(H > 0 && eps >= 0.f, "rms_norm needs a positive width and eps >= 0");
   INF_CHECK_ARG(rows == 0 || (x && w && out), "null pointer");
-  return launch_rms_norm(as_stream(stream), x, w, rows, H, eps, out);
+  return launch_rms_norm(as_stream(stream), x, w, rows, H, eps, out, INFERNO_F32);
 }
 
 // ------------------------------------------------------------- layer
@@ -531,6 +531,81 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
                                   w.moe.y, k, nullptr, residual, T, Is, H, out);
   }
   return launch_topk_combine(s, nullptr, residual, w.moe.y, nullptr, T, H, k, out);
+}
+
+// ------------------------------------------------------------- stack
+
+namespace {
+struct StackScratch {
+  void* normed;      // [T, H] activations of the current layer (fp32 or bf16)
+  float* stream[2];  // [T, H] residual stream between layers (ping-pong)
+  void* layer_ws;    // the layers' own workspace (the largest one)
+  size_t layer_ws_bytes;
+};
+StackScratch carve_stack(Carver& c, const inferno_moe_layer* layers, size_t n, size_t T) {
+  StackScratch s;
+  const size_t H = n ? layers[0].hidden : 0;
+  s.normed = c.take<float>(T * H);
+  // layer l (but the last) writes stream[l & 1]
+  s.stream[0] = c.take<float>(n > 1 ? T * H : 0);
+  s.stream[1] = c.take<float>(n > 2 ? T * H : 0);
+  size_t most = 0;
+  for (size_t l = 0; l < n; ++l) most = std::max(most, inferno_moe_layer_workspace_bytes(&layers[l], T));
+  s.layer_ws = c.take<char>(most);
+  s.layer_ws_bytes = most;
+  return s;
+}
+}  // namespace
+
+size_t inferno_moe_stack_workspace_bytes(const inferno_moe_layer* layers, size_t n_layers,
+                                         size_t T) {
+  if (!layers || n_layers == 0) return 0;
+  Carver c{nullptr};
+  carve_stack(c, layers, n_layers, T);
+  return c.used;
+}
+
+int inferno_moe_stack_forward(void* stream, const inferno_moe_layer* layers, size_t n_layers,
+                              const float* const* norm_weights, float eps, int act_dtype,
+                              const float* hidden, size_t T, float* out,
+                              uint32_t* expert_ids_out, void* workspace, size_t workspace_bytes) {
+  clear_error();
+  INF_CHECK_ARG(layers != nullptr && norm_weights != nullptr && n_layers > 0, "empty layer stack");
+  INF_CHECK_ARG(act_dtype == INFERNO_F32 || act_dtype == INFERNO_BF16,
+                "activation dtype must be F32 or BF16");
+  INF_CHECK_ARG(eps >= 0.f && std::isfinite(eps), "rms_norm eps must be finite and >= 0");
+  INF_CHECK_ARG(hidden && out && workspace && T > 0, "null pointer or no tokens");
+  INF_CHECK_ARG(hidden != out, "the stack output must not alias its input");
+  const size_t H = layers[0].hidden;
+  for (size_t l = 0; l < n_layers; ++l) {
+    INF_CHECK_ARG(layers[l].hidden == H, "every layer of a stack must have the same hidden size");
+    INF_CHECK_ARG(norm_weights[l] != nullptr, "null RMSNorm weight");
+  }
+  const size_t need = inferno_moe_stack_workspace_bytes(layers, n_layers, T);
+  if (workspace_bytes < need) {
+    set_error("workspace too small: need " + std::to_string(need) + " bytes");
+    return INFERNO_ERR_SIZE;
+  }
+  Carver c{static_cast<char*>(workspace)};
+  StackScratch w = carve_stack(c, layers, n_layers, T);
+  hipStream_t s = as_stream(stream);
+  const float* r = hidden;
+  size_t id_off = 0;
+  for (size_t l = 0; l < n_layers; ++l) {
+    float* next = l + 1 == n_layers ? out : w.stream[l & 1];
+    int st = launch_rms_norm(s, r, norm_weights[l], T, H, eps, w.normed, act_dtype);
+    if (st) return st;
+    st = inferno_moe_layer_forward(stream, &layers[l], w.normed, act_dtype, r, T, next,
+                                   expert_ids_out ? expert_ids_out + id_off : nullptr, nullptr,
+                                   w.layer_ws, w.layer_ws_bytes);
+    if (st) {
+      set_error("layer " + std::to_string(l) + ": " + g_last_error);
+      return st;
+    }
+    id_off += T * layers[l].top_k;
+    r = next;
+  }
+  return INFERNO_OK;
 }
 
 // ------------------------------------------------------ synthetic data

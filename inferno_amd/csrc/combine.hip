@@ -1,6 +1,8 @@
 // Data movement and combine kernels. Every output element is written by one
 // thread that sums its contributions in a fixed order — no float atomics, so
 // results are bitwise reproducible run to run.
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace inferno {
@@ -50,9 +52,12 @@ __global__ void __launch_bounds__(256)
 }
 
 // One workgroup per row; fp32 sum of squares reduced in a fixed tree order.
+// The output is fp32 or bf16 (round to nearest even), the activation type a
+// following layer consumes.
+template <typename OutT>
 __global__ void __launch_bounds__(256)
     rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, size_t H, float eps,
-                    float* __restrict__ out) {
+                    OutT* __restrict__ out) {
   __shared__ float part[256];
   const float* row = x + size_t(blockIdx.x) * H;
   float s = 0.f;
@@ -64,8 +69,13 @@ __global__ void __launch_bounds__(256)
     __syncthreads();
   }
   float scale = sqrtf(part[0] / float(H) + eps);
-  for (size_t i = threadIdx.x; i < H; i += 256)
-    out[size_t(blockIdx.x) * H + i] = row[i] / scale * w[i];
+  for (size_t i = threadIdx.x; i < H; i += 256) {
+    const float v = row[i] / scale * w[i];
+    if constexpr (std::is_same<OutT, float>::value)
+      out[size_t(blockIdx.x) * H + i] = v;
+    else
+      out[size_t(blockIdx.x) * H + i] = f32_to_bf16_bits(v);
+  }
 }
 
 unsigned blocks_for(size_t n) { return unsigned((n + 255) / 256); }
@@ -100,9 +110,13 @@ int launch_gather(hipStream_t s, const float* x, const uint32_t* tok, size_t T, 
 }
 
 int launch_rms_norm(hipStream_t s, const float* x, const float* w, size_t rows, size_t H,
-                    float eps, float* out) {
+                    float eps, void* out, int out_dtype) {
   if (rows == 0) return INFERNO_OK;
-  rms_norm_kernel<<<unsigned(rows), 256, 0, s>>>(x, w, H, eps, out);
+  if (out_dtype == INFERNO_BF16)
+    rms_norm_kernel<uint16_t><<<unsigned(rows), 256, 0, s>>>(x, w, H, eps,
+                                                             static_cast<uint16_t*>(out));
+  else
+    rms_norm_kernel<float><<<unsigned(rows), 256, 0, s>>>(x, w, H, eps, static_cast<float*>(out));
   INF_LAUNCHED();
   return INFERNO_OK;
 }

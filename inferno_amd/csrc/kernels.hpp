@@ -52,7 +52,8 @@ int launch_index_add_combine(hipStream_t s, const float* acc, const uint32_t* to
                              size_t H, size_t A, float* out);
 int launch_gather(hipStream_t s, const float* x, const uint32_t* token_idx, size_t T, size_t H,
                   size_t A, float* out);
+// out is fp32 or bf16 (out_dtype INFERNO_F32 / INFERNO_BF16)
 int launch_rms_norm(hipStream_t s, const float* x, const float* w, size_t rows, size_t H,
-                    float eps, float* out);
+                    float eps, void* out, int out_dtype = INFERNO_F32);
 
 }  // namespace inferno

@@ -271,3 +271,41 @@ class MoELayer:
             _s(), C.byref(self.desc), _p(_dev(x)), _DT[x.dtype], _p(residual), T, _p(out),
             _p(ids), _p(weights), _p(self._ws), self._ws.numel()))
         return out
+
+
+class MoEStack:
+    """Consecutive MoE layers on one residual stream (inferno_moe_stack_forward):
+    for each layer, RMSNorm of the stream (rounded to ``act_dtype``), then
+    stream += routed + shared expert outputs of the normalised activations."""
+
+    def __init__(self, layers, norm_weights, eps=1e-6, act_dtype=torch.bfloat16, max_tokens=1):
+        if len(layers) != len(norm_weights) or not layers:
+            raise ValueError("one RMSNorm weight per layer is needed")
+        self.layers = list(layers)
+        self.norm_weights = list(norm_weights)
+        self.eps, self.act_dtype = float(eps), act_dtype
+        n = len(layers)
+        self.descs = (LayerDesc * n)(*[l.desc for l in layers])
+        self.norm_ptrs = (C.c_void_p * n)(*[w.data_ptr() for w in norm_weights])
+        self.hidden = layers[0].hidden
+        self.device = layers[0].device
+        self._ws = None
+        self.reserve(max_tokens)
+
+    def reserve(self, T):
+        need = lib().inferno_moe_stack_workspace_bytes(self.descs, len(self.layers), T)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+
+    def forward(self, hidden, out=None, ids=None):
+        """hidden: fp32 [T, H] residual stream. ids (optional int32 tensor of
+        sum_l T*k_l) receives every layer's routing, layer after layer."""
+        T = hidden.shape[0]
+        self.reserve(T)
+        if out is None:
+            out = torch.empty(T, self.hidden, dtype=torch.float32, device=hidden.device)
+        check(lib().inferno_moe_stack_forward(
+            _s(), self.descs, len(self.layers), self.norm_ptrs, self.eps, _DT[self.act_dtype],
+            _p(_dev(hidden)), T, _p(out), _p(ids), _p(self._ws), self._ws.numel()))
+        return out
+
