@@ -254,3 +254,16 @@ def test_shared_q8_0_matches_fp64():
     hs = rn.silu(x64 @ Wg.T) * (x64 @ Wu.T)
     ref = ra + rb + hs @ Wd.T
     assert rn.rel_l2(got, ref) < 1e-5
+
+
+def test_bf16_round_matches_torch_nearest_even():
+    # the host-side bf16 rounding the stack tests use, against torch's
+    # fp32 -> bf16 conversion (round to nearest even), ties included
+    import parity_helpers as ph
+    import torch
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(100000) * 10.0 ** rng.integers(-20, 20, 100000)).astype(np.float32)
+    ties = (rng.integers(0, 0x7F00, 1000, dtype=np.uint32) << 16) | 0x8000  # finite
+    x = np.concatenate([x, ties.view(np.float32), np.float32([0.0, -0.0, 1.0, 65504.0])])
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(ph.bf16_round(x).view(np.uint32), want.view(np.uint32))
