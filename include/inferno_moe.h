@@ -244,6 +244,23 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* layer, cons
                               uint32_t* expert_ids_out, float* expert_weights_out,
                               void* workspace, size_t workspace_bytes);
 
+/* inferno_moe_layer_forward without a workspace argument and without any
+ * device allocation. No counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Its scratch is a fixed device array of
+ * inferno_moe_layer_noalloc_max_bytes() bytes (32 MiB) per GPU, held until
+ * the process ends; shapes whose inferno_moe_layer_workspace_bytes exceeds it
+ * return INFERNO_ERR_SIZE (decode up to T = 32 fits the c2 and c4 shapes).
+ * Every call on one GPU uses that GPU's one array: calls that overlap on a GPU
+ * (several streams or threads) race and must be serialised by the caller.
+ * Nothing in the scratch needs to start at zero; it keeps the last call's
+ * contents. */
+size_t inferno_moe_layer_noalloc_max_bytes(void);
+int inferno_moe_layer_forward_noalloc(void* stream, const inferno_moe_layer* layer,
+                                      const void* x, int x_dtype, const float* residual,
+                                      size_t T, float* out, uint32_t* expert_ids_out,
+                                      float* expert_weights_out);
+
 /* ---------------------------------------------------------- layer stack */
 
 /* n_layers consecutive MoE layers on one residual stream, as the reference

@@ -62,6 +62,9 @@ SIGNATURES = {
     "inferno_moe_layer_workspace_bytes": (_sz, [C.POINTER(LayerDesc), _sz]),
     "inferno_moe_layer_forward": (_i, [_vp, C.POINTER(LayerDesc), _vp, _i, _vp, _sz, _vp, _vp,
                                        _vp, _vp, _sz]),
+    "inferno_moe_layer_noalloc_max_bytes": (_sz, []),
+    "inferno_moe_layer_forward_noalloc": (_i, [_vp, C.POINTER(LayerDesc), _vp, _i, _vp, _sz,
+                                               _vp, _vp, _vp]),
     "inferno_moe_stack_workspace_bytes": (_sz, [C.POINTER(LayerDesc), _sz, _sz]),
     "inferno_moe_stack_forward": (_i, [_vp, C.POINTER(LayerDesc), _sz, C.POINTER(_vp), _f, _i,
                                        _vp, _sz, _vp, _vp, _vp, _sz]),

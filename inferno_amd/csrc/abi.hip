@@ -3,6 +3,7 @@
 // crates/backend/src/metal/moe.rs:582-623), workspace carving and kernel
 // sequencing. No function allocates device memory or synchronises.
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -531,6 +532,64 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
                                   w.moe.y, k, nullptr, residual, T, Is, H, out);
   }
   return launch_topk_combine(s, nullptr, residual, w.moe.y, nullptr, T, H, k, out);
+}
+
+// ------------------------------------------------- layer, no allocation
+
+namespace {
+// Device-resident scratch for inferno_moe_layer_forward_noalloc: one copy per
+// GPU (each device's code object holds its own), kept until the process ends.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of the current device's `scratch` (host code may not use
+// the array's name as an address); looked up once per device.
+int scratch_ptr(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("no-alloc layer: cannot query the current device");
+    return INFERNO_ERR_DEVICE;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error(std::string("no-alloc layer: hipGetSymbolAddress(scratch) failed: ") +
+                hipGetErrorString(e));
+      return INFERNO_ERR_DEVICE;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return INFERNO_OK;
+}
+}  // namespace
+
+size_t inferno_moe_layer_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+int inferno_moe_layer_forward_noalloc(void* stream, const inferno_moe_layer* L, const void* x,
+                                      int x_dtype, const float* residual, size_t T, float* out,
+                                      uint32_t* expert_ids_out, float* expert_weights_out) {
+  clear_error();
+  INF_CHECK_ARG(L != nullptr, "null layer");
+  const size_t need = inferno_moe_layer_workspace_bytes(L, T);
+  if (need > kNoAllocScratchBytes) {
+    set_error("no-alloc layer: these shapes need " + std::to_string(need) +
+              " bytes of scratch, above the fixed maximum of " +
+              std::to_string(kNoAllocScratchBytes) + " (use inferno_moe_layer_forward with a "
+              "caller workspace)");
+    return INFERNO_ERR_SIZE;
+  }
+  void* ws = nullptr;
+  int st = scratch_ptr(&ws);
+  if (st) return st;
+  return inferno_moe_layer_forward(stream, L, x, x_dtype, residual, T, out, expert_ids_out,
+                                   expert_weights_out, ws, kNoAllocScratchBytes);
 }
 
 // ------------------------------------------------------------- stack

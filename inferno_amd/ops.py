@@ -309,3 +309,15 @@ class MoEStack:
             _p(_dev(hidden)), T, _p(out), _p(ids), _p(self._ws), self._ws.numel()))
         return out
 
+
+def layer_forward_noalloc(layer, x, residual=None, out=None, ids=None, weights=None):
+    """``layer``'s forward through inferno_moe_layer_forward_noalloc: the
+    library's fixed device scratch instead of a workspace (no allocation in
+    the library; ``out`` is allocated here when not given)."""
+    T = x.shape[0]
+    if out is None:
+        out = torch.empty(T, layer.hidden, dtype=torch.float32, device=x.device)
+    check(lib().inferno_moe_layer_forward_noalloc(
+        _s(), C.byref(layer.desc), _p(_dev(x)), _DT[x.dtype], _p(residual), T, _p(out), _p(ids),
+        _p(weights)))
+    return out
