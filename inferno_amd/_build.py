@@ -53,7 +53,7 @@ def build_hip():
 
 def build_oracle():
     tmp = ORACLE_LIB.with_suffix(".so.tmp")
-    _run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared",
+    _run(["g++", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared",
           "-pthread", "-o", str(tmp), str(ORACLE_DIR / "oracle.cpp")])
     os.replace(tmp, ORACLE_LIB)
     return ORACLE_LIB

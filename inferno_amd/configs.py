@@ -31,6 +31,7 @@ class Config:
     tokens: tuple
     zipf: float = 0.0          # >0: bias calibrated so expert load follows Zipf(s)
     balanced: bool = False     # bias calibrated so expert load is near-uniform (Zipf(0))
+    zipf_empty: int = 0        # experts given no slot by the calibrated bias
     rms_eps: float = 1e-6
     notes: str = ""
     weight_std: float = 0.02
@@ -55,7 +56,7 @@ CONFIGS = {
                  (Q2_K, Q2_K, Q3_K, Q3_K), SCORE_SOFTMAX, True, 1.0, 0.0, 1536, torch.bfloat16,
                  (1, 32)),
     "c5": Config("c5_glm_q2k_prefill_t4096_zipf", 4, 6144, 256, 2048, 8, (Q2_K,), SCORE_SIGMOID,
-                 True, 2.5, 0.1, 2048, torch.bfloat16, (4096,), zipf=1.1),
+                 True, 2.5, 0.1, 2048, torch.bfloat16, (4096,), zipf=1.1, zipf_empty=40),
 }
 
 # sub-stream ids
@@ -112,40 +113,65 @@ def build_layer(cfg, layer=0, device="cuda", max_tokens=1, bias=None):
     return lt
 
 
-def zipf_bias(cfg, logits, iters=200):
-    """Correction bias that makes top-k load follow Zipf(cfg.zipf) (cfg.zipf
-    = 0: equal load, for the near-uniform workload).
-
-    Target share of rank r is r^-s normalised; an expert can take at most one
-    slot per token, so targets are capped at T and the excess is spread over
-    the rest; experts whose target is below half a slot get none. The bias is
-    fitted by multiplicative updates on the host (numpy) from the device
-    logits of the actual input.
-    """
-    T, E = logits.shape
-    k = cfg.top_k
+def load_targets(cfg, T):
+    """Integer slot counts per expert rank for a T-token batch: Zipf(cfg.zipf)
+    over the first E - cfg.zipf_empty ranks (cfg.zipf = 0: equal load), none
+    for the last cfg.zipf_empty. An expert takes at most one slot per token,
+    so a share above T slots is capped at T (for top-8: 12.5% of the slots)
+    and the excess spread over the other active ranks in proportion."""
+    E, k = cfg.experts, cfg.top_k
     A = T * k
-    p = np.arange(1, E + 1, dtype=np.float64) ** (-cfg.zipf)
+    active = E - cfg.zipf_empty
+    p = np.zeros(E)
+    p[:active] = np.arange(1, active + 1, dtype=np.float64) ** (-cfg.zipf)
     target = A * p / p.sum()
-    for _ in range(10):
+    for _ in range(64):
         over = target > T
         if not over.any():
             break
         excess = (target[over] - T).sum()
         target[over] = T
-        rest = ~over
+        rest = (~over) & (p > 0)
         target[rest] += excess * target[rest] / target[rest].sum()
-    target[target < 0.5] = 0.0
-    target *= A / target.sum()
+    counts = np.floor(target).astype(np.int64)
+    counts[np.argsort(-(target - counts), kind="stable")[:A - counts.sum()]] += 1
+    return counts
+
+
+def zipf_bias(cfg, logits, iters=60):
+    """Correction bias that gives expert e exactly load_targets(cfg, T)[e]
+    top-k slots on these router logits (sigmoid scores), to within a slot.
+
+    Damped best response: with the other experts' biases fixed, expert e is
+    selected by token t exactly when score[t, e] + b_e exceeds the k-th
+    largest selection value among the other experts of t; the bias that gives
+    e its target count c is the midpoint between the c-th and (c+1)-th
+    smallest of those margins. Every expert moves halfway to its best
+    response per iteration (numpy, on the host, from the device logits).
+    """
+    T, E = logits.shape
+    k = cfg.top_k
+    target = load_targets(cfg, T)
     score = 1.0 / (1.0 + np.exp(-logits.astype(np.float64)))
-    bias = np.where(target > 0, 0.0, -4.0)
+    b = np.zeros(E)
     for _ in range(iters):
-        sel = score + bias
-        top = np.argpartition(-sel, k - 1, axis=1)[:, :k]
-        count = np.bincount(top.reshape(-1), minlength=E).astype(np.float64)
-        live = target > 0
-        bias[live] += 0.05 * (np.log(target[live] + 1) - np.log(count[live] + 1))
-    return bias.astype(np.float32)
+        sel = score + b
+        top = -np.partition(-sel, k, axis=1)[:, :k + 1]
+        top.sort(axis=1)  # ascending: (k+1)-th largest first
+        kth, k1th = top[:, 1], top[:, 0]
+        thr = np.where(sel >= kth[:, None], k1th[:, None], kth[:, None])
+        need = np.sort(thr - score, axis=0)
+        nb = np.empty(E)
+        for e in range(E):
+            c = target[e]
+            if c == 0:
+                nb[e] = need[0, e] - 1.0
+            elif c >= T:
+                nb[e] = need[T - 1, e] + 1.0
+            else:
+                nb[e] = 0.5 * (need[c - 1, e] + need[c, e])
+        b = 0.5 * b + 0.5 * nb
+    return b.astype(np.float32)
 
 
 def build_stack(cfg, device="cuda", max_tokens=1):

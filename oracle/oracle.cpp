@@ -185,6 +185,90 @@ int row_dot(int quant, const uint8_t* row, size_t cols, const float* x, float* r
   return 0;
 }
 
+// Dequantises one row (cols values) into out; the values row_dot uses.
+int dq_row(int quant, const uint8_t* row, size_t cols, float* out) {
+  const size_t bv = size_t(oracle_block_values(quant));
+  const size_t bb = size_t(oracle_block_bytes(quant));
+  for (size_t b = 0; b < cols / bv; ++b) {
+    int st = dq_block(quant, row + b * bb, out + b * bv);
+    if (st) return st;
+  }
+  return 0;
+}
+
+// row_dot over an already dequantised row: the same per-block then
+// sequential summation order, so the same fp32 result.
+float dot_dequantized(const float* vals, size_t cols, size_t bv, const float* x) {
+  float sum = 0.0f;
+  for (size_t b = 0; b < cols / bv; ++b) {
+    float bd = 0.0f;
+    for (size_t v = 0; v < bv; ++v) bd += x[b * bv + v] * vals[b * bv + v];
+    sum += bd;
+  }
+  return sum;
+}
+
+// Activation rows interleaved eight at a time, [group][column][8] (lanes
+// past the last row zero), so that one dequantised weight row is dotted with
+// eight rows as eight independent summation chains that advance as a vector.
+struct Panel {
+  size_t n = 0, cols = 0;
+  std::vector<float> data;
+  template <typename RowAt>
+  void build(size_t rows, size_t c, RowAt row_at) {
+    n = rows;
+    cols = c;
+    data.assign(((rows + 7) / 8) * c * 8, 0.0f);
+    for (size_t r = 0; r < rows; ++r) {
+      const float* src = row_at(r);
+      float* dst = data.data() + (r / 8) * c * 8 + (r % 8);
+      for (size_t v = 0; v < c; ++v) dst[v * 8] = src[v];
+    }
+  }
+};
+
+// out[w * n + r] = dot_dequantized(row w of vals, row r of the panel) for
+// nw dequantised weight rows (stride cols) and every panel row: each lane
+// keeps dot_dequantized's order (per-block sums, then blocks in order); the
+// eight lanes are one vector of independent fp32 operations (no
+// contraction), two groups in flight for latency. Panel groups are the outer
+// loop so they stay in cache across the rows.
+typedef float F8 __attribute__((vector_size(32)));
+
+inline F8 load8(const float* p) {
+  F8 v;
+  std::memcpy(&v, p, sizeof(v));
+  return v;
+}
+
+__attribute__((target_clones("avx2", "default")))
+void dot_panel(const float* vals, size_t nw, size_t bv, const Panel& p, float* out) {
+  const size_t groups = (p.n + 7) / 8;
+  for (size_t g = 0; g < groups; g += 2) {
+    const bool two = g + 1 < groups;
+    const float* x0 = p.data.data() + g * p.cols * 8;
+    const float* x1 = two ? x0 + p.cols * 8 : x0;
+    for (size_t w = 0; w < nw; ++w) {
+      const float* wr = vals + w * p.cols;
+      F8 s0 = {}, s1 = {};
+      for (size_t b = 0; b < p.cols; b += bv) {
+        F8 d0 = {}, d1 = {};
+        for (size_t v = b; v < b + bv; ++v) {
+          const float wv = wr[v];
+          d0 += load8(x0 + v * 8) * wv;
+          d1 += load8(x1 + v * 8) * wv;
+        }
+        s0 += d0;
+        s1 += d1;
+      }
+      for (size_t j = 0; j < 8 && g * 8 + j < p.n; ++j) out[w * p.n + g * 8 + j] = s0[j];
+      if (two)
+        for (size_t j = 0; j < 8 && (g + 1) * 8 + j < p.n; ++j)
+          out[w * p.n + (g + 1) * 8 + j] = s1[j];
+    }
+  }
+}
+
 inline float silu(float g) { return g / (1.0f + std::exp(-g)); }
 
 // total_cmp ordering of crates/model/src/moe_router.rs:930-936: the float's
@@ -379,39 +463,91 @@ int oracle_moe_routed(int quant, int down_quant, const uint8_t* gate, const uint
   for (size_t a = 0; a < T * k; ++a)
     if (ids[a] >= E) return -1;
   const size_t grow = H / kKBlock * size_t(gbb), drow = I / kKBlock * size_t(dbb);
+  const size_t gbv = size_t(oracle_block_values(quant)), dbv = size_t(oracle_block_values(down_quant));
   const size_t A = T * k;
+  // assignments of each expert (any order: every (assignment, row) value is
+  // computed on its own); each expert row is dequantised once and dotted with
+  // the activations of all the expert's assignments
+  std::vector<std::vector<uint32_t>> of(E);
+  for (size_t a = 0; a < A; ++a) of[ids[a]].push_back(uint32_t(a));
+  std::vector<uint32_t> used;
+  for (size_t e = 0; e < E; ++e)
+    if (!of[e].empty()) used.push_back(uint32_t(e));
   std::vector<float> h(A * I);
-  std::vector<int> status(std::max<size_t>(A * I, T * H), 0);
+  constexpr size_t kRowsPerItem = 16;
+  const size_t gate_items = (I + kRowsPerItem - 1) / kRowsPerItem;
+  std::vector<int> status(std::max<size_t>(used.size() * gate_items, H), 0);
   // gate/up + SwiGLU * routing weight: gguf_moe_kernels.metal:340-400
-  parallel_for(A * I, threads, [&](size_t b, size_t e) {
-    for (size_t idx = b; idx < e; ++idx) {
-      size_t a = idx / I, i = idx % I;
-      size_t t = a / k, ex = ids[a];
-      float g, u;
-      int s1 = row_dot(quant, gate + (ex * I + i) * grow, H, x + t * H, &g);
-      int s2 = row_dot(quant, up + (ex * I + i) * grow, H, x + t * H, &u);
-      status[idx] = s1 ? s1 : s2;
-      h[idx] = silu(g) * u * weights[a];
+  parallel_for(used.size() * gate_items, threads, [&](size_t b, size_t e) {
+    std::vector<float> gv(kRowsPerItem * H), uv(kRowsPerItem * H), gs(kRowsPerItem * A),
+        us(kRowsPerItem * A);
+    Panel xp;
+    size_t panel_ex = size_t(-1);
+    for (size_t item = b; item < e; ++item) {
+      const size_t ex = used[item / gate_items];
+      const std::vector<uint32_t>& as = of[ex];
+      if (ex != panel_ex) {
+        xp.build(as.size(), H, [&](size_t j) { return x + (as[j] / k) * H; });
+        panel_ex = ex;
+      }
+      const size_t i0 = (item % gate_items) * kRowsPerItem;
+      const size_t nr = std::min(I, i0 + kRowsPerItem) - i0;
+      int st = 0;
+      for (size_t r = 0; r < nr && !st; ++r) {
+        st = dq_row(quant, gate + (ex * I + i0 + r) * grow, H, gv.data() + r * H);
+        if (!st) st = dq_row(quant, up + (ex * I + i0 + r) * grow, H, uv.data() + r * H);
+      }
+      if (st) {
+        status[item] = st;
+        continue;
+      }
+      dot_panel(gv.data(), nr, gbv, xp, gs.data());
+      dot_panel(uv.data(), nr, gbv, xp, us.data());
+      const size_t n = as.size();
+      for (size_t r = 0; r < nr; ++r)
+        for (size_t j = 0; j < n; ++j)
+          h[size_t(as[j]) * I + i0 + r] = silu(gs[r * n + j]) * us[r * n + j] * weights[as[j]];
     }
   });
-  for (size_t i = 0; i < A * I; ++i)
+  for (size_t i = 0; i < status.size(); ++i)
     if (status[i]) return status[i];
   // down, summed over ranks in rank order: gguf_moe_kernels.metal:457-510
-  parallel_for(T * H, threads, [&](size_t b, size_t e) {
-    for (size_t idx = b; idx < e; ++idx) {
-      size_t t = idx / H, o = idx % H;
-      float acc = 0.0f;
-      for (size_t r = 0; r < k; ++r) {
-        size_t a = t * k + r, ex = ids[a];
-        float v;
-        int st = row_dot(down_quant, down + (ex * H + o) * drow, I, h.data() + a * I, &v);
-        if (st) status[idx] = st;
-        acc += v;
-      }
-      y[idx] = acc;
+  const size_t down_items = (H + kRowsPerItem - 1) / kRowsPerItem;
+  std::vector<Panel> hps(E);
+  parallel_for(used.size(), threads, [&](size_t b, size_t e) {
+    for (size_t u = b; u < e; ++u) {
+      const std::vector<uint32_t>& as = of[used[u]];
+      hps[used[u]].build(as.size(), I, [&](size_t j) { return h.data() + size_t(as[j]) * I; });
     }
   });
-  for (size_t i = 0; i < T * H; ++i)
+  parallel_for(down_items, threads, [&](size_t b, size_t e) {
+    std::vector<float> dv(kRowsPerItem * I), v(kRowsPerItem * A), r(kRowsPerItem * A);
+    for (size_t item = b; item < e; ++item) {
+      const size_t o0 = item * kRowsPerItem, nr = std::min(H, o0 + kRowsPerItem) - o0;
+      for (uint32_t ex : used) {
+        const std::vector<uint32_t>& as = of[ex];
+        int st = 0;
+        for (size_t q = 0; q < nr && !st; ++q)
+          st = dq_row(down_quant, down + (ex * H + o0 + q) * drow, I, dv.data() + q * I);
+        if (st) {
+          status[item] = st;
+          break;
+        }
+        dot_panel(dv.data(), nr, dbv, hps[ex], r.data());
+        const size_t n = as.size();
+        for (size_t q = 0; q < nr; ++q)
+          for (size_t j = 0; j < n; ++j) v[q * A + as[j]] = r[q * n + j];
+      }
+      if (status[item]) continue;
+      for (size_t q = 0; q < nr; ++q)
+        for (size_t t = 0; t < T; ++t) {
+          float acc = 0.0f;
+          for (size_t rk = 0; rk < k; ++rk) acc += v[q * A + t * k + rk];
+          y[t * H + o0 + q] = acc;
+        }
+    }
+  });
+  for (size_t i = 0; i < status.size(); ++i)
     if (status[i]) return status[i];
   return 0;
 }
@@ -422,32 +558,47 @@ int oracle_shared_q8_0(const uint8_t* gate, const uint8_t* up, const uint8_t* do
   if (H % 32 || Is % 32) return -1;
   const size_t grow = H / 32 * 34, drow = Is / 32 * 34;
   std::vector<float> hs(T * Is);
-  std::vector<int> status(std::max(T * Is, T * H), 0);
-  // q2_kernels.metal:2133-2235 (Q8_0 gate/up SwiGLU, no routing weight)
-  parallel_for(T * Is, threads, [&](size_t b, size_t e) {
-    for (size_t idx = b; idx < e; ++idx) {
-      size_t t = idx / Is, i = idx % Is;
-      float g, u;
-      int s1 = row_dot(ORC_Q8_0, gate + i * grow, H, x + t * H, &g);
-      int s2 = row_dot(ORC_Q8_0, up + i * grow, H, x + t * H, &u);
-      status[idx] = s1 ? s1 : s2;
-      hs[idx] = silu(g) * u;
+  std::vector<int> status(std::max(Is, H), 0);
+  // q2_kernels.metal:2133-2235 (Q8_0 gate/up SwiGLU, no routing weight); each
+  // weight row dequantised once and dotted with every token
+  Panel xp;
+  xp.build(T, H, [&](size_t t) { return x + t * H; });
+  parallel_for(Is, threads, [&](size_t b, size_t e) {
+    std::vector<float> gv(H), uv(H), gs(T), us(T);
+    for (size_t i = b; i < e; ++i) {
+      int st = dq_row(ORC_Q8_0, gate + i * grow, H, gv.data());
+      if (!st) st = dq_row(ORC_Q8_0, up + i * grow, H, uv.data());
+      if (st) {
+        status[i] = st;
+        continue;
+      }
+      dot_panel(gv.data(), 1, 32, xp, gs.data());
+      dot_panel(uv.data(), 1, 32, xp, us.data());
+      for (size_t t = 0; t < T; ++t) hs[t * Is + i] = silu(gs[t]) * us[t];
     }
   });
-  for (size_t i = 0; i < T * Is; ++i)
+  for (size_t i = 0; i < Is; ++i)
     if (status[i]) return status[i];
   // q2_kernels.metal:2066-2131: residual_a + residual_b + value
-  parallel_for(T * H, threads, [&](size_t b, size_t e) {
-    for (size_t idx = b; idx < e; ++idx) {
-      size_t t = idx / H, o = idx % H;
-      float v;
-      int st = row_dot(ORC_Q8_0, down + o * drow, Is, hs.data() + t * Is, &v);
-      if (st) status[idx] = st;
-      float ra = routed ? routed[idx] : 0.0f, rb = residual ? residual[idx] : 0.0f;
-      out[idx] = ra + rb + v;
+  Panel hp;
+  hp.build(T, Is, [&](size_t t) { return hs.data() + t * Is; });
+  parallel_for(H, threads, [&](size_t b, size_t e) {
+    std::vector<float> dv(Is), r(T);
+    for (size_t o = b; o < e; ++o) {
+      int st = dq_row(ORC_Q8_0, down + o * drow, Is, dv.data());
+      if (st) {
+        status[o] = st;
+        continue;
+      }
+      dot_panel(dv.data(), 1, 32, hp, r.data());
+      for (size_t t = 0; t < T; ++t) {
+        const size_t idx = t * H + o;
+        float ra = routed ? routed[idx] : 0.0f, rb = residual ? residual[idx] : 0.0f;
+        out[idx] = ra + rb + r[t];
+      }
     }
   });
-  for (size_t i = 0; i < T * H; ++i)
+  for (size_t i = 0; i < H; ++i)
     if (status[i]) return status[i];
   return 0;
 }

@@ -24,7 +24,12 @@ _SIG = {
     "oracle_rms_norm": (_i, [_vp, _vp, _sz, _sz, _f, _vp]),
 }
 
-THREADS = 8
+import os as _os
+
+try:
+    THREADS = max(1, min(16, len(_os.sched_getaffinity(0))))
+except AttributeError:
+    THREADS = 8
 
 
 def L():

@@ -267,3 +267,29 @@ def test_bf16_round_matches_torch_nearest_even():
     x = np.concatenate([x, ties.view(np.float32), np.float32([0.0, -0.0, 1.0, 65504.0])])
     want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     assert np.array_equal(ph.bf16_round(x).view(np.uint32), want.view(np.uint32))
+
+
+def test_oracle_batched_rows_match_per_token_calls():
+    # the oracle dequantises each expert row once and dots it with all the
+    # expert's tokens, four summation chains at a time; every token's result
+    # must equal the same token computed on its own (one row per call, the
+    # single-chain path), bit for bit
+    T, H, I, E, k = 9, 512, 256, 4, 3
+    gate = _random_blocks(Q2_K, E * I * H // 256)
+    up = _random_blocks(Q2_K, E * I * H // 256)
+    dn = _random_blocks(Q2_K, E * H * I // 256)
+    x = (0.05 * rng.standard_normal((T, H))).astype(np.float32)
+    ids = rng.integers(0, E, T * k).astype(np.uint32)  # repeats inside a token allowed
+    w = rng.random(T * k).astype(np.float32)
+    batch = orc.moe_routed(Q2_K, Q2_K, gate, up, dn, x, ids, w, E, k, I)
+    for t in range(T):
+        one = orc.moe_routed(Q2_K, Q2_K, gate, up, dn, x[t:t + 1], ids[t * k:(t + 1) * k],
+                             w[t * k:(t + 1) * k], E, k, I)
+        assert np.array_equal(one.view(np.uint32), batch[t:t + 1].view(np.uint32))
+    sg = _random_blocks(Q8_0, 256 * H // 32)
+    su = _random_blocks(Q8_0, 256 * H // 32)
+    sd = _random_blocks(Q8_0, H * 256 // 32)
+    sb = orc.shared_q8_0(sg, su, sd, x, 256, routed=batch)
+    for t in range(T):
+        one = orc.shared_q8_0(sg, su, sd, x[t:t + 1], 256, routed=batch[t:t + 1])
+        assert np.array_equal(one.view(np.uint32), sb[t:t + 1].view(np.uint32))
