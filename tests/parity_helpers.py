@@ -70,22 +70,36 @@ def oracle_layer_tokens(cfg, lt, x, residual, tokens, ids_gpu, w_gpu, bias_np=No
     xs = x_f32(x)[tokens]
     res = None if residual is None else to_np(residual)[tokens]
     g_ids = np.asarray(ids_gpu).reshape(-1, cfg.top_k)[tokens].reshape(-1)
-    return oracle_layer_rows(cfg, lt, xs, res, g_ids, bias_np)
+    g_w = None if w_gpu is None else np.asarray(w_gpu).reshape(-1, cfg.top_k)[tokens].reshape(-1)
+    return oracle_layer_rows(cfg, lt, xs, res, g_ids, bias_np, w_gpu_rows=g_w)
 
 
 def oracle_layer_rows(cfg, lt, xs, res, ids_gpu_rows, bias_np=None, tie=NEAR_TIE,
-                      tie_tokens=None):
+                      tie_tokens=None, w_gpu_rows=None):
     """Oracle forward of layer `lt` on activation rows xs (fp32 numpy) with
     residual rows res (or None); ids_gpu_rows = the GPU's routing of the same
     rows, compared with the oracle's (near-ties within `tie` counted, their
-    rows appended to tie_tokens)."""
+    rows appended to tie_tokens). When the GPU's weights w_gpu_rows are given,
+    the experts of a near-tie row are computed with the GPU's selection (ids
+    and weights), so that row's expert arithmetic is still compared."""
     router = to_np(lt.router)
     bias = bias_np if bias_np is not None else (None if lt.bias is None else to_np(lt.bias))
     logits = orc.linear(xs, router)
     ids_o, w_o = orc.router_topk(logits, bias, cfg.top_k, cfg.score_fn, cfg.norm, cfg.scale)
     sel = selection_values(cfg, logits, bias)
     k = cfg.top_k
-    _, flips = compare_routing(cfg, ids_gpu_rows, ids_o, sel, tie, tie_tokens)
+    rows_tied = []
+    _, flips = compare_routing(cfg, ids_gpu_rows, ids_o, sel, tie, rows_tied)
+    if tie_tokens is not None:
+        tie_tokens.extend(rows_tied)
+    if w_gpu_rows is not None and rows_tied:
+        ids_o = ids_o.reshape(-1, k).copy()
+        w_o = w_o.reshape(-1, k).copy()
+        gi = np.asarray(ids_gpu_rows).reshape(-1, k)
+        gw = np.asarray(w_gpu_rows).reshape(-1, k)
+        for t in rows_tied:
+            ids_o[t], w_o[t] = gi[t], gw[t]
+        ids_o, w_o = ids_o.reshape(-1), w_o.reshape(-1)
     experts = np.unique(ids_o)
     remap = {int(e): i for i, e in enumerate(experts)}
     g, u, d = compact_experts(lt, cfg, torch.as_tensor(experts.astype(np.int64), device=lt.gate.device))
