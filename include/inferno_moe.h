@@ -14,9 +14,12 @@
  *    stream-ordered; no function synchronises the stream except
  *    inferno_stream_synchronize.
  *  - Return value: INFERNO_OK (0), INFERNO_UNSUPPORTED (1, the reference's
- *    `Ok(None)`: the caller may fall back) or a negative error (the
- *    reference's `Err(Error::Backend{..})`), with a message retrievable via
- *    inferno_last_error() on the calling thread. Nothing throws across the ABI.
+ *    `Ok(None)`: the caller may fall back; returned by every entry point that
+ *    launches work when the process sees no HIP device, after argument
+ *    validation, as backend.rs:6688-6692 returns Ok(None) without a native
+ *    device) or a negative error (the reference's `Err(Error::Backend{..})`),
+ *    with a message retrievable via inferno_last_error() on the calling
+ *    thread. Nothing throws across the ABI.
  *  - Quantised expert tensors are the exact GGUF byte layouts: a 3-D tensor
  *    [E][rows][cols/256] of super-blocks (Q8_0: [E][rows][cols/32] blocks),
  *    expert stride = rows * (cols/values_per_block) * block_bytes. Byte lengths

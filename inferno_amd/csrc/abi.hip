@@ -152,6 +152,21 @@ int run_routed(hipStream_t s, int quant, int down_quant, const void* gate, const
   });
 }
 
+// The reference returns Ok(None) ("unsupported here, the caller may fall
+// back") when no native device backs the backend (backend.rs:6688-6692 and
+// the non-Metal branches); the counterpart here is INFERNO_UNSUPPORTED when
+// the process sees no HIP device. Argument errors are reported before this
+// check, as the reference validates before it looks for the device.
+int require_device() {
+  static const int count = [] {
+    int n = 0;
+    return hipGetDeviceCount(&n) == hipSuccess ? n : 0;
+  }();
+  if (count > 0) return INFERNO_OK;
+  set_error("no HIP device is available (unsupported here; the caller may fall back)");
+  return INFERNO_UNSUPPORTED;
+}
+
 int need_ws(void* ws, size_t have, size_t need) {
   if (need > 0 && (ws == nullptr || have < need)) {
     set_error("workspace too small: need " + std::to_string(need) + " bytes");
@@ -210,6 +225,7 @@ int inferno_gguf_dequantize(void* stream, int quant, const void* blocks, size_t 
   clear_error();
   INF_CHECK_ARG(block_bytes(quant) > 0, "unknown quant kind");
   INF_CHECK_ARG(n_blocks == 0 || (blocks && out), "null pointer");
+  if (int st_ = require_device()) return st_;
   return launch_dequant(as_stream(stream), quant, blocks, n_blocks, out);
 }
 
@@ -220,6 +236,7 @@ int inferno_router_logits(void* stream, const void* x, int x_dtype, const float*
   INF_CHECK_ARG(H > 0 && H % 4 == 0, "hidden size must be a positive multiple of 4");
   INF_CHECK_ARG(E > 0, "expert count must be positive");
   INF_CHECK_ARG(T == 0 || (x && w_router && logits), "null pointer");
+  if (int st_ = require_device()) return st_;
   return launch_router_logits(as_stream(stream), x, x_dtype, w_router, T, H, E, logits);
 }
 
@@ -246,6 +263,7 @@ int inferno_moe_router_topk(void* stream, const float* logits, const float* bias
                 "score_fn must be SIGMOID or SOFTMAX");
   INF_CHECK_ARG(std::isfinite(routed_scaling_factor), "MoE router routed scaling factor must be finite");
   INF_CHECK_ARG(logits && expert_ids && expert_weights, "null pointer");
+  if (int st_ = require_device()) return st_;
   return launch_router_topk(as_stream(stream), logits, bias, T, E, k, score_fn, norm_topk_prob,
                             routed_scaling_factor, expert_ids, expert_weights, token_indices);
 }
@@ -256,6 +274,7 @@ int inferno_moe_dispatch(void* stream, const uint32_t* expert_ids, size_t T, siz
   INF_CHECK_ARG(E > 0 && E <= size_t(kMaxExperts), "expert_count must be in 1..=256");
   INF_CHECK_ARG(T * k < (size_t(1) << 31), "too many assignments");
   INF_CHECK_ARG(offsets && active && (T * k == 0 || (expert_ids && sorted)), "null pointer");
+  if (int st_ = require_device()) return st_;
   return launch_dispatch(as_stream(stream), expert_ids, T, k, E, offsets, sorted, active);
 }
 
@@ -281,6 +300,7 @@ int inferno_gguf_moe(void* stream, int quant, int down_quant, const void* gate,
     set_error("workspace too small: need " + std::to_string(need) + " bytes");
     return INFERNO_ERR_SIZE;
   }
+  if (int st_ = require_device()) return st_;
   Carver c{static_cast<char*>(workspace)};
   MoeScratch m = carve_moe(c, T, k, E, H, I);
   hipStream_t s = as_stream(stream);
@@ -309,6 +329,7 @@ int inferno_moe_expert_gate_up_swiglu(void* stream, int quant, const void* gate,
   INF_CHECK_ARG(gate && up && x && offsets && sorted && active && expert_weights && h,
                 "null pointer");
   if ((st = need_ws(workspace, workspace_bytes, gemv_stage_bytes(quant, T, H, x_dtype)))) return st;
+  if (int st_ = require_device()) return st_;
   return launch_gemv_gate_up_routed(as_stream(stream), quant, gate, up, x, x_dtype,
                                     static_cast<uint32_t*>(workspace), false, offsets, sorted,
                                     active, expert_weights, T, k, E, H, I, h, nullptr);
@@ -326,6 +347,7 @@ int inferno_moe_expert_down(void* stream, int down_quant, const void* down, size
   if ((st = need_ws(workspace, workspace_bytes,
                     gemv_stage_bytes(down_quant, T * k, I, INFERNO_F32))))
     return st;
+  if (int st_ = require_device()) return st_;
   return launch_gemv_down_routed(as_stream(stream), down_quant, down, h,
                                  static_cast<uint32_t*>(workspace), false, offsets, sorted, active,
                                  T, k, E, H, I, y);
@@ -344,6 +366,7 @@ int inferno_q8_0_gate_up_swiglu(void* stream, const void* gate, size_t gate_byte
   INF_CHECK_ARG(gate && up && x && out, "null pointer");
   if ((st = need_ws(workspace, workspace_bytes, gemv_stage_bytes(INFERNO_Q8_0, T, H, x_dtype))))
     return st;
+  if (int st_ = require_device()) return st_;
   return launch_gemv_gate_up_dense(as_stream(stream), INFERNO_Q8_0, gate, up, x, x_dtype,
                                    static_cast<uint32_t*>(workspace), false, T, H, Is, out,
                                    nullptr);
@@ -361,6 +384,7 @@ int inferno_q8_0_matvec_add2(void* stream, const void* w, size_t w_bytes, const 
   INF_CHECK_ARG(w && input && out, "null pointer");
   if ((st = need_ws(workspace, workspace_bytes, gemv_stage_bytes(INFERNO_Q8_0, T, In, INFERNO_F32))))
     return st;
+  if (int st_ = require_device()) return st_;
   return launch_gemv_down_dense(as_stream(stream), INFERNO_Q8_0, w, input,
                                 static_cast<uint32_t*>(workspace), false, nullptr, 0, residual_a,
                                 residual_b, T, In, O, out);
@@ -372,6 +396,7 @@ int inferno_moe_topk_combine_residual(void* stream, const float* shared, const f
   clear_error();
   INF_CHECK_ARG(k > 0 && H > 0, "top_k and hidden size must be positive");
   INF_CHECK_ARG(T == 0 || (expert_outputs && expert_weights && out), "null pointer");
+  if (int st_ = require_device()) return st_;
   return launch_topk_combine(as_stream(stream), shared, residual, expert_outputs, expert_weights,
                              T, H, k, out);
 }
@@ -384,6 +409,7 @@ int inferno_moe_weighted_index_add_combine(void* stream, const float* acc,
   clear_error();
   INF_CHECK_ARG(T == 0 || (acc && out), "null pointer");
   INF_CHECK_ARG(A == 0 || (token_indices && expert_outputs && expert_weights), "null pointer");
+  if (int st_ = require_device()) return st_;
   return launch_index_add_combine(as_stream(stream), acc, token_indices, expert_outputs,
                                   expert_weights, T, H, A, out);
 }
@@ -392,6 +418,7 @@ int inferno_moe_gather_tokens(void* stream, const float* x, const uint32_t* toke
                               size_t T, size_t H, size_t A, float* out) {
   clear_error();
   INF_CHECK_ARG(A == 0 || (x && token_indices && out), "null pointer");
+  if (int st_ = require_device()) return st_;
   return launch_gather(as_stream(stream), x, token_indices, T, H, A, out);
 }
 
@@ -400,6 +427,7 @@ int inferno_rms_norm(void* stream, const float* x, const float* w, size_t rows, 
   clear_error();
   INF_CHECK_ARG(H > 0 && eps >= 0.f, "rms_norm needs a positive width and eps >= 0");
   INF_CHECK_ARG(rows == 0 || (x && w && out), "null pointer");
+  if (int st_ = require_device()) return st_;
   return launch_rms_norm(as_stream(stream), x, w, rows, H, eps, out, INFERNO_F32);
 }
 
@@ -477,6 +505,7 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
     set_error("workspace too small: need " + std::to_string(need) + " bytes");
     return INFERNO_ERR_SIZE;
   }
+  if (int st_ = require_device()) return st_;
   Carver c{static_cast<char*>(workspace)};
   LayerScratch w = carve_layer(c, L, T);
   hipStream_t s = as_stream(stream);
@@ -585,6 +614,7 @@ int inferno_moe_layer_forward_noalloc(void* stream, const inferno_moe_layer* L, 
               "caller workspace)");
     return INFERNO_ERR_SIZE;
   }
+  if (int st_ = require_device()) return st_;
   void* ws = nullptr;
   int st = scratch_ptr(&ws);
   if (st) return st;
@@ -645,6 +675,7 @@ int inferno_moe_stack_forward(void* stream, const inferno_moe_layer* layers, siz
     set_error("workspace too small: need " + std::to_string(need) + " bytes");
     return INFERNO_ERR_SIZE;
   }
+  if (int st_ = require_device()) return st_;
   Carver c{static_cast<char*>(workspace)};
   StackScratch w = carve_stack(c, layers, n_layers, T);
   hipStream_t s = as_stream(stream);
@@ -674,6 +705,7 @@ int inferno_synth_normal(void* stream, uint64_t seed, float stddev, size_t n, in
   clear_error();
   INF_CHECK_ARG(dtype == INFERNO_F32 || dtype == INFERNO_BF16, "dtype must be F32 or BF16");
   INF_CHECK_ARG(n == 0 || out, "null pointer");
+  if (int st_ = require_device()) return st_;
   return launch_synth_normal(as_stream(stream), seed, stddev, n, dtype, out);
 }
 
@@ -701,6 +733,7 @@ int inferno_synth_quantized(void* stream, int quant, uint64_t seed, float stddev
   clear_error();
   INF_CHECK_ARG(block_bytes(quant) > 0, "unknown quant kind");
   INF_CHECK_ARG(cols % size_t(block_values(quant)) == 0, "cols must be a multiple of the block size");
+  if (int st_ = require_device()) return st_;
   return launch_synth_quantized(as_stream(stream), quant, seed, stddev, rows, cols, out);
 }
 

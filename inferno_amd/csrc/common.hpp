@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <cstdlib>
 #include <string>
 
 #include "inferno_moe.h"
@@ -12,6 +13,14 @@
 #define HD __host__ __device__ __forceinline__
 
 namespace inferno {
+
+// True when the environment variable `name` starts with '0' (a kernel-variant
+// switch turned off). Read on every call, so a process can change it between
+// calls; it costs one environment scan per launch decision.
+inline bool switch_off(const char* name) {
+  const char* v = std::getenv(name);
+  return v && v[0] == '0';
+}
 
 constexpr int kWave = 64;        // CDNA wavefront width
 constexpr int kKBlock = 256;     // K-quant super-block values

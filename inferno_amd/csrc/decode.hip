@@ -6,9 +6,8 @@
 //   select   logits = ordered sum of the partials, exact top-k per token
 //            (one wavefront each), stable dispatch (one wavefront for T = 1);
 //   gate/up  routed and Q8_0 shared-expert 16-row tiles in one grid, writing
-//            the SwiGLU intermediate already staged for the down pass (an
-//            opt-in alternative for one token streams the tiles through an
-//            LDS ring, decode_ring.hpp);
+//            the SwiGLU intermediate already staged for the down pass (one
+//            Q2_K bf16 token: the matrix-core kernels of decode_mfma.hpp);
 //   down     8-row output tiles over all ranks plus the shared expert, with
 //            out = (residual + shared) + routed summed in a fixed order,
 //            deterministic without float atomics.
@@ -19,7 +18,6 @@
 // (shared expert plus two residual adds), moe_kernels.metal:210-238 (rank
 // order combine).
 #include "decode.hpp"
-#include "decode_ring.hpp"
 #include "decode_mfma.hpp"
 
 #include <cstdlib>
@@ -589,19 +587,6 @@ void launch_down(hipStream_t s, const DecodeArgs& a) {
     down8_kernel<Q, kMax8><<<grid, 256, lds, s>>>(a);
 }
 
-// One-token gate/up through the LDS ring (decode_ring.hpp): opt-in with
-// INFERNO_DECODE_RING=1. It measures level with the tile grid on the GLM
-// decode layer (both about 33 us for the routed + shared gate/up), so the
-// grid stays the default; the plan returns false outside what the ring
-// kernel covers (then the tile grid runs).
-bool ring_enabled() {
-  static const bool on = [] {
-    const char* v = std::getenv("INFERNO_DECODE_RING");
-    return v && v[0] == '1';
-  }();
-  return on;
-}
-
 int device_cus() {
   static int cus[64] = {0};
   int dev = 0;
@@ -611,72 +596,10 @@ int device_cus() {
   return cus[dev];
 }
 
-bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
-
-bool ring_plan(const DecodeArgs& a, int quant, ring::RingPlan& pl, unsigned& grid, size_t& lds,
-               int& pw) {
-  if (!ring_enabled() || a.T != 1 || a.x_dtype == INFERNO_F32 || quant != INFERNO_Q2_K) return false;
-  const int nsb = a.H / kKBlock;
-  if (a.I % kRows || a.Is % kRows) return false;
-  if (!ring::ring_shape_q2k(nsb, pl.routed)) return false;
-  if (a.Is) {
-    if (!ring::ring_shape_q8(nsb, pl.shared)) return false;
-  } else {
-    pl.shared = pl.routed;
-  }
-  if (!aligned16(a.gate) || !aligned16(a.up) || !aligned16(a.stage_x) ||
-      (a.Is && (!aligned16(a.sgate) || !aligned16(a.sup))))
-    return false;
-  pl.tiles_i = a.I / kRows;
-  pl.S = a.Is / kRows;
-  pl.R = a.k * pl.tiles_i;
-  pl.x_bytes = uint32_t(staged_stride(a.H, false)) * 4;
-  pl.x_pieces = int((pl.x_bytes + 1023) / 1024);
-  const int pieces = std::max(pl.routed.pieces, a.Is ? pl.shared.pieces : 0);
-  pw = (pieces + ring::kDmaWaves - 1) / ring::kDmaWaves;
-  if (pw < 4 || pw > 6) return false;
-  const int cus = device_cus();
-  if (cus <= 0) return false;
-  grid = unsigned(2 * cus);
-  if (int(grid) <= pl.S) return false;
-  lds = size_t(pl.x_pieces) * 1024 + ring::kPartFloats * 4 + size_t(ring::kDepth) * ring::kSlotBytes;
-  return lds <= 160 * 1024;
-}
-
-template <int PW>
-int launch_gate_up_ring_pw(hipStream_t s, const DecodeArgs& a, const ring::RingPlan& pl,
-                           unsigned grid, size_t lds) {
-  static bool attr = false;
-  if (!attr) {
-    if (hipFuncSetAttribute((const void*)ring::gate_up_ring_kernel<PW>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
-      set_error("gate/up ring kernel: cannot raise its LDS limit");
-      return INFERNO_ERR_DEVICE;
-    }
-    attr = true;
-  }
-  ring::gate_up_ring_kernel<PW><<<grid, 256, lds, s>>>(a, pl);
-  INF_LAUNCHED();
-  return INFERNO_OK;
-}
-
-int launch_gate_up_ring(hipStream_t s, const DecodeArgs& a, const ring::RingPlan& pl,
-                        unsigned grid, size_t lds, int pw) {
-  switch (pw) {
-    case 4: return launch_gate_up_ring_pw<4>(s, a, pl, grid, lds);
-    case 5: return launch_gate_up_ring_pw<5>(s, a, pl, grid, lds);
-    default: return launch_gate_up_ring_pw<6>(s, a, pl, grid, lds);
-  }
-}
-
 // Routed Q2_K gate/up for one bf16 token on the matrix cores
 // (decode_mfma.hpp); on by default, INFERNO_DECODE_MFMA=0 turns it off.
 bool mfma_enabled() {
-  static const bool on = [] {
-    const char* v = std::getenv("INFERNO_DECODE_MFMA");
-    return !(v && v[0] == '0');
-  }();
-  return on;
+  return !switch_off("INFERNO_DECODE_MFMA");
 }
 
 // K parts of the shared gate/up on the MFMA path: the largest of 4, 3, 2
@@ -861,18 +784,11 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   // the route launch), then the routed down with the shared down and the
   // residual folded in: one stream, no events
   a.routed_tiles = a.max_slots * (a.I / kRows);
-  ring::RingPlan pl;
-  unsigned ring_grid = 0;
-  size_t ring_lds = 0;
-  int ring_pw = 0;
-  const bool use_ring = ring_plan(a, quant, pl, ring_grid, ring_lds, ring_pw);
   const char* gu_label =
       use_mfma ? "mfma: gate_up_q2k_kernel (routed Q2_K tiles on MFMA; shared gate/up in the route launch)"
-      : use_ring ? "ring: gate_up_ring_kernel (routed + Q8_0 shared tiles)"
-                 : "tiles: gate_up_kernel (routed + Q8_0 shared tiles)";
+               : "tiles: gate_up_kernel (routed + Q8_0 shared tiles)";
   int st = timed(s, kTimerGateUp, gu_label, [&]() -> int {
     if (use_mfma) return launch_gate_up_mfma(s, a);
-    if (use_ring) return launch_gate_up_ring(s, a, pl, ring_grid, ring_lds, ring_pw);
     switch (quant) {
       case INFERNO_Q2_K: xsplit ? launch_gate_up<INFERNO_Q2_K, true>(s, a) : launch_gate_up<INFERNO_Q2_K, false>(s, a); break;
       case INFERNO_Q3_K: xsplit ? launch_gate_up<INFERNO_Q3_K, true>(s, a) : launch_gate_up<INFERNO_Q3_K, false>(s, a); break;

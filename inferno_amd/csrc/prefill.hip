@@ -847,11 +847,7 @@ __global__ void __launch_bounds__(256)
 
 // INFERNO_PREFILL_GEMM2=0 keeps the four-wavefront kernel for every format.
 bool gemm2_enabled() {
-  static const bool on = [] {
-    const char* v = std::getenv("INFERNO_PREFILL_GEMM2");
-    return !(v && v[0] == '0');
-  }();
-  return on;
+  return !switch_off("INFERNO_PREFILL_GEMM2");
 }
 
 template <int Q, int NMAT, int TM>

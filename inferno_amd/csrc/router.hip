@@ -316,11 +316,7 @@ __global__ void __launch_bounds__(256)
 
 // INFERNO_ROUTER_BF16X3=0 keeps the fp32 matrix-core logits for bf16 tokens.
 static bool bf16x3_enabled() {
-  static const bool on = [] {
-    const char* v = getenv("INFERNO_ROUTER_BF16X3");
-    return !(v && v[0] == '0');
-  }();
-  return on;
+  return !switch_off("INFERNO_ROUTER_BF16X3");
 }
 
 int launch_router_logits(hipStream_t s, const void* x, int x_dtype, const float* w, size_t T,

@@ -55,6 +55,21 @@ def test_error_paths_without_gpu():
     assert st < 0
 
 
+def test_valid_call_without_a_device_is_unsupported():
+    # the reference's Ok(None) when no native device backs the backend
+    # (crates/backend/src/backend.rs:6688-6692): INFERNO_UNSUPPORTED (1), after
+    # argument validation; nothing is launched
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present: the call would run")
+    import ctypes as C
+    L = lib()
+    x = C.c_void_p(16)  # never dereferenced: no device to launch on
+    st = L.inferno_rms_norm(None, x, x, 1, 64, 1e-6, x)
+    assert st == 1 and b"no HIP device" in L.inferno_last_error()
+    st = L.inferno_rms_norm(None, x, x, 1, 0, 1e-6, x)  # invalid arguments still come first
+    assert st == -1
+
+
 def test_synth_normal_host_statistics_and_determinism():
     a = ops.synth_normal_host(5, 1.0, 200000).numpy()
     b = ops.synth_normal_host(5, 1.0, 200000).numpy()

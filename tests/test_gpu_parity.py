@@ -526,41 +526,43 @@ def test_stack_c4_each_layer_on_gpu_stream(cuda, T):
             r = nxt
 
 
-def test_layer_prefill_fragment_kernel_variant(cuda):
+@pytest.fixture
+def switches(monkeypatch):
+    """Sets kernel-variant switches for one test (the library reads them on
+    every call); monkeypatch restores the environment afterwards."""
+    def set_(**kv):
+        for k, v in kv.items():
+            monkeypatch.setenv(k, v)
+    return set_
+
+
+def test_layer_prefill_fragment_kernel_variant(cuda, switches):
     """The prefill GEMMs all on the fragment-load kernel and the fp32 router
-    logits (INFERNO_PREFILL_GEMM2=0, INFERNO_ROUTER_BF16X3=0) in a child
-    process (the switches are read once per process)."""
-    import os
-    import subprocess
-    import sys
-    from pathlib import Path
-    env = dict(os.environ, INFERNO_PREFILL_GEMM2="0", INFERNO_ROUTER_BF16X3="0")
-    script = Path(__file__).resolve().parent / "prefill_variant_check.py"
-    r = subprocess.run([sys.executable, "-u", str(script)], env=env, capture_output=True,
-                       text=True, timeout=240)
-    print(r.stdout[-2000:], r.stderr[-2000:])
-    assert r.returncode == 0 and "gemm1 ok" in r.stdout
+    logits (INFERNO_PREFILL_GEMM2=0, INFERNO_ROUTER_BF16X3=0): c3, every
+    token, against the oracle."""
+    switches(INFERNO_PREFILL_GEMM2="0", INFERNO_ROUTER_BF16X3="0")
+    _layer_parity(cuda, "c3", 512)
 
 
-@pytest.mark.parametrize("variant", ["tiles", "ring"])
-def test_layer_decode_variants(cuda, variant):
-    """The non-default one-token decode paths in a child process each (the
-    switches are read once per process): the packed-f16 tile kernels
-    (INFERNO_DECODE_MFMA=0) and the opt-in LDS-ring gate/up
-    (INFERNO_DECODE_RING=1 on top of that)."""
-    import os
-    import subprocess
-    import sys
-    from pathlib import Path
-    env = dict(os.environ, INFERNO_DECODE_MFMA="0")
-    env.pop("INFERNO_DECODE_RING", None)
-    if variant == "ring":
-        env["INFERNO_DECODE_RING"] = "1"
-    script = Path(__file__).resolve().parent / "decode_variant_check.py"
-    r = subprocess.run([sys.executable, "-u", str(script), variant], env=env,
-                       capture_output=True, text=True, timeout=240)
-    print(r.stdout[-2000:], r.stderr[-2000:])
-    assert r.returncode == 0 and f"{variant} ok" in r.stdout
+@pytest.mark.parametrize("key", ["c2", "c4"])
+def test_layer_decode_tile_kernel_variant(cuda, switches, key):
+    """One-token Q2_K decode on the packed-f16 tile kernels
+    (INFERNO_DECODE_MFMA=0) instead of the matrix-core kernels: c2 and c4
+    layer 0, eight seeded tokens, against the oracle; the launch label
+    confirms which gate/up kernel ran."""
+    switches(INFERNO_DECODE_MFMA="0")
+    _layer_parity(cuda, key, 1, variants=8)
+    cfg = cf.CONFIGS[key]
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=1)
+    ops.kernel_timing(True)
+    try:
+        lt.layer.forward(cf.make_input(cfg, 1, device=cuda), None)
+        torch.cuda.synchronize()
+        label = ops.kernel_timing_label(ops.TIMER_GATE_UP)
+        ops.kernel_timing_read(ops.TIMER_GATE_UP)
+    finally:
+        ops.kernel_timing(False)
+    assert label.startswith("tiles:"), label
 
 
 def test_kernel_timing_hook_counts_decode_launches(cuda):
