@@ -34,7 +34,21 @@ KernelTimers& timers() {
 
 void kernel_timing_enable(bool on) {
   std::lock_guard<std::mutex> lock(timers().mu);
-  timers().on = on;
+  KernelTimers& k = timers();
+  k.on = on;
+  if (!on) {
+    // timing off: unread launches are dropped (after they complete, so the
+    // pairs can be recorded again) and the sums cleared
+    for (const Pending& pd : k.pending) {
+      (void)hipEventSynchronize(pd.e1);
+      k.free_pairs[pd.dev].push_back({pd.e0, pd.e1});
+    }
+    k.pending.clear();
+    for (int i = 0; i < kNumTimers; ++i) {
+      k.ms[i] = 0;
+      k.n[i] = 0;
+    }
+  }
 }
 
 bool kernel_timing_on() {
@@ -83,7 +97,12 @@ int kernel_timing_begin(hipEvent_t* start, hipEvent_t* stop, int* dev_out) {
     // event that the timing does not need: the events only timestamp
     // kernels of one stream)
     INF_HIP(hipEventCreateWithFlags(&a, hipEventDisableSystemFence));
-    INF_HIP(hipEventCreateWithFlags(&b, hipEventDisableSystemFence));
+    const hipError_t e = hipEventCreateWithFlags(&b, hipEventDisableSystemFence);
+    if (e != hipSuccess) {
+      (void)hipEventDestroy(a);
+      set_error(std::string("hipEventCreateWithFlags: ") + hipGetErrorString(e));
+      return INFERNO_ERR_DEVICE;
+    }
     fp.push_back({a, b});
   }
   *start = fp.back().first;
@@ -97,6 +116,11 @@ void kernel_timing_end(int which, int dev, hipEvent_t start, hipEvent_t stop, co
   std::lock_guard<std::mutex> lock(timers().mu);
   timers().pending.push_back({which, dev, start, stop});
   timers().label[which] = label;
+}
+
+void kernel_timing_abort(int dev, hipEvent_t start, hipEvent_t stop) {
+  std::lock_guard<std::mutex> lock(timers().mu);
+  timers().free_pairs[dev].push_back({start, stop});
 }
 
 const char* kernel_timing_label(int which) {

@@ -13,6 +13,8 @@ bool kernel_timing_read(int which, double* ms, uint64_t* n);
 bool kernel_timing_on();
 // An event pair of the current device for one timed launch (pooled).
 int kernel_timing_begin(hipEvent_t* start, hipEvent_t* stop, int* dev);
+// Returns a pair taken by kernel_timing_begin whose launch failed to the pool.
+void kernel_timing_abort(int dev, hipEvent_t start, hipEvent_t stop);
 // Files the recorded pair under timer `which`; read sums it later.
 void kernel_timing_end(int which, int dev, hipEvent_t start, hipEvent_t stop, const char* label);
 // Label of the last launch a timer measured (a static string), or "".
@@ -28,9 +30,19 @@ int timed(hipStream_t s, int which, const char* label, Fn launch) {
   hipEvent_t e0, e1;
   int dev = 0, st;
   if ((st = kernel_timing_begin(&e0, &e1, &dev))) return st;
-  INF_HIP(hipEventRecord(e0, s));
-  if ((st = launch())) return st;
-  INF_HIP(hipEventRecord(e1, s));
+  hipError_t e = hipEventRecord(e0, s);
+  if (e == hipSuccess) {
+    if ((st = launch())) {
+      kernel_timing_abort(dev, e0, e1);
+      return st;
+    }
+    e = hipEventRecord(e1, s);
+  }
+  if (e != hipSuccess) {
+    kernel_timing_abort(dev, e0, e1);
+    set_error(std::string("hipEventRecord: ") + hipGetErrorString(e));
+    return INFERNO_ERR_DEVICE;
+  }
   kernel_timing_end(which, dev, e0, e1, label);
   return INFERNO_OK;
 }

@@ -73,8 +73,10 @@ class TensorInfo:
         if self.ty not in BLOCKS:
             raise GGUFError(f"GGUF tensor {self.name} has unsupported type {self.ty}")
         per, size = BLOCKS[self.ty]
-        if self.dims[0] % per:
-            raise GGUFError(f"GGUF tensor {self.name} row width {self.dims[0]} is not a "
+        # the reference checks the element count (lib.rs:1890-1900); the
+        # expert kernels check row widths themselves
+        if self.elements % per:
+            raise GGUFError(f"GGUF tensor {self.name} element count {self.elements} is not a "
                             f"multiple of the {per}-value block")
         return self.elements // per * size
 
@@ -119,8 +121,10 @@ class _Reader:
                 raise GGUFError(f"invalid GGUF bool value {v}; expected 0 or 1")
             return bool(v)
         if t == MT_STRING:
-            s = self.string()
-            return s if store else ""
+            if not store:  # skipped unchecked, as skip_string (lib.rs:1741-1746)
+                self.take(self.scalar("<Q"))
+                return ""
+            return self.string()
         et = self.value_type()
         n = self.scalar("<Q")
         keep = store and n <= MAX_STORED_ARRAY_VALUES
@@ -167,15 +171,22 @@ class GGUFFile:
         self.tensor_count = r.scalar("<Q")
         self.metadata_kv_count = r.scalar("<Q")
         self.metadata = {}
+        self.metadata_types = {}
         for _ in range(self.metadata_kv_count):
             key = r.string(MAX_KEY_BYTES)
             _check_key(key)
-            val = r.value(r.value_type())
+            t = r.value_type()
+            val = r.value(t)
             if key in self.metadata:
                 raise GGUFError(f"duplicate GGUF metadata key {key}")
             self.metadata[key] = val
-        al = self.metadata.get("general.alignment", DEFAULT_ALIGNMENT)
-        if isinstance(al, bool) or not isinstance(al, int) or al < 8 or al % 8:
+            self.metadata_types[key] = t
+        # metadata_alignment (lib.rs:1821-1840): only an unsigned integer value
+        # counts; any other type falls back to the default
+        al = DEFAULT_ALIGNMENT
+        if self.metadata_types.get("general.alignment") in (MT_U8, MT_U16, MT_U32, MT_U64):
+            al = self.metadata["general.alignment"]
+        if al < 8 or al % 8:
             raise GGUFError(f"GGUF general.alignment must be a multiple of 8 and at least 8, "
                             f"got {al}")
         self.alignment = al

@@ -158,3 +158,28 @@ def test_overlapping_tensors_and_short_storage(tmp_path):
         with pytest.raises(G.GGUFError, match="needs 68 bytes"):
             g.tensor_bytes("q")
         assert g.tensor_bytes("n").size == 32
+
+
+@pytest.mark.parametrize("t,v", [(G.MT_I32, 64), (G.MT_F32, 64.0), (G.MT_STRING, "64")])
+def test_alignment_key_of_another_type_falls_back_to_32(tmp_path, t, v):
+    # metadata_alignment (lib.rs:1821-1840) reads only unsigned integers;
+    # any other value type means the default alignment
+    path = tmp_path / "a.gguf"
+    G.write_gguf(path, [("general.alignment", t, v)],
+                 [("x.weight", (8,), G.GGML_F32, np.zeros(8, np.float32).tobytes())])
+    with G.GGUFFile(path) as g:
+        assert g.alignment == 32
+
+
+def test_unstored_array_strings_are_skipped_unchecked(tmp_path):
+    # strings inside arrays of more than 1024 values are skipped without
+    # UTF-8 validation (skip_string, lib.rs:1741-1746)
+    path = tmp_path / "s.gguf"
+    G.write_gguf(path, [("tok", G.MT_ARRAY, (G.MT_STRING, ["ok"] * 1100))],
+                 [("x.weight", (8,), G.GGML_F32, np.zeros(8, np.float32).tobytes())])
+    raw = bytearray(path.read_bytes())
+    i = raw.index(struct.pack("<Q", 2) + b"ok") + 8
+    raw[i] = 0xFF  # an invalid UTF-8 byte in an unstored string
+    path.write_bytes(bytes(raw))
+    with G.GGUFFile(path) as g:
+        assert g.metadata["tok"].length == 1100 and g.metadata["tok"].values is None
