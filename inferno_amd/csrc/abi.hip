@@ -446,6 +446,7 @@ struct LayerScratch {
   float* ys;
   uint4* slots;
   uint32_t* stage_xm;
+  uint32_t* stage_xr;
   float* shared_gu;
 };
 LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
@@ -460,6 +461,7 @@ LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   s.ys = c.take<float>(T * L->hidden);
   s.slots = c.take<uint4>(L->experts);
   s.stage_xm = c.take<uint32_t>(T * decode_mfma_stage_words(L->hidden));
+  s.stage_xr = c.take<uint32_t>(T * decode_runs_stage_words(L->hidden));
   s.shared_gu = c.take<float>(L->shared_intermediate
                                   ? decode_shared_partial_floats(L->hidden, L->shared_intermediate)
                                   : 1);
@@ -528,6 +530,7 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
     d.partials = w.partials; d.stage_x = w.moe.stage_x; d.offsets = w.moe.offsets;
     d.sorted = w.moe.sorted; d.active = w.moe.active; d.stage_h = w.moe.stage_h;
     d.stage_hs = w.stage_hs; d.slots = w.slots; d.stage_xm = w.stage_xm;
+    d.stage_xr = w.stage_xr;
     d.shared_gu = w.shared_gu;
     d.ys = w.ys;
     return launch_decode_layer(s, d, L->quant);

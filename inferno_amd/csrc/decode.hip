@@ -19,6 +19,7 @@
 // order combine).
 #include "decode.hpp"
 #include "decode_mfma.hpp"
+#include "decode_runs.hpp"
 
 #include <cstdlib>
 #include "timing.hpp"
@@ -96,6 +97,22 @@ __global__ void __launch_bounds__(256) route_kernel(DecodeArgs p, int gx, int gy
       for (int i = 0; i < 16; ++i) v[i] = to_f32(src[i]);
       constexpr bool kSplit = !std::is_same<XT, uint16_t>::value;
       stage_run<kSplit>(v, p.stage_x + size_t(t) * staged_stride(H, kSplit), H, run);
+    }
+  }
+  // staging for the runs gate/up (bf16 tokens): a 16-lane group per 16-value
+  // run, scaled for the field offsets of format xr_quant (decode_runs.hpp)
+  if constexpr (std::is_same<XT, uint16_t>::value) {
+    if (p.stage_xr) {
+      const int runs = H / 16, run_id = (g * 256 + tid) >> 4;
+      if (run_id < T * runs) {  // uniform per 16-lane group
+        const int t = run_id / runs, run = run_id % runs;
+        const float v = to_f32(static_cast<const XT*>(p.x)[size_t(t) * H + run * 16 + (tid & 15)]);
+        const int r16 = run & 15;
+        const int shift = p.xr_quant == INFERNO_Q4_K ? runs_decode::RF<INFERNO_Q4_K>::run_shift(r16)
+                                                     : runs_decode::RF<INFERNO_Q2_K>::run_shift(r16);
+        runs_decode::stage_run16(v, p.stage_xr + size_t(t) * runs_decode::run_words(H), H, run,
+                                 shift);
+      }
     }
   }
   // staging for the MFMA gate/up: one wavefront per 256-value column
@@ -723,20 +740,38 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   a.n_chunks = a.H / a.chunk;
   a.max_slots = std::min(a.E, a.T * a.k);
   const bool xsplit = a.x_dtype == INFERNO_F32;
-  const bool use_mfma = mfma_gate_up_covers(a, quant);
-  // with the MFMA gate/up the shared expert's gate/up runs in the route
+  // gate/up: fp8 x fp4 matrix-core kernel (one Q2_K bf16 token), else the
+  // f16-run matrix-core kernel (one token, any routed format, with its down
+  // kernel), else the packed-f16 tile kernels
+  const bool shared_down_ok = a.H % kSharedDownRows == 0 && a.Is % kKBlock == 0 &&
+                              (a.Is == 0 || a.ys != nullptr);
+  const bool use_fp4 = mfma_gate_up_covers(a, quant);
+  // (fp32 tokens stay on the tile kernels: the run gate/up carries them as two
+  // f16 terms, twice the matrix-core work, and measured slower there)
+  const bool use_runs = !use_fp4 && mfma_enabled() && a.T == 1 && a.x_dtype == INFERNO_BF16 &&
+                        shared_down_ok &&
+                        (a.Is == 0 || a.shared_gu != nullptr) && a.stage_xr != nullptr &&
+                        a.I % kRows == 0 && runs_gate_up_covers(quant, a.H, a.x_dtype) &&
+                        runs_down_covers(quant, a.H, a.I, a.k);
+  const bool use_mfma = use_fp4 || use_runs;
+  // with a matrix-core gate/up the shared expert's gate/up runs in the route
   // launch and stages its own x; otherwise x is staged for the tile kernels
   a.shared_parts = shared_parts(a.H);
   if (use_mfma) a.stage_x = nullptr;
-  else a.stage_xm = nullptr;
-  // the MFMA down kernel follows the MFMA gate/up (it reads h in that
-  // kernel's layout); the shared down then runs in the select launch
-  const bool use_mfma_down = use_mfma && mfma_decode::down_covers(a.I, a.k) &&
-                             a.H % kSharedDownRows == 0 && a.Is % kKBlock == 0 &&
-                             mfma_decode::down_lds_bytes(a.I) <= 160 * 1024 &&
-                             (a.Is == 0 || a.ys != nullptr);
+  if (!use_fp4) a.stage_xm = nullptr;
+  if (!use_runs) a.stage_xr = nullptr;
+  a.xr_quant = quant;
+  // down after a matrix-core gate/up (h in the run layout): the Q2_K kernel
+  // (I = 2048, k <= 8) or the run kernel; the shared down then runs in the
+  // select launch
+  const bool use_q2k_down = use_fp4 && mfma_decode::down_covers(a.I, a.k) && shared_down_ok &&
+                            mfma_decode::down_lds_bytes(a.I) <= 160 * 1024;
+  const bool use_runs_down = !use_q2k_down && use_mfma && shared_down_ok &&
+                             runs_down_covers(quant, a.H, a.I, a.k);
+  const bool use_mfma_down = use_q2k_down || use_runs_down;
   a.h_mfma = use_mfma_down ? 1 : 0;
-  if (!use_mfma_down) a.ys = nullptr;
+  // the shared down output ys exists only with a shared expert on that path
+  if (!use_mfma_down || a.Is == 0) a.ys = nullptr;
   if (!decode_supported(a.T, a.k, a.E, a.H, a.I, a.Is, a.x_dtype, quant, quant)) {
     set_error("fused decode path does not cover this layer shape");
     return INFERNO_ERR_INVALID;
@@ -745,7 +780,8 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   {
     const int runs = a.T * a.H / 16;
     const int gx = (a.E + 3) / 4;
-    const int need = std::max((runs + 255) / 256, (a.T * (a.H / kKBlock) + 3) / 4);
+    const int need = std::max(std::max((runs + 255) / 256, (a.T * (a.H / kKBlock) + 3) / 4),
+                              a.stage_xr ? (a.T * a.H + 255) / 256 : 0);
     const int gy = std::max(a.n_chunks, (need + gx - 1) / gx);
     const int shared_wgs = use_mfma ? a.Is / kRows * a.shared_parts : 0;
     const unsigned grid = unsigned(gx * gy + shared_wgs);
@@ -785,10 +821,12 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   // residual folded in: one stream, no events
   a.routed_tiles = a.max_slots * (a.I / kRows);
   const char* gu_label =
-      use_mfma ? "mfma: gate_up_q2k_kernel (routed Q2_K tiles on MFMA; shared gate/up in the route launch)"
-               : "tiles: gate_up_kernel (routed + Q8_0 shared tiles)";
+      use_fp4 ? "mfma: gate_up_q2k_kernel (routed Q2_K tiles on MFMA; shared gate/up in the route launch)"
+      : use_runs ? "runs: gate_up_runs_kernel (routed tiles on f16 MFMA; shared gate/up in the route launch)"
+                 : "tiles: gate_up_kernel (routed + Q8_0 shared tiles)";
   int st = timed(s, kTimerGateUp, gu_label, [&]() -> int {
-    if (use_mfma) return launch_gate_up_mfma(s, a);
+    if (use_fp4) return launch_gate_up_mfma(s, a);
+    if (use_runs) return launch_gate_up_runs(s, a, quant);
     switch (quant) {
       case INFERNO_Q2_K: xsplit ? launch_gate_up<INFERNO_Q2_K, true>(s, a) : launch_gate_up<INFERNO_Q2_K, false>(s, a); break;
       case INFERNO_Q3_K: xsplit ? launch_gate_up<INFERNO_Q3_K, true>(s, a) : launch_gate_up<INFERNO_Q3_K, false>(s, a); break;
@@ -798,11 +836,16 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
     return INFERNO_OK;
   });
   if (st) return st;
-  if (use_mfma_down)
+  if (use_q2k_down)
     return timed(s, kTimerDown,
                  "mfma-down: down_q2k_kernel (routed Q2_K down on MFMA + combine; shared down "
                  "in the select launch)",
                  [&] { return launch_down_mfma(s, a); });
+  if (use_runs_down)
+    return timed(s, kTimerDown,
+                 "runs-down: down_runs_kernel (routed down on f16 MFMA + combine; shared down "
+                 "in the select launch)",
+                 [&] { return launch_down_runs(s, a, quant); });
   return timed(s, kTimerDown, "down8: down8_kernel (routed + Q8_0 shared down + combine)", [&] {
     switch (quant) {
       case INFERNO_Q2_K: launch_down<INFERNO_Q2_K>(s, a); break;

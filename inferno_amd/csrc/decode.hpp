@@ -36,6 +36,8 @@ struct DecodeArgs {
   uint32_t* stage_h;      // [T*k, staged_stride(I, true)]
   uint32_t* stage_hs;     // [T, staged_stride(Is, true)]
   uint32_t* stage_xm;     // [T, decode_mfma_stage_words(H)]: x staged for the MFMA gate/up
+  uint32_t* stage_xr;     // [T, decode_runs_stage_words(H)]: x as f16 runs (runs gate/up)
+  int xr_quant;           // format whose field offsets the x runs are staged for
   float* shared_gu;       // [shared_parts][2][Is]: shared gate/up partial sums (MFMA path, T = 1)
   int shared_parts;       // K parts of the shared gate/up in the route launch
   float* ys;              // [T, H]: shared down output (MFMA down path)
@@ -50,9 +52,18 @@ bool decode_supported(size_t T, size_t k, size_t E, size_t H, size_t I, size_t I
 int decode_chunk(size_t H);
 // Words per token of the activation staging used by the MFMA gate/up kernel.
 size_t decode_mfma_stage_words(size_t H);
+// Words per token of the f16-run staging of x (fp32 tokens: split layout).
+size_t decode_runs_stage_words(size_t H);
 // Floats of the shared gate/up partial-sum buffer (T = 1 MFMA path).
 size_t decode_shared_partial_floats(size_t H, size_t Is);
 int launch_decode_layer(hipStream_t s, const DecodeArgs& a, int quant);
+
+// f16-run matrix-core decode kernels (decode_runs.hip): whether they cover a
+// shape, and their launchers (one token; gate/up writes h as run rows).
+bool runs_gate_up_covers(int quant, int H, int x_dtype);
+bool runs_down_covers(int quant, int H, int I, int k);
+int launch_gate_up_runs(hipStream_t s, const DecodeArgs& a, int quant);
+int launch_down_runs(hipStream_t s, const DecodeArgs& a, int quant);
 
 
 }  // namespace inferno

@@ -1,0 +1,488 @@
+// Decode GEMVs of the routed Q2_K / Q3_K / Q4_K experts for one token on the
+// matrix cores (v_mfma_f32_16x16x32_f16), activations staged as f16 runs.
+//
+// Both expert GEMVs (gate/up against x, down against h) share one block dot:
+// a 16-row tile of one super-block column (256 values) is one set of MFMA
+// tiles C[m][n] = sum_k A[m][k] B[k][n] with
+//   B (weights, row n = lane & 15): a quant field masked in place inside a
+//     16-bit half is an exact f16 subnormal q 2^(b - 24) (b = the field's bit
+//     offset), so two fields come out of one v_and_b32;
+//   A (activations): row m is the 16-value run m of the column (one group of
+//     Q2_K/Q3_K, half a group of Q4_K), holding the run's values only in the
+//     K slots that carry that run's fields, zeros elsewhere (block diagonal);
+//     each run's dot product lands in its own row of C;
+//   the run's f16 values are x * s_run * 2^-shift(run), with s_run a power of
+//     two per run (max |x| of the run in [2^14, 2^15)) and shift the field
+//     offset that format puts the run at, so C = s_run 2^-24 sum x q for
+//     every run whatever its field offset; the run factors 2^48 / s_run and
+//     the run sums of x are staged beside the values.
+// Group scales and minimums enter after the MFMA, per C row.
+//
+// Staged run row (words), K values: [pairs K/2][run sums K/16][run factors
+// K/16]; run r holds 8 words, word j = values (base, base + 2) with base =
+// 4 (j >> 1) + (j & 1), the order in which masked fields pair up.
+//
+// Reference semantics: dequantize_q2_k_block / q3_k / q4_k
+// (crates/gguf/src/lib.rs:1226-1405); gate/up with SwiGLU and the routing
+// weight folded into h, down summed over the ranks
+// (crates/backend/src/metal/kernels/gguf_moe_kernels.metal:340-565,
+// laguna_xs_kernels.metal:1578-1715). Accumulation is fp32; the order differs
+// from the reference's (the parity bound is the layer tolerance).
+#pragma once
+#include "decode.hpp"
+#include "decode_mfma.hpp"
+
+namespace inferno {
+namespace runs_decode {
+
+using mfma_decode::as_h2;
+using mfma_decode::floatx4;
+using mfma_decode::half8;
+using mfma_decode::u32x4;
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32_a2 __attribute__((aligned(2)));
+
+constexpr int kWaves = 16;
+constexpr int kThreads = 64 * kWaves;
+constexpr float kTwoM24 = 1.0f / 16777216.0f;
+
+__host__ __device__ constexpr int run_words(int K) { return K / 2 + K / 8; }
+
+// ------------------------------------------------------------- formats
+
+template <int Q>
+struct RF;
+
+__device__ __forceinline__ half8 load_a(const uint32_t* p) {
+  return __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(p));
+}
+__device__ __forceinline__ floatx4 mfma(half8 a, uint4 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(half8, b), c, 0, 0, 0);
+}
+
+// Q2_K [scales 16 | qs 64 | d | dmin]. Run = group g (16 values) = 8 h + 2 p
+// + s: field plane p of qs bytes 32 h + 16 s + i. MFMA (pp, hf): B lane group
+// q = 2 h + s takes qs bytes 16 q + 8 hf + {0, 2, 1, 3, 4, 6, 5, 7} at plane
+// pp; run m is live in lane group 2 (m >> 3) + (m & 1), MFMAs pp = (m >> 1) & 3.
+template <>
+struct RF<INFERNO_Q2_K> {
+  static constexpr int kBytes = 84;
+  typedef mfma_decode::half2v half2v_t;
+  __host__ __device__ static int run_shift(int r) { return 2 * ((r >> 1) & 3); }
+  template <int NA>
+  __device__ static void dot(const uint8_t* blk, const uint32_t* const (&cols)[NA],
+                             const uint32_t* zero, int n, int q, floatx4 (&C)[NA]) {
+    const bool act = q == 2 * (n >> 3) + (n & 1);
+    const int pm = (n >> 1) & 3;
+    const u32x4_a2 qs = *reinterpret_cast<const u32x4_a2*>(blk + 16 + 16 * q);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const uint32_t w0 = hf ? qs.z : qs.x, w1 = hf ? qs.w : qs.y;
+      const uint32_t o0 = w0 >> 8, o1 = w1 >> 8;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const uint32_t M = 0x00030003u << (2 * pp);
+        const uint4 bv = make_uint4(w0 & M, o0 & M, w1 & M, o1 & M);
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+          const uint32_t* src = (act && pp == pm) ? cols[a] + n * 8 + 4 * hf : zero;
+          C[a] = mfma(load_a(src), bv, C[a]);
+        }
+      }
+    }
+  }
+  // sum over this lane's C rows (runs 4 q + j) of the group dots, the run sums
+  // and factors at sums[4 q + j], kk[4 q + j]
+  __device__ static float epilogue(const uint8_t* blk, floatx4 C, float4 sums, float4 kk,
+                                   int q) {
+    const uint32_t scw = *reinterpret_cast<const u32_a2*>(blk + 4 * q);
+    const half2v_t dm = as_h2(*reinterpret_cast<const u32_a2*>(blk + 80));
+    const float c[4] = {C[0], C[1], C[2], C[3]};
+    const float s[4] = {sums.x, sums.y, sums.z, sums.w};
+    const float f[4] = {kk.x, kk.y, kk.z, kk.w};
+    float S = 0.f, Mn = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t b = (scw >> (8 * j)) & 0xffu;
+      S = fmaf(float(b & 15u), c[j] * f[j], S);
+      Mn = fmaf(float(b >> 4), s[j], Mn);
+    }
+    return (float)dm.x * (S * kTwoM24) - (float)dm.y * Mn;
+  }
+};
+
+// Q3_K [hmask 32 | qs 64 | scales 12 | d]: the low two bits sit where Q2_K's
+// do (qs at byte 32), the high bit of value i of group g = 8 h + 2 p + s in
+// hmask byte 16 s + i, bit 4 h + p. Masked at bit 2 pp + 2 of the same half
+// it joins the low field: q3 4^pp = (low + 4 hbit) 4^pp, one MFMA per
+// (pp, hf) as for Q2_K. Value = gs (q3 - 4), gs = d (s6 - 32).
+template <>
+struct RF<INFERNO_Q3_K> {
+  static constexpr int kBytes = 110;
+  typedef mfma_decode::half2v half2v_t;
+  __host__ __device__ static int run_shift(int r) { return 2 * ((r >> 1) & 3); }
+  template <int NA>
+  __device__ static void dot(const uint8_t* blk, const uint32_t* const (&cols)[NA],
+                             const uint32_t* zero, int n, int q, floatx4 (&C)[NA]) {
+    const bool act = q == 2 * (n >> 3) + (n & 1);
+    const int pm = (n >> 1) & 3;
+    const u32x4_a2 qs = *reinterpret_cast<const u32x4_a2*>(blk + 32 + 16 * q);
+    const u32x4_a2 hm = *reinterpret_cast<const u32x4_a2*>(blk + 16 * (q & 1));
+    // lane group q = 2 h + s needs bit 4 h + pp of each hmask byte: shifted
+    // down by 4 h once, bit pp of every byte is that bit
+    const int hsh = 4 * (q >> 1);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const uint32_t w0 = hf ? qs.z : qs.x, w1 = hf ? qs.w : qs.y;
+      const uint32_t x0 = (hf ? hm.z : hm.x) >> hsh, x1 = (hf ? hm.w : hm.y) >> hsh;
+      const uint32_t o0 = w0 >> 8, o1 = w1 >> 8;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const uint32_t M = 0x00030003u << (2 * pp);
+        const uint32_t MH = 0x00040004u << (2 * pp);
+        // bytes 0, 2: bit pp to bit 2 pp + 2; bytes 1, 3: bit 8 + pp to 2 pp + 2
+        const uint4 bv = make_uint4((w0 & M) | ((x0 << (pp + 2)) & MH),
+                                    (o0 & M) | ((x0 >> (6 - pp)) & MH),
+                                    (w1 & M) | ((x1 << (pp + 2)) & MH),
+                                    (o1 & M) | ((x1 >> (6 - pp)) & MH));
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+          const uint32_t* src = (act && pp == pm) ? cols[a] + n * 8 + 4 * hf : zero;
+          C[a] = mfma(load_a(src), bv, C[a]);
+        }
+      }
+    }
+  }
+  __device__ static float epilogue(const uint8_t* blk, floatx4 C, float4 sums, float4 kk,
+                                   int q) {
+    // groups 4 q + j: low nibble of scales[(4 q + j) % 8] (high nibble for
+    // q >= 2), high two bits of scales[8 + j] at bit 2 q
+    const uint32_t lo = *reinterpret_cast<const u32_a2*>(blk + 96 + 4 * (q & 1));
+    const uint32_t hi = *reinterpret_cast<const u32_a2*>(blk + 104);
+    const uint32_t s6 = ((lo >> (4 * (q >> 1))) & 0x0f0f0f0fu) | (((hi >> (2 * q)) & 0x03030303u) << 4);
+    const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 108));
+    const float c[4] = {C[0], C[1], C[2], C[3]};
+    const float s[4] = {sums.x, sums.y, sums.z, sums.w};
+    const float f[4] = {kk.x, kk.y, kk.z, kk.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float gs = float(int((s6 >> (8 * j)) & 0xffu) - 32);
+      acc = fmaf(gs, fmaf(c[j] * f[j], kTwoM24, -4.0f * s[j]), acc);
+    }
+    return d * acc;
+  }
+};
+
+// Q4_K [d | dmin | scales 12 | qs 128]: group g (32 values) = runs 2 g, 2 g +
+// 1; qs chunk c (bytes 32 c ..) holds groups 2 c (low nibbles) and 2 c + 1
+// (high nibbles). MFMA (jj, nib): lane group q takes chunk q bytes 8 jj +
+// {0, 2, 1, 3, 4, 6, 5, 7}, nibble nib (a field at bit 4 nib of the byte).
+// Run m = 2 g + half is live in lane group m >> 2, MFMAs nib = (m >> 1) & 1,
+// jj = 2 (m & 1) + {0, 1} (its 16 values are chunk bytes 16 (m & 1) ..).
+template <>
+struct RF<INFERNO_Q4_K> {
+  static constexpr int kBytes = 144;
+  typedef mfma_decode::half2v half2v_t;
+  __host__ __device__ static int run_shift(int r) { return 4 * ((r >> 1) & 1); }
+  template <int NA>
+  __device__ static void dot(const uint8_t* blk, const uint32_t* const (&cols)[NA],
+                             const uint32_t* zero, int n, int q, floatx4 (&C)[NA]) {
+    const bool act = q == (n >> 2);
+    const int nm = (n >> 1) & 1, hm = n & 1;
+    const u32x4_a2 c0 = *reinterpret_cast<const u32x4_a2*>(blk + 16 + 32 * q);
+    const u32x4_a2 c1 = *reinterpret_cast<const u32x4_a2*>(blk + 32 + 32 * q);
+    const uint32_t w[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const uint32_t w0 = w[2 * jj], w1 = w[2 * jj + 1];
+      const uint32_t o0 = w0 >> 8, o1 = w1 >> 8;
+#pragma unroll
+      for (int nib = 0; nib < 2; ++nib) {
+        const uint32_t M = nib ? 0x00f000f0u : 0x000f000fu;
+        const uint4 bv = make_uint4(w0 & M, o0 & M, w1 & M, o1 & M);
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+          const uint32_t* src =
+              (act && nib == nm && (jj >> 1) == hm) ? cols[a] + n * 8 + 4 * (jj & 1) : zero;
+          C[a] = mfma(load_a(src), bv, C[a]);
+        }
+      }
+    }
+  }
+  __device__ static float epilogue(const uint8_t* blk, floatx4 C, float4 sums, float4 kk,
+                                   int q) {
+    // runs 4 q + j: groups 2 q (j < 2) and 2 q + 1 (j >= 2); 6-bit scale and
+    // min of group g (crates/gguf/src/lib.rs:1407-1416)
+    const uint8_t* sb = blk + 4;
+    float sc[2], mn[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int g = 2 * q + k;
+      uint32_t s, m;
+      if (g < 4) {
+        s = sb[g] & 63u;
+        m = sb[g + 4] & 63u;
+      } else {
+        s = (sb[g + 4] & 15u) | ((uint32_t(sb[g - 4]) >> 6) << 4);
+        m = (uint32_t(sb[g + 4]) >> 4) | ((uint32_t(sb[g]) >> 6) << 4);
+      }
+      sc[k] = float(s);
+      mn[k] = float(m);
+    }
+    const half2v_t dm = as_h2(*reinterpret_cast<const u32_a2*>(blk));
+    const float S0 = fmaf(C[0], kk.x, C[1] * kk.y), S1 = fmaf(C[2], kk.z, C[3] * kk.w);
+    const float D = fmaf(sc[0], S0, sc[1] * S1) * kTwoM24;
+    const float Mn = fmaf(mn[0], sums.x + sums.y, mn[1] * (sums.z + sums.w));
+    return (float)dm.x * D - (float)dm.y * Mn;
+  }
+};
+
+// ------------------------------------------------------------- staging
+
+// Stages one 16-value run held one value per lane by a 16-lane group (lane i
+// of the group holds value i; all 16 call it) into the run row layout above,
+// values scaled by s_run 2^-shift.
+__device__ __forceinline__ void stage_run16(float v, uint32_t* row, int K, int run, int shift) {
+  const int lane = threadIdx.x & 63, i = lane & 15;
+  float m = fabsf(v), sum = v;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) {
+    m = fmaxf(m, __shfl_xor(m, o, 16));
+    sum += __shfl_xor(sum, o, 16);
+  }
+  float s = 1.0f;  // zero or non-finite runs keep scale 1
+  if (m > 0.f && m < 3.0e38f) {
+    int e;
+    frexpf(m, &e);
+    s = ldexpf(1.0f, 15 - e);
+  }
+  const _Float16 hv = (_Float16)(v * (s * ldexpf(1.0f, -shift)));
+  const uint32_t hb = __builtin_bit_cast(uint16_t, hv);
+  const int j = i & 7, base = 4 * (j >> 1) + (j & 1);
+  const uint32_t h0 = __shfl(hb, base, 16), h1 = __shfl(hb, base + 2, 16);
+  if (i < 8) row[run * 8 + j] = h0 | (h1 << 16);
+  if (i == 0) {
+    float* sums = reinterpret_cast<float*>(row + K / 2);
+    sums[run] = sum;
+    sums[K / 16 + run] = 16777216.0f * 16777216.0f / s;
+  }
+}
+
+// ------------------------------------------------------------- gate/up
+
+// Persistent over 16-row tiles t = blockIdx.x + j gridDim.x of the active
+// slots (gate and up rows of one expert, 2 x 16 x NB x kBytes contiguous
+// bytes, loaded into registers, stored to LDS, the next tile's loads in
+// flight while this one is computed). x is the token's staged run row (bf16
+// tokens: exact in f16 with the run scale), copied to LDS once. Units (matrix, column) are spread
+// over the wavefronts; the gate and up sums meet in LDS in wavefront order.
+// h = silu(gate) * up * w goes out as a staged run row for the down kernel.
+template <int Q, int NB>
+struct GateUpShape {
+  static constexpr int H = NB * kKBlock;
+  static constexpr int rb = NB * RF<Q>::kBytes;
+  static constexpr int Sx = run_words(H);
+  static constexpr int chunks = 2 * 16 * rb / 16;  // per tile
+  static constexpr int PER = (chunks + kThreads - 1) / kThreads;
+};
+
+template <int Q, int NB>
+__host__ __device__ constexpr size_t gate_up_runs_lds() {
+  using S = GateUpShape<Q, NB>;
+  return size_t(S::Sx + 4) * 4 + size_t(2 * 16) * S::rb + size_t(kWaves * 2 * 16) * 4 +
+         size_t(3 * kMaxExperts) * 4;
+}
+
+template <int Q, int NB>
+__global__ void __launch_bounds__(kThreads) gate_up_runs_kernel(DecodeArgs p, int ntiles) {
+  using S = GateUpShape<Q, NB>;
+  extern __shared__ uint32_t smem[];
+  constexpr int rb = S::rb, PER = S::PER, Sx = S::Sx, H = S::H;
+  const int I = p.I;
+  uint32_t* xs = smem;
+  uint32_t* zero = smem + Sx;
+  uint8_t* tl = reinterpret_cast<uint8_t*>(zero + 4);                     // [2][16 rows of rb]
+  float* part = reinterpret_cast<float*>(tl + 2 * 16 * rb);              // [wave][2][16]
+  uint32_t* slot_e = reinterpret_cast<uint32_t*>(part + kWaves * 2 * 16);
+  uint32_t* slot_a = slot_e + kMaxExperts;
+  float* slot_w = reinterpret_cast<float*>(slot_a + kMaxExperts);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, q = lane >> 4;
+  const int tiles_i = I / kRows;
+  u32x4 v[PER];
+  auto fetch = [&](int t, uint32_t expert) {
+    const size_t off = size_t(expert) * p.gate_stride + size_t(t % tiles_i) * 16 * size_t(rb);
+    const u32x4* g4 = reinterpret_cast<const u32x4*>(p.gate + off);
+    const u32x4* u4 = reinterpret_cast<const u32x4*>(p.up + off);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      int i = j * kThreads + tid;
+      i = i < S::chunks ? i : S::chunks - 1;  // clamped; the extra chunks are not stored
+      v[j] = i < S::chunks / 2 ? g4[i] : u4[i - S::chunks / 2];
+    }
+  };
+  int t = blockIdx.x;
+  if (t < ntiles) fetch(t, p.slots[t / tiles_i].x);
+  for (int i = tid; i < Sx / 4; i += kThreads)
+    reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(p.stage_xr)[i];
+  if (tid < 4) zero[tid] = 0;
+  for (int j = tid; j < p.max_slots; j += kThreads) {
+    const uint4 sl = p.slots[j];
+    slot_e[j] = sl.x;
+    slot_a[j] = sl.w;
+    slot_w[j] = p.weights[sl.w];
+  }
+  const float* sums = reinterpret_cast<const float*>(xs + H / 2);
+  const float* kks = sums + H / 16;
+  for (; t < ntiles; t += gridDim.x) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = j * kThreads + tid;
+      if (i < S::chunks) *reinterpret_cast<u32x4*>(tl + 16 * i) = v[j];  // tiles are contiguous
+    }
+    __syncthreads();
+    if (t + int(gridDim.x) < ntiles) fetch(t + gridDim.x, slot_e[(t + gridDim.x) / tiles_i]);
+    const int slot = t / tiles_i, tile = t - slot * tiles_i;
+    float acc[2] = {0.f, 0.f};
+    for (int u = wave; u < 2 * NB; u += kWaves) {
+      const int mat = u & 1, c = u >> 1;
+      const uint8_t* blk = tl + (mat * 16 + n) * rb + c * RF<Q>::kBytes;
+      const float4 xsum = *reinterpret_cast<const float4*>(sums + c * 16 + 4 * q);
+      const float4 kk = *reinterpret_cast<const float4*>(kks + c * 16 + 4 * q);
+      const uint32_t* const cols[1] = {xs + c * 128};
+      floatx4 C[1] = {{0.f, 0.f, 0.f, 0.f}};
+      RF<Q>::template dot<1>(blk, cols, zero, n, q, C);
+      const float r = RF<Q>::epilogue(blk, C[0], xsum, kk, q);
+      acc[0] += mat == 0 ? r : 0.f;
+      acc[1] += mat == 1 ? r : 0.f;
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      float r = acc[m];
+      r += __shfl_xor(r, 16, kWave);
+      r += __shfl_xor(r, 32, kWave);
+      if (q == 0) part[(wave * 2 + m) * 16 + n] = r;
+    }
+    __syncthreads();
+    // lanes 0..15 sum gate rows, 16..31 up rows, over the wavefronts in
+    // order; the next tile's LDS writes start only after a barrier these
+    // lanes also reach
+    if (tid < 32) {
+      float r = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) r += part[(w * 2 + (tid >> 4)) * 16 + (tid & 15)];
+      const float u = __shfl_down(r, 16, kWave);
+      const uint32_t a = slot_a[slot];  // the slot's (single) assignment
+      const float h = silu(r) * u * slot_w[slot];
+      if (tid < 16)
+        stage_run16(h, p.stage_h + size_t(a) * run_words(I), I, tile,
+                           RF<Q>::run_shift(tile & 15));
+    }
+  }
+}
+
+// ------------------------------------------------------------------ down
+
+// Output tile = TR rows of H over all k ranks (rank r's down rows [TR t,
+// TR t + TR) of expert e_r, TR * NB * kBytes contiguous bytes each); block
+// (rank, column) = one block dot against h_r (staged run rows written by the
+// gate/up kernel). Lanes n >= TR read row TR - 1 again and are not written.
+// out = (residual + shared down) + routed, wavefronts summed in order:
+// deterministic, no float atomics.
+template <int Q, int NB, int TR>
+struct DownShape {
+  static constexpr int K = NB * kKBlock;  // the expert intermediate I
+  static constexpr int rb = NB * RF<Q>::kBytes;
+  static constexpr int Sh = run_words(K);
+  static_assert(TR * rb % 16 == 0, "a rank tile must be whole 16-byte chunks");
+};
+
+template <int Q, int NB, int TR>
+__host__ __device__ constexpr size_t down_runs_lds(int k) {
+  using S = DownShape<Q, NB, TR>;
+  return size_t(k * S::Sh + 4) * 4 + size_t(k * TR) * S::rb + size_t(kWaves * 16) * 4 +
+         size_t(kMaxTopK) * 4;
+}
+
+template <int Q, int NB, int TR>
+__host__ __device__ constexpr int down_runs_per(int k) {
+  return (k * TR * NB * RF<Q>::kBytes / 16 + kThreads - 1) / kThreads;
+}
+
+template <int Q, int NB, int TR, int PER>
+__global__ void __launch_bounds__(kThreads) down_runs_kernel(DecodeArgs p, int ntiles) {
+  using S = DownShape<Q, NB, TR>;
+  extern __shared__ uint32_t smem[];
+  constexpr int K = S::K, rb = S::rb, Sh = S::Sh;
+  constexpr int cr = TR * rb / 16;  // 16-byte chunks per rank tile
+  const int k = p.k;
+  uint32_t* hs = smem;                                     // [k][Sh]
+  uint32_t* zero = hs + k * Sh;
+  uint8_t* tl = reinterpret_cast<uint8_t*>(zero + 4);     // [k][TR rows of rb], contiguous
+  float* part = reinterpret_cast<float*>(tl + k * TR * rb);  // [wave][16]
+  uint32_t* rank_e = reinterpret_cast<uint32_t*>(part + kWaves * 16);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, q = lane >> 4;
+  const int nr = n < TR ? n : TR - 1;
+  if (tid < k) rank_e[tid] = p.ids[tid];
+  u32x4 v[PER];
+  auto fetch = [&](int t) {
+    const int nv = k * cr;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      int i = j * kThreads + tid;
+      i = i < nv ? i : nv - 1;  // clamped; the extra chunks are not stored
+      const int r = i / cr, w = i - r * cr;
+      const u32x4* src = reinterpret_cast<const u32x4*>(
+          p.down + size_t(rank_e[r]) * p.down_stride + size_t(t) * TR * rb);
+      v[j] = src[w];
+    }
+  };
+  int t = blockIdx.x;
+  __syncthreads();
+  if (t < ntiles) fetch(t);
+  for (int i = tid; i < k * Sh / 4; i += kThreads)
+    reinterpret_cast<uint4*>(hs)[i] = reinterpret_cast<const uint4*>(p.stage_h)[i];
+  if (tid < 4) zero[tid] = 0;
+  const int nblk = k * NB;
+  for (; t < ntiles; t += gridDim.x) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = j * kThreads + tid;
+      if (i < k * cr) *reinterpret_cast<u32x4*>(tl + 16 * i) = v[j];
+    }
+    __syncthreads();
+    if (t + int(gridDim.x) < ntiles) fetch(t + gridDim.x);
+    float acc = 0.f;
+    for (int b = wave; b < nblk; b += kWaves) {
+      const int r = b / NB, c = b - r * NB;
+      const uint32_t* hr = hs + r * Sh;
+      const float* sums = reinterpret_cast<const float*>(hr + K / 2);
+      const float4 hsum = *reinterpret_cast<const float4*>(sums + c * 16 + 4 * q);
+      const float4 kk = *reinterpret_cast<const float4*>(sums + K / 16 + c * 16 + 4 * q);
+      const uint8_t* blk = tl + (r * TR + nr) * rb + c * RF<Q>::kBytes;
+      const uint32_t* const cols[1] = {hr + c * 128};
+      floatx4 C[1] = {{0.f, 0.f, 0.f, 0.f}};
+      RF<Q>::template dot<1>(blk, cols, zero, n, q, C);
+      acc += RF<Q>::epilogue(blk, C[0], hsum, kk, q);
+    }
+    acc += __shfl_xor(acc, 16, kWave);
+    acc += __shfl_xor(acc, 32, kWave);
+    if (q == 0) part[wave * 16 + n] = acc;
+    __syncthreads();
+    if (tid < TR) {
+      float y = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) y += part[w * 16 + tid];
+      const size_t o = size_t(t) * TR + tid;
+      const float base = (p.residual ? p.residual[o] : 0.f) + (p.ys ? p.ys[o] : 0.f);
+      p.out[o] = base + y;
+    }
+  }
+}
+
+}  // namespace runs_decode
+}  // namespace inferno

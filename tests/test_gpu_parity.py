@@ -297,7 +297,10 @@ def _layer_parity(cuda, key, T, tokens=None, variants=1):
         out = lt.layer.forward(x, residual, ids=ids, weights=w)
         out2 = lt.layer.forward(x, residual)
         torch.cuda.synchronize()
-        assert torch.equal(out, out2), "layer output is not bitwise reproducible"
+        assert torch.equal(out, out2), (
+            f"layer output is not bitwise reproducible: {(out != out2).sum().item()} of "
+            f"{out.numel()} differ, NaNs {torch.isnan(out).sum().item()}/"
+            f"{torch.isnan(out2).sum().item()}, first at {(out != out2).nonzero()[:4].tolist()}")
         ref, _, _, f = ph.oracle_layer_tokens(cfg, lt, x, residual, tokens,
                                               ph.to_np(ids).view(np.uint32), ph.to_np(w))
         flips += f
@@ -391,6 +394,40 @@ def test_layer_q2k_decode_mfma_shapes(cuda, H, E, I, k, Is):
     cfg = cf.Config(f"q2k_decode_h{H}_e{E}_i{I}_k{k}_s{Is}", 20 + H // 1024, H, E, I, k,
                     (cf.Q2_K,), cf.SCORE_SIGMOID, True, 2.5, 0.1, Is, torch.bfloat16, (1,))
     _layer_parity(cuda, cfg, 1)
+
+
+# One-token layers on the f16-run matrix-core kernels (gate/up and down) for
+# every routed format: bf16 tokens, 3 to 8 down columns, 4 to 16 ranks, with
+# and without a shared expert. Q2_K keeps the fp8 x fp4 gate/up and takes the
+# run down; fp32 tokens keep the tile kernels.
+@pytest.mark.parametrize("quant", [Q2_K, Q3_K, Q4_K])
+@pytest.mark.parametrize("H,E,I,k,Is,dt", [(2048, 64, 768, 8, 0, torch.float32),
+                                           (4096, 128, 1536, 10, 1536, torch.bfloat16),
+                                           (1024, 32, 1024, 16, 256, torch.bfloat16),
+                                           (3072, 16, 2048, 4, 512, torch.bfloat16),
+                                           (2048, 64, 768, 8, 0, torch.bfloat16)])
+def test_layer_runs_decode_shapes(cuda, quant, H, E, I, k, Is, dt):
+    cfg = cf.Config(f"runs_decode_q{quant}_h{H}_i{I}_k{k}_s{Is}", 40 + H // 1024 + quant, H, E, I,
+                    k, (quant,), cf.SCORE_SOFTMAX if k == 10 else cf.SCORE_SIGMOID, True, 2.5,
+                    0.0 if k == 10 else 0.1, Is, dt, (1,))
+    _layer_parity(cuda, cfg, 1, variants=4)
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=1)
+    ops.kernel_timing(True)
+    try:
+        lt.layer.forward(cf.make_input(cfg, 1, device=cuda), None)
+        torch.cuda.synchronize()
+        gu = ops.kernel_timing_label(ops.TIMER_GATE_UP)
+        dn = ops.kernel_timing_label(ops.TIMER_DOWN)
+    finally:
+        ops.kernel_timing(False)
+    if dt == torch.float32:
+        assert gu.startswith("tiles:"), gu
+        return
+    if quant == Q2_K:
+        assert gu.startswith("mfma:"), gu
+    else:
+        assert gu.startswith("runs:"), gu
+    assert dn.startswith("runs-down:") or dn.startswith("mfma-down:"), dn
 
 
 def test_layer_c3_glm_q3k_prefill_all_tokens(cuda):
