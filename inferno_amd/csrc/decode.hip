@@ -628,44 +628,56 @@ int shared_parts(int H) {
   return 1;
 }
 
+// The fp8 x fp4 gate/up: one bf16 token, Q2_K (NB a multiple of 4, 4..28)
+// or Q3_K (NB a multiple of 8, 8..24).
 bool mfma_gate_up_covers(const DecodeArgs& a, int quant) {
-  return mfma_enabled() && a.T == 1 && quant == INFERNO_Q2_K && a.x_dtype == INFERNO_BF16 &&
-         (a.Is == 0 || a.shared_gu != nullptr) &&
-         a.I % kRows == 0 && mfma_decode::covers_width(a.H) &&
-         mfma_decode::lds_bytes(a.H) <= 160 * 1024 && a.stage_xm != nullptr &&
+  const int NB = a.H / kKBlock;
+  const bool shape = quant == INFERNO_Q2_K ? mfma_decode::covers_width(a.H)
+                     : quant == INFERNO_Q3_K ? (a.H % kKBlock == 0 && NB % 8 == 0 && NB >= 8 && NB <= 24)
+                                             : false;
+  return mfma_enabled() && a.T == 1 && shape && a.x_dtype == INFERNO_BF16 &&
+         (a.Is == 0 || a.shared_gu != nullptr) && a.I % kRows == 0 &&
+         mfma_decode::lds_bytes(a.H, quant) <= 160 * 1024 && a.stage_xm != nullptr &&
          device_cus() > 0;
 }
 
-template <int NB>
+template <int Q, int NB>
 int launch_gate_up_mfma_nb(hipStream_t s, const DecodeArgs& a, int ntiles) {
   static bool attr = false;
+  auto* kern = mfma_decode::gate_up_fp4_kernel<Q, NB>;
   if (!attr) {
-    if (hipFuncSetAttribute((const void*)mfma_decode::gate_up_q2k_kernel<NB>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024) != hipSuccess) {
       set_error("MFMA gate/up kernel: cannot raise its LDS limit");
       return INFERNO_ERR_DEVICE;
     }
     attr = true;
   }
   const unsigned grid = unsigned(std::min(ntiles, device_cus()));
-  mfma_decode::gate_up_q2k_kernel<NB>
-      <<<grid, mfma_decode::kThreads, mfma_decode::lds_bytes(a.H), s>>>(a, ntiles);
+  kern<<<grid, mfma_decode::kThreads, mfma_decode::lds_bytes(a.H, Q), s>>>(a, ntiles);
   INF_LAUNCHED();
   return INFERNO_OK;
 }
 
-// The routed tiles of the k slots on the MFMA kernel (the shared expert's
-// gate/up already ran in the route launch).
-int launch_gate_up_mfma(hipStream_t s, const DecodeArgs& a0) {
+// The routed tiles of the k slots on the fp8 x fp4 kernel (the shared
+// expert's gate/up already ran in the route launch).
+int launch_gate_up_mfma(hipStream_t s, const DecodeArgs& a0, int quant) {
   const int ntiles = a0.max_slots * (a0.I / kRows);
+  if (quant == INFERNO_Q3_K) {
+    switch (a0.H / kKBlock) {
+      case 8: return launch_gate_up_mfma_nb<INFERNO_Q3_K, 8>(s, a0, ntiles);
+      case 16: return launch_gate_up_mfma_nb<INFERNO_Q3_K, 16>(s, a0, ntiles);
+      default: return launch_gate_up_mfma_nb<INFERNO_Q3_K, 24>(s, a0, ntiles);
+    }
+  }
   switch (a0.H / kKBlock) {
-    case 4: return launch_gate_up_mfma_nb<4>(s, a0, ntiles);
-    case 8: return launch_gate_up_mfma_nb<8>(s, a0, ntiles);
-    case 12: return launch_gate_up_mfma_nb<12>(s, a0, ntiles);
-    case 16: return launch_gate_up_mfma_nb<16>(s, a0, ntiles);
-    case 20: return launch_gate_up_mfma_nb<20>(s, a0, ntiles);
-    case 24: return launch_gate_up_mfma_nb<24>(s, a0, ntiles);
-    default: return launch_gate_up_mfma_nb<28>(s, a0, ntiles);
+    case 4: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 4>(s, a0, ntiles);
+    case 8: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 8>(s, a0, ntiles);
+    case 12: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 12>(s, a0, ntiles);
+    case 16: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 16>(s, a0, ntiles);
+    case 20: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 20>(s, a0, ntiles);
+    case 24: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 24>(s, a0, ntiles);
+    default: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 28>(s, a0, ntiles);
   }
 }
 
@@ -764,7 +776,8 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   // down after a matrix-core gate/up (h in the run layout): the Q2_K kernel
   // (I = 2048, k <= 8) or the run kernel; the shared down then runs in the
   // select launch
-  const bool use_q2k_down = use_fp4 && mfma_decode::down_covers(a.I, a.k) && shared_down_ok &&
+  const bool use_q2k_down = use_fp4 && quant == INFERNO_Q2_K && mfma_decode::down_covers(a.I, a.k) &&
+                            shared_down_ok &&
                             mfma_decode::down_lds_bytes(a.I) <= 160 * 1024;
   const bool use_runs_down = !use_q2k_down && use_mfma && shared_down_ok &&
                              runs_down_covers(quant, a.H, a.I, a.k);
@@ -821,11 +834,11 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   // residual folded in: one stream, no events
   a.routed_tiles = a.max_slots * (a.I / kRows);
   const char* gu_label =
-      use_fp4 ? "mfma: gate_up_q2k_kernel (routed Q2_K tiles on MFMA; shared gate/up in the route launch)"
+      use_fp4 ? "mfma: gate_up_fp4_kernel (routed tiles on fp8 x fp4 MFMA; shared gate/up in the route launch)"
       : use_runs ? "runs: gate_up_runs_kernel (routed tiles on f16 MFMA; shared gate/up in the route launch)"
                  : "tiles: gate_up_kernel (routed + Q8_0 shared tiles)";
   int st = timed(s, kTimerGateUp, gu_label, [&]() -> int {
-    if (use_fp4) return launch_gate_up_mfma(s, a);
+    if (use_fp4) return launch_gate_up_mfma(s, a, quant);
     if (use_runs) return launch_gate_up_runs(s, a, quant);
     switch (quant) {
       case INFERNO_Q2_K: xsplit ? launch_gate_up<INFERNO_Q2_K, true>(s, a) : launch_gate_up<INFERNO_Q2_K, false>(s, a); break;

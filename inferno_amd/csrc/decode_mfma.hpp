@@ -48,6 +48,8 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32_a2 __attribute__((aligned(2)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 
 constexpr int kWaves = 16;
@@ -64,7 +66,7 @@ constexpr int kRowPad = 16;    // LDS row padding (bytes): rows start on distinc
 // below ~max|x| 2^-17 of its column. Staged row (words), per token:
 //   [column images K/256 x 256][run sums K/16][column exponents K/256], padded to 4.
 // A column image is [term 2][group m 16][half 2] x 16 bytes laid out for the
-// A operand of v_mfma_scale_f32_16x16x128_f8f6f4 (see gate_up_q2k_kernel):
+// A operand of v_mfma_scale_f32_16x16x128_f8f6f4 (see gate_up_fp4_kernel):
 // byte t of (m, half) holds value i = 4 j + b of group m, j = 2 half + t / 8,
 // b = (t % 8) / 2, when t % 2 == p(m) >> 1, and 0 otherwise.
 
@@ -194,19 +196,32 @@ __device__ __forceinline__ void fetch_tile(u32x4 (&v)[PER], const DecodeArgs& p,
   }
 }
 
+// Block bytes of the formats the fp8 x fp4 gate/up takes.
+__host__ __device__ constexpr int fp4_block_bytes(int Q) { return Q == INFERNO_Q3_K ? 110 : kQ2Bytes; }
+
 // Chunks per thread of a layer with NB super-block columns.
-__host__ __device__ constexpr int chunks_per_thread(int NB) {
-  return (2 * NB * kQ2Bytes + kThreads - 1) / kThreads;
+__host__ __device__ constexpr int chunks_per_thread(int NB, int bytes = kQ2Bytes) {
+  return (2 * NB * bytes + kThreads - 1) / kThreads;
 }
 
-// NB = H / 256 super-block columns (a multiple of 4, so rows are whole
-// 16-byte chunks); compile-time so that the chunk -> (matrix, row, column)
-// split and the LDS addressing use constant divisors and strides.
-template <int NB>
-__global__ void __launch_bounds__(kThreads) gate_up_q2k_kernel(DecodeArgs p, int ntiles) {
+// NB = H / 256 super-block columns (rows must be whole 16-byte chunks: NB a
+// multiple of 4 for Q2_K, of 8 for Q3_K); compile-time so that the chunk ->
+// (matrix, row, column) split and the LDS addressing use constant divisors
+// and strides.
+//
+// Q3_K [hmask 32 | qs 64 | scales 12 | d] has Q2_K's low two bits in qs at
+// byte 32 and the high bit of value i of group g = 8 h + 2 p + s in hmask
+// byte 16 s + i, bit 4 h + p: lane group q = 2 h + s moves bit 4 h + p of
+// hmask byte i into the low bit of the nibble that holds plane p of qs byte
+// i, a second fp4 B (value hbit / 2) whose MFMAs take the A scale + 2 (x 4),
+// so C = sum x (low + 4 hbit) / 2 = sum x q3 / 2; value = gs (q3 - 4).
+template <int Q, int NB>
+__global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int ntiles) {
   extern __shared__ uint32_t smem[];
-  constexpr int H = NB * kKBlock, PER = chunks_per_thread(NB);
-  constexpr int rb = NB * kQ2Bytes, RS = rb + kRowPad, nv = rb;
+  constexpr int kB = fp4_block_bytes(Q);
+  constexpr int H = NB * kKBlock, PER = chunks_per_thread(NB, kB);
+  constexpr int rb = NB * kB, RS = rb + kRowPad, nv = rb;
+  static_assert(rb % 16 == 0, "rows must be whole 16-byte chunks");
   constexpr int Sm = stage_words(H);
   const int I = p.I;
   uint32_t* xs = smem;
@@ -287,18 +302,61 @@ __global__ void __launch_bounds__(kThreads) gate_up_q2k_kernel(DecodeArgs p, int
       const int sa1 = 127 + e1s[c], sa2 = sa1 - 4;  // E8M0 scales of the two x terms
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
-        const uint8_t* blk = tl + (m * 16 + n) * RS + c * kQ2Bytes;
-        const u32x4_a4 qs = *reinterpret_cast<const u32x4_a4*>(blk + 16 + 16 * q);
-        const uint32_t scw = *reinterpret_cast<const uint32_t*>(blk + 4 * q);
-        const uint32_t dmw = *reinterpret_cast<const uint32_t*>(blk + 80);
+        const uint8_t* blk = tl + (m * 16 + n) * RS + c * kB;
         // B (fp4 weights): a 2-bit field in the low bits of a nibble is the
         // e2m1 value q / 2; planes 0 (low nibble) and 2 (high nibble) in
         // MFMA 0, planes 1 and 3 in MFMA 1
         const uint32_t F = 0x33333333u;
+        floatx4 C = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (Q == INFERNO_Q3_K) {
+          const u32x4_a2 qs = *reinterpret_cast<const u32x4_a2*>(blk + 32 + 16 * q);
+          const u32x4_a2 hm = *reinterpret_cast<const u32x4_a2*>(blk + 16 * (q & 1));
+          const v8i B0 = v8i{int(qs.x & F), int(qs.y & F), int(qs.z & F), int(qs.w & F), 0, 0, 0, 0};
+          const v8i B1 = v8i{int((qs.x >> 2) & F), int((qs.y >> 2) & F), int((qs.z >> 2) & F),
+                             int((qs.w >> 2) & F), 0, 0, 0, 0};
+          // high bits: bit 4 h + p of each hmask byte to bit 0 of the nibble
+          // holding plane p (p = 0, 2 for MFMA 0; 1, 3 for MFMA 1)
+          const int hsh = 4 * (q >> 1);
+          const uint32_t x0 = hm.x >> hsh, x1 = hm.y >> hsh, x2 = hm.z >> hsh, x3 = hm.w >> hsh;
+          const uint32_t L = 0x01010101u, U = 0x10101010u;
+          const v8i H0 = v8i{int((x0 & L) | ((x0 << 2) & U)), int((x1 & L) | ((x1 << 2) & U)),
+                             int((x2 & L) | ((x2 << 2) & U)), int((x3 & L) | ((x3 << 2) & U)),
+                             0, 0, 0, 0};
+          const v8i H1 = v8i{int(((x0 >> 1) & L) | ((x0 << 1) & U)),
+                             int(((x1 >> 1) & L) | ((x1 << 1) & U)),
+                             int(((x2 >> 1) & L) | ((x2 << 1) & U)),
+                             int(((x3 >> 1) & L) | ((x3 << 1) & U)), 0, 0, 0, 0};
+          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][0], B0, C, 0, 4, 0, sa1, 0, 127);
+          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][1], B1, C, 0, 4, 0, sa1, 0, 127);
+          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][0], B0, C, 0, 4, 0, sa2, 0, 127);
+          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][1], B1, C, 0, 4, 0, sa2, 0, 127);
+          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][0], H0, C, 0, 4, 0, sa1 + 2, 0, 127);
+          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][1], H1, C, 0, 4, 0, sa1 + 2, 0, 127);
+          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][0], H0, C, 0, 4, 0, sa2 + 2, 0, 127);
+          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][1], H1, C, 0, 4, 0, sa2 + 2, 0, 127);
+          // groups 4 q + j: 6-bit scale = low nibble of scales[(4 q + j) % 8]
+          // (high nibble for q >= 2) | high two bits of scales[8 + j] at bit 2 q
+          const uint32_t lo = *reinterpret_cast<const u32_a2*>(blk + 96 + 4 * (q & 1));
+          const uint32_t hi = *reinterpret_cast<const u32_a2*>(blk + 104);
+          const uint32_t s6 = ((lo >> (4 * (q >> 1))) & 0x0f0f0f0fu) |
+                              (((hi >> (2 * q)) & 0x03030303u) << 4);
+          const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 108));
+          const float xs4[4] = {xsum.x, xsum.y, xsum.z, xsum.w};
+          float t = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float gs = float(int((s6 >> (8 * j)) & 0xffu) - 32);
+            t = fmaf(gs, fmaf(2.0f, C[j], -4.0f * xs4[j]), t);
+          }
+          acc[m] = fmaf(d, t, acc[m]);
+          continue;
+        }
+        const u32x4_a4 qs = *reinterpret_cast<const u32x4_a4*>(blk + 16 + 16 * q);
+        const uint32_t scw = *reinterpret_cast<const uint32_t*>(blk + 4 * q);
+        const uint32_t dmw = *reinterpret_cast<const uint32_t*>(blk + 80);
         const v8i B0 = v8i{int(qs.x & F), int(qs.y & F), int(qs.z & F), int(qs.w & F), 0, 0, 0, 0};
         const v8i B1 = v8i{int((qs.x >> 2) & F), int((qs.y >> 2) & F), int((qs.z >> 2) & F),
                            int((qs.w >> 2) & F), 0, 0, 0, 0};
-        floatx4 C = {0.f, 0.f, 0.f, 0.f};
         C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][0], B0, C, 0, 4, 0, sa1, 0, 127);
         C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][1], B1, C, 0, 4, 0, sa1, 0, 127);
         C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][0], B0, C, 0, 4, 0, sa2, 0, 127);
@@ -510,8 +568,8 @@ inline bool covers_width(int H) {
   return H % kKBlock == 0 && NB % 4 == 0 && NB >= 4 && NB <= 28;
 }
 
-inline size_t lds_bytes(int H) {
-  const int rb = H / kKBlock * kQ2Bytes;
+inline size_t lds_bytes(int H, int quant = INFERNO_Q2_K) {
+  const int rb = H / kKBlock * fp4_block_bytes(quant);
   return size_t(stage_words(H) + 4) * 4 + size_t(2 * 16) * (rb + kRowPad) +
          size_t(kWaves * 2 * 16) * 4 + size_t(3 * kMaxExperts) * 4;
 }

@@ -399,7 +399,8 @@ def test_layer_q2k_decode_mfma_shapes(cuda, H, E, I, k, Is):
 # One-token layers on the f16-run matrix-core kernels (gate/up and down) for
 # every routed format: bf16 tokens, 3 to 8 down columns, 4 to 16 ranks, with
 # and without a shared expert. Q2_K keeps the fp8 x fp4 gate/up and takes the
-# run down; fp32 tokens keep the tile kernels.
+# run down, as does Q3_K when its rows are whole 16-byte chunks (H a multiple
+# of 2048); fp32 tokens keep the tile kernels.
 @pytest.mark.parametrize("quant", [Q2_K, Q3_K, Q4_K])
 @pytest.mark.parametrize("H,E,I,k,Is,dt", [(2048, 64, 768, 8, 0, torch.float32),
                                            (4096, 128, 1536, 10, 1536, torch.bfloat16),
@@ -423,8 +424,8 @@ def test_layer_runs_decode_shapes(cuda, quant, H, E, I, k, Is, dt):
     if dt == torch.float32:
         assert gu.startswith("tiles:"), gu
         return
-    if quant == Q2_K:
-        assert gu.startswith("mfma:"), gu
+    if quant == Q2_K or (quant == Q3_K and (H // 256) % 8 == 0):
+        assert gu.startswith("mfma:"), gu  # the fp8 x fp4 gate/up
     else:
         assert gu.startswith("runs:"), gu
     assert dn.startswith("runs-down:") or dn.startswith("mfma-down:"), dn
