@@ -501,9 +501,11 @@ def test_stack_c4_laguna_q2k_q3k_rmsnorm_chain(cuda, T):
     expert), RMSNorm (eps 1e-6) before every layer, bf16 activations, one
     residual stream, against the oracle chain run from the same input.
     T = 1: 16 seeded tokens, one stack call each; T = 32: every token.
-    Tokens whose expert set differs from the oracle chain's within CHAIN_TIE
-    of the k-th selection value (the chain's inputs drift apart by rounding)
-    are counted and left out of the error; any other set difference fails.
+    Tokens whose expert set differs from the oracle chain's within the drift
+    bound of the k-th selection value (sum_h |W_r| |a_gpu - a_oracle|, from
+    the GPU's own stream entering the layer: the chain's inputs drift apart
+    by rounding) are counted and left out of the error; any other set
+    difference fails.
 
     Tolerance: each layer is held to the north_star's 2e-3 by
     test_stack_c4_each_layer_on_gpu_stream (same input on both sides). Along
@@ -513,6 +515,9 @@ def test_stack_c4_laguna_q2k_q3k_rmsnorm_chain(cuda, T):
     cfg = cf.CONFIGS["c4"]
     k = cfg.top_k
     lts, stack = cf.build_stack(cfg, cuda, max_tokens=T)
+    prefixes = [ops.MoEStack([lt.layer for lt in lts[:l]], [lt.norm_w for lt in lts[:l]],
+                             eps=cfg.rms_eps, act_dtype=cfg.x_dtype, max_tokens=T)
+                for l in range(1, cfg.layers)]
     variants = range(16) if T == 1 else [0]
     got_all, ref_all, r0_all = [], [], []
     n_tie = [0] * cfg.layers
@@ -521,10 +526,12 @@ def test_stack_c4_laguna_q2k_q3k_rmsnorm_chain(cuda, T):
         ids = torch.empty(cfg.layers * T * k, dtype=torch.int32, device=cuda)
         out = stack.forward(hidden, ids=ids)
         out2 = stack.forward(hidden)
+        streams = [hidden] + [pre.forward(hidden) for pre in prefixes]
         torch.cuda.synchronize()
         assert torch.equal(out, out2), "stack output is not bitwise reproducible"
         tokens = np.arange(T)
-        ref, ties = ph.oracle_stack_tokens(cfg, lts, hidden, tokens, ph.to_np(ids).view(np.uint32))
+        ref, ties = ph.oracle_stack_tokens(cfg, lts, hidden, tokens, ph.to_np(ids).view(np.uint32),
+                                           gpu_streams=streams)
         drop = set(t for tl in ties for t in tl)
         keep = np.array([t for t in tokens if t not in drop], dtype=np.int64)
         n_tie = [a + len(b) for a, b in zip(n_tie, ties)]
