@@ -231,10 +231,15 @@ typedef struct inferno_moe_layer {
   const void* down;
   size_t gate_bytes, up_bytes, down_bytes;
   size_t shared_intermediate; /* Is; 0 = no shared expert */
-  const void* shared_gate;    /* Q8_0 [Is rows of H] */
+  const void* shared_gate;    /* [Is rows of H], shared_quant */
   const void* shared_up;
-  const void* shared_down;    /* Q8_0 [H rows of Is] */
+  const void* shared_down;    /* [H rows of Is], shared_down_quant */
   size_t shared_gate_bytes, shared_up_bytes, shared_down_bytes;
+  /* Shared expert formats; 0 = Q8_0 (GLM, Laguna S). Laguna XS: Q4_K gate/up
+   * with Q4_K or Q6_K down (crates/model/src/laguna/gguf_model.rs:829-849,
+   * laguna_xs_gguf_moe_shared_device backend.rs:1754). */
+  int shared_quant;           /* Q8_0, Q2_K, Q3_K or Q4_K */
+  int shared_down_quant;      /* Q8_0, Q2_K, Q3_K, Q4_K or Q6_K */
 } inferno_moe_layer;
 
 size_t inferno_moe_layer_workspace_bytes(const inferno_moe_layer* layer, size_t T);

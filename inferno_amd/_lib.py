@@ -27,6 +27,7 @@ class LayerDesc(C.Structure):
         ("shared_intermediate", _sz),
         ("shared_gate", _vp), ("shared_up", _vp), ("shared_down", _vp),
         ("shared_gate_bytes", _sz), ("shared_up_bytes", _sz), ("shared_down_bytes", _sz),
+        ("shared_quant", _i), ("shared_down_quant", _i),
     ]
 
 

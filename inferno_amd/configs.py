@@ -32,6 +32,10 @@ class Config:
     zipf: float = 0.0          # >0: bias calibrated so expert load follows Zipf(s)
     balanced: bool = False     # bias calibrated so expert load is near-uniform (Zipf(0))
     zipf_empty: int = 0        # experts given no slot by the calibrated bias
+    down_quant: int = 0        # routed down format (0: the gate/up format)
+    shared_quant: int = Q8_0   # shared expert gate/up format
+    shared_down_quant: int = 0  # shared down format (0: the routed down format for a
+                                # non-Q8_0 shared expert, as Laguna XS; Q8_0 otherwise)
     rms_eps: float = 1e-6
     notes: str = ""
     weight_std: float = 0.02
@@ -77,6 +81,9 @@ class LayerTensors:
     down: torch.Tensor
     shared: tuple = None
     norm_w: torch.Tensor = None
+    down_quant: int = 0
+    shared_quant: int = Q8_0
+    shared_down_quant: int = Q8_0
     layer: ops.MoELayer = field(default=None, repr=False)
 
 
@@ -92,24 +99,29 @@ def build_layer(cfg, layer=0, device="cuda", max_tokens=1, bias=None):
     router = ops.synth_normal(stream_seed(cfg, layer, _ROUTER), ws, E * H, device=device).view(E, H)
     if bias is None and cfg.bias_std > 0:
         bias = ops.synth_normal(stream_seed(cfg, layer, _BIAS), cfg.bias_std, E, device=device)
+    dq = cfg.down_quant or q
+    sq = cfg.shared_quant
+    sdq = cfg.shared_down_quant or (Q8_0 if sq == Q8_0 else dq)
     gate = ops.synth_quantized(q, stream_seed(cfg, layer, _GATE), ws, E * I, H, device)
     up = ops.synth_quantized(q, stream_seed(cfg, layer, _UP), ws, E * I, H, device)
-    down = ops.synth_quantized(q, stream_seed(cfg, layer, _DOWN), ws, E * H, I, device)
+    down = ops.synth_quantized(dq, stream_seed(cfg, layer, _DOWN), ws, E * H, I, device)
     shared = None
     Is = cfg.shared_intermediate
     if Is:
-        shared = (ops.synth_quantized(Q8_0, stream_seed(cfg, layer, _SG), ws, Is, H, device),
-                  ops.synth_quantized(Q8_0, stream_seed(cfg, layer, _SU), ws, Is, H, device),
-                  ops.synth_quantized(Q8_0, stream_seed(cfg, layer, _SD), ws, H, Is, device))
+        shared = (ops.synth_quantized(sq, stream_seed(cfg, layer, _SG), ws, Is, H, device),
+                  ops.synth_quantized(sq, stream_seed(cfg, layer, _SU), ws, Is, H, device),
+                  ops.synth_quantized(sdq, stream_seed(cfg, layer, _SD), ws, H, Is, device))
     norm_w = 1.0 + ops.synth_normal(stream_seed(cfg, layer, _NORM), 0.1, H, device=device)
-    lt = LayerTensors(q, router, bias, gate, up, down, shared, norm_w)
+    lt = LayerTensors(q, router, bias, gate, up, down, shared, norm_w, down_quant=dq,
+                      shared_quant=sq, shared_down_quant=sdq)
     lt.layer = ops.MoELayer(
-        hidden=H, experts=E, intermediate=I, top_k=cfg.top_k, quant=q, down_quant=q,
+        hidden=H, experts=E, intermediate=I, top_k=cfg.top_k, quant=q, down_quant=dq,
         score_fn=cfg.score_fn, norm_topk_prob=cfg.norm, routed_scaling_factor=cfg.scale,
         router=router, router_bias=bias, gate=gate, up=up, down=down,
         shared_intermediate=Is,
         shared_gate=shared[0] if shared else None, shared_up=shared[1] if shared else None,
-        shared_down=shared[2] if shared else None, max_tokens=max_tokens)
+        shared_down=shared[2] if shared else None, shared_quant=sq, shared_down_quant=sdq,
+        max_tokens=max_tokens)
     return lt
 
 

@@ -492,16 +492,26 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
   INF_CHECK_ARG(std::isfinite(L->routed_scaling_factor), "routed scaling factor must be finite");
   INF_CHECK_ARG(L->router && L->gate && L->up && L->down && x && out && workspace, "null pointer");
   const size_t Is = L->shared_intermediate;
+  const int sq = L->shared_quant ? L->shared_quant : INFERNO_Q8_0;
+  const int sdq = L->shared_down_quant ? L->shared_down_quant : INFERNO_Q8_0;
   if (Is) {
     INF_CHECK_ARG(L->shared_gate && L->shared_up && L->shared_down, "null shared expert pointer");
-    if ((st = check_len("shared gate", L->shared_gate_bytes, 1, matrix_bytes(INFERNO_Q8_0, Is, H))))
-      return st;
-    if ((st = check_len("shared up", L->shared_up_bytes, 1, matrix_bytes(INFERNO_Q8_0, Is, H))))
-      return st;
-    if ((st = check_len("shared down", L->shared_down_bytes, 1, matrix_bytes(INFERNO_Q8_0, H, Is))))
-      return st;
+    INF_CHECK_ARG(sq == INFERNO_Q8_0 || is_routed_quant(sq),
+                  "shared gate/up must be Q8_0, Q2_K, Q3_K or Q4_K");
+    INF_CHECK_ARG(sdq == INFERNO_Q8_0 || is_down_quant(sdq),
+                  "shared down must be Q8_0, Q2_K, Q3_K, Q4_K or Q6_K");
     INF_CHECK_ARG(Is % kKBlock == 0, "shared intermediate must be a multiple of 256");
+    if ((st = check_len("shared gate", L->shared_gate_bytes, 1, matrix_bytes(sq, Is, H))))
+      return st;
+    if ((st = check_len("shared up", L->shared_up_bytes, 1, matrix_bytes(sq, Is, H))))
+      return st;
+    if ((st = check_len("shared down", L->shared_down_bytes, 1, matrix_bytes(sdq, H, Is))))
+      return st;
   }
+  // the fused decode launches and the dense MFMA shared GEMMs take a Q8_0
+  // shared expert (the GLM and Laguna S layers); other formats (Laguna XS:
+  // Q4_K gate/up, Q4_K or Q6_K down) run the shared expert on the GEMV kernels
+  const bool shared_q8 = Is == 0 || (sq == INFERNO_Q8_0 && sdq == INFERNO_Q8_0);
   size_t need = inferno_moe_layer_workspace_bytes(L, T);
   if (workspace_bytes < need) {
     set_error("workspace too small: need " + std::to_string(need) + " bytes");
@@ -517,7 +527,7 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
   // there the grouped MFMA GEMM reads each expert's weights once for all its
   // tokens (c4 at T = 32, 2.5 tokens per expert: 2.5 ms against 3.9 ms)
   const bool decode = decode_supported(T, k, E, H, I, Is, x_dtype, L->quant, L->down_quant) &&
-                      (T == 1 || !use_mfma(L->quant, L->down_quant, T, k, E, H, I));
+                      shared_q8 && (T == 1 || !use_mfma(L->quant, L->down_quant, T, k, E, H, I));
   if (decode) {
     DecodeArgs d{};
     d.T = int(T); d.H = int(H); d.E = int(E); d.I = int(I); d.k = int(k); d.Is = int(Is);
@@ -544,13 +554,30 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
   if ((st = launch_router_topk(s, w.logits, L->router_bias, T, E, k, L->score_fn,
                                L->norm_topk_prob, L->routed_scaling_factor, ids, wts, nullptr)))
     return st;
+  // shared expert on the GEMV kernels: gate/up from x staged in moe.stage_x
+  // (h staged for the down when its format has a packed-f16 kernel), down
+  // with the routed rows and the residual folded in
+  const bool sdq_staged = dot2_supported(sdq);
+  auto shared_gate_up_gemv = [&](bool staged_ready) {
+    return launch_gemv_gate_up_dense(s, sq, L->shared_gate, L->shared_up, x, x_dtype,
+                                     w.moe.stage_x, staged_ready, T, H, Is, w.hs,
+                                     sdq_staged ? w.stage_hs : nullptr);
+  };
+  auto shared_down_gemv = [&] {
+    return launch_gemv_down_dense(s, sdq, L->shared_down, w.hs, sdq_staged ? w.stage_hs : nullptr,
+                                  sdq_staged, w.moe.y, k, nullptr, residual, T, Is, H, out);
+  };
   if (use_mfma(L->quant, L->down_quant, T, k, E, H, I)) {
+    // a shared expert in another format than Q8_0 runs its gate/up first,
+    // while moe.stage_x still holds its staging (the f16 copy of x reuses it)
+    if (!shared_q8 && (st = shared_gate_up_gemv(false))) return st;
     // x in f16 once for the routed and the shared expert GEMMs
     uint16_t* x16 = reinterpret_cast<uint16_t*>(w.moe.stage_x);
     if ((st = launch_to_f16(s, x, x_dtype, T, H, x16))) return st;
     if ((st = run_routed(s, L->quant, L->down_quant, L->gate, L->up, L->down, x, x_dtype, ids,
                          wts, T, k, E, H, I, w.moe, false, x16)))
       return st;
+    if (!shared_q8) return shared_down_gemv();
     if (Is && (st = launch_prefill_dense(s, L->shared_gate, L->shared_up, L->shared_down, x16, T,
                                          H, Is, reinterpret_cast<uint16_t*>(w.hs), w.ys)))
       return st;
@@ -562,11 +589,8 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
                        T, k, E, H, I, w.moe, true)))
     return st;
   if (Is) {
-    if ((st = launch_gemv_gate_up_dense(s, INFERNO_Q8_0, L->shared_gate, L->shared_up, x, x_dtype,
-                                        w.moe.stage_x, true, T, H, Is, w.hs, w.stage_hs)))
-      return st;
-    return launch_gemv_down_dense(s, INFERNO_Q8_0, L->shared_down, w.hs, w.stage_hs, true,
-                                  w.moe.y, k, nullptr, residual, T, Is, H, out);
+    if ((st = shared_gate_up_gemv(true))) return st;
+    return shared_down_gemv();
   }
   return launch_topk_combine(s, nullptr, residual, w.moe.y, nullptr, T, H, k, out);
 }

@@ -273,6 +273,10 @@ def _q(t: TensorInfo):
     return t.ty
 
 
+_SHARED_GU = {GGML_Q8_0, GGML_Q2_K, GGML_Q3_K, GGML_Q4_K}
+_SHARED_DOWN = _SHARED_GU | {GGML_Q6_K}
+
+
 def packed_experts(g: GGUFFile, layer: int) -> PackedExperts:
     """``blk.{layer}.ffn_{gate,up,down}_exps.weight`` (index.rs:426-428) with
     their dims checked against each other (moe_ffn.rs:2385-2410)."""
@@ -297,8 +301,9 @@ def moe_layer_from_gguf(g: GGUFFile, layer: int, *, top_k: int, score_fn: int,
                         device="cuda", max_tokens=1):
     """An ``ops.MoELayer`` over layer ``layer``'s tensors, copied to ``device``:
     router ``ffn_gate_inp.weight`` (f32 [H, E]), optional correction bias
-    ``exp_probs_b.bias`` (f32 [E]), packed experts, optional Q8_0 shared
-    expert ``ffn_{gate,up,down}_shexp.weight`` (index.rs:417-429)."""
+    ``exp_probs_b.bias`` (f32 [E]), packed experts, optional shared
+    expert ``ffn_{gate,up,down}_shexp.weight`` (index.rs:417-429): Q8_0, or a
+    K-quant gate/up (Laguna XS: Q4_K) with a K-quant or Q8_0 down."""
     import torch
 
     from . import ops
@@ -326,11 +331,17 @@ def moe_layer_from_gguf(g: GGUFFile, layer: int, *, top_k: int, score_fn: int,
     if f"{p}.ffn_gate_shexp.weight" in g.tensors:
         sg, su, sd = (g.tensor(f"{p}.ffn_{m}_shexp.weight") for m in ("gate", "up", "down"))
         Is = int(sg.dims[1])
-        for t, want in ((sg, (H, Is)), (su, (H, Is)), (sd, (Is, H))):
-            if t.ty != GGML_Q8_0 or t.dims != want:
-                raise GGUFError(f"{t.name} must be Q8_0 {list(want)}, is type {t.ty} dims "
-                                f"{list(t.dims)}")
-        shared = dict(shared_gate=dev(sg.name), shared_up=dev(su.name), shared_down=dev(sd.name))
+        # Q8_0 (GLM, Laguna S) or Laguna XS's Q4_K gate/up with a K-quant down
+        # (crates/model/src/laguna/gguf_model.rs:829-849)
+        for t, want, kinds in ((sg, (H, Is), _SHARED_GU), (su, (H, Is), _SHARED_GU),
+                               (sd, (Is, H), _SHARED_DOWN)):
+            if t.ty not in kinds or t.dims != want:
+                raise GGUFError(f"{t.name} must be {list(want)} of type {sorted(kinds)}, is type "
+                                f"{t.ty} dims {list(t.dims)}")
+        if su.ty != sg.ty:
+            raise GGUFError(f"{su.name} type {su.ty} differs from {sg.name} type {sg.ty}")
+        shared = dict(shared_gate=dev(sg.name), shared_up=dev(su.name), shared_down=dev(sd.name),
+                      shared_quant=sg.ty, shared_down_quant=sd.ty)
     return ops.MoELayer(
         hidden=H, experts=E, intermediate=I, top_k=top_k, quant=px.gate.ty,
         down_quant=px.down.ty, score_fn=score_fn, norm_topk_prob=norm_topk_prob,

@@ -236,7 +236,7 @@ class MoELayer:
     def __init__(self, *, hidden, experts, intermediate, top_k, quant, down_quant, score_fn,
                  norm_topk_prob, routed_scaling_factor, router, router_bias, gate, up, down,
                  shared_intermediate=0, shared_gate=None, shared_up=None, shared_down=None,
-                 max_tokens=1):
+                 shared_quant=Q8_0, shared_down_quant=Q8_0, max_tokens=1):
         self.tensors = [router, router_bias, gate, up, down, shared_gate, shared_up, shared_down]
         d = LayerDesc()
         d.hidden, d.experts, d.intermediate, d.top_k = hidden, experts, intermediate, top_k
@@ -251,6 +251,7 @@ class MoELayer:
             d.shared_gate_bytes = shared_gate.numel()
             d.shared_up_bytes = shared_up.numel()
             d.shared_down_bytes = shared_down.numel()
+            d.shared_quant, d.shared_down_quant = shared_quant, shared_down_quant
         self.desc = d
         self.hidden, self.top_k = hidden, top_k
         self.device = gate.device

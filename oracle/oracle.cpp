@@ -552,28 +552,31 @@ int oracle_moe_routed(int quant, int down_quant, const uint8_t* gate, const uint
   return 0;
 }
 
-int oracle_shared_q8_0(const uint8_t* gate, const uint8_t* up, const uint8_t* down,
-                       const float* x, size_t T, size_t H, size_t Is, const float* routed,
-                       const float* residual, float* out, int threads) {
-  if (H % 32 || Is % 32) return -1;
-  const size_t grow = H / 32 * 34, drow = Is / 32 * 34;
+int oracle_shared_ffn(int quant, int down_quant, const uint8_t* gate, const uint8_t* up,
+                      const uint8_t* down, const float* x, size_t T, size_t H, size_t Is,
+                      const float* routed, const float* residual, float* out, int threads) {
+  const int gbv = oracle_block_values(quant), dbv = oracle_block_values(down_quant);
+  if (gbv < 0 || dbv < 0 || H % size_t(gbv) || Is % size_t(dbv)) return -1;
+  const size_t grow = H / size_t(gbv) * size_t(oracle_block_bytes(quant));
+  const size_t drow = Is / size_t(dbv) * size_t(oracle_block_bytes(down_quant));
   std::vector<float> hs(T * Is);
   std::vector<int> status(std::max(Is, H), 0);
-  // q2_kernels.metal:2133-2235 (Q8_0 gate/up SwiGLU, no routing weight); each
+  // q2_kernels.metal:2133-2235 (Q8_0 gate/up SwiGLU, no routing weight;
+  // Laguna XS: Q4_K gate/up, laguna_xs_kernels.metal:1922-1926); each
   // weight row dequantised once and dotted with every token
   Panel xp;
   xp.build(T, H, [&](size_t t) { return x + t * H; });
   parallel_for(Is, threads, [&](size_t b, size_t e) {
     std::vector<float> gv(H), uv(H), gs(T), us(T);
     for (size_t i = b; i < e; ++i) {
-      int st = dq_row(ORC_Q8_0, gate + i * grow, H, gv.data());
-      if (!st) st = dq_row(ORC_Q8_0, up + i * grow, H, uv.data());
+      int st = dq_row(quant, gate + i * grow, H, gv.data());
+      if (!st) st = dq_row(quant, up + i * grow, H, uv.data());
       if (st) {
         status[i] = st;
         continue;
       }
-      dot_panel(gv.data(), 1, 32, xp, gs.data());
-      dot_panel(uv.data(), 1, 32, xp, us.data());
+      dot_panel(gv.data(), 1, size_t(gbv), xp, gs.data());
+      dot_panel(uv.data(), 1, size_t(gbv), xp, us.data());
       for (size_t t = 0; t < T; ++t) hs[t * Is + i] = silu(gs[t]) * us[t];
     }
   });
@@ -585,12 +588,12 @@ int oracle_shared_q8_0(const uint8_t* gate, const uint8_t* up, const uint8_t* do
   parallel_for(H, threads, [&](size_t b, size_t e) {
     std::vector<float> dv(Is), r(T);
     for (size_t o = b; o < e; ++o) {
-      int st = dq_row(ORC_Q8_0, down + o * drow, Is, dv.data());
+      int st = dq_row(down_quant, down + o * drow, Is, dv.data());
       if (st) {
         status[o] = st;
         continue;
       }
-      dot_panel(dv.data(), 1, 32, hp, r.data());
+      dot_panel(dv.data(), 1, size_t(dbv), hp, r.data());
       for (size_t t = 0; t < T; ++t) {
         const size_t idx = t * H + o;
         float ra = routed ? routed[idx] : 0.0f, rb = residual ? residual[idx] : 0.0f;
@@ -601,6 +604,13 @@ int oracle_shared_q8_0(const uint8_t* gate, const uint8_t* up, const uint8_t* do
   for (size_t i = 0; i < H; ++i)
     if (status[i]) return status[i];
   return 0;
+}
+
+int oracle_shared_q8_0(const uint8_t* gate, const uint8_t* up, const uint8_t* down,
+                       const float* x, size_t T, size_t H, size_t Is, const float* routed,
+                       const float* residual, float* out, int threads) {
+  return oracle_shared_ffn(ORC_Q8_0, ORC_Q8_0, gate, up, down, x, T, H, Is, routed, residual, out,
+                           threads);
 }
 
 // crates/backend/src/backend.rs:10298-10352 (expert-major assignment order)

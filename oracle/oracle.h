@@ -77,6 +77,12 @@ int oracle_moe_routed(int quant, int down_quant, const uint8_t* gate, const uint
 
 /* Q8_0 shared expert: out[t,o] = routed[t,o] + residual[t,o] + W_d . (silu(W_g x) * (W_u x)).
  * routed/residual nullable (treated as zero). */
+// Shared expert of any gate/up and down format (Q8_0 for GLM / Laguna S;
+// Laguna XS: Q4_K gate/up, Q4_K or Q6_K down): out = routed + residual +
+// W_down (silu(W_gate x) * (W_up x)); routed / residual may be NULL.
+int oracle_shared_ffn(int quant, int down_quant, const uint8_t* gate, const uint8_t* up,
+                      const uint8_t* down, const float* x, size_t T, size_t H, size_t Is,
+                      const float* routed, const float* residual, float* out, int threads);
 int oracle_shared_q8_0(const uint8_t* gate, const uint8_t* up, const uint8_t* down,
                        const float* x, size_t T, size_t H, size_t Is, const float* routed,
                        const float* residual, float* out, int threads);

@@ -20,6 +20,7 @@ _SIG = {
     "oracle_moe_routed": (_i, [_i, _i, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp,
                                _vp, _i]),
     "oracle_shared_q8_0": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _i]),
+    "oracle_shared_ffn": (_i, [_i, _i, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _i]),
     "oracle_weighted_index_add_combine": (_i, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "oracle_rms_norm": (_i, [_vp, _vp, _sz, _sz, _f, _vp]),
 }
@@ -117,6 +118,19 @@ def shared_q8_0(gate, up, down, x, Is, routed=None, residual=None):
     gate, up, down = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
     _ok(L().oracle_shared_q8_0(_p(gate), _p(up), _p(down), _p(x), T, H, Is, _p(r), _p(s),
                                _p(out), THREADS), "shared_q8_0")
+    return out
+
+
+def shared_ffn(quant, down_quant, gate, up, down, x, Is, routed=None, residual=None):
+    """Shared expert of any format (Q8_0 GLM / Laguna S; Q4_K + Q4_K/Q6_K XS)."""
+    x = np.ascontiguousarray(x, np.float32)
+    T, H = x.shape
+    out = np.empty((T, H), np.float32)
+    r = None if routed is None else np.ascontiguousarray(routed, np.float32)
+    s = None if residual is None else np.ascontiguousarray(residual, np.float32)
+    gate, up, down = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
+    _ok(L().oracle_shared_ffn(quant, down_quant, _p(gate), _p(up), _p(down), _p(x), T, H, Is,
+                              _p(r), _p(s), _p(out), THREADS), "shared_ffn")
     return out
 
 

@@ -104,12 +104,14 @@ def oracle_layer_rows(cfg, lt, xs, res, ids_gpu_rows, bias_np=None, tie=NEAR_TIE
     remap = {int(e): i for i, e in enumerate(experts)}
     g, u, d = compact_experts(lt, cfg, torch.as_tensor(experts.astype(np.int64), device=lt.gate.device))
     ids_c = np.array([remap[int(e)] for e in ids_o], np.uint32)
-    routed = orc.moe_routed(lt.quant, lt.quant, g, u, d, xs, ids_c, w_o, len(experts), k,
+    dq = getattr(lt, "down_quant", 0) or lt.quant
+    routed = orc.moe_routed(lt.quant, dq, g, u, d, xs, ids_c, w_o, len(experts), k,
                             cfg.intermediate)
     if lt.shared is not None:
         sg, su, sd = (to_np(s) for s in lt.shared)
-        out = orc.shared_q8_0(sg, su, sd, xs, cfg.shared_intermediate, routed=routed,
-                              residual=res)
+        out = orc.shared_ffn(getattr(lt, "shared_quant", 8), getattr(lt, "shared_down_quant", 8),
+                             sg, su, sd, xs, cfg.shared_intermediate, routed=routed,
+                             residual=res)
     else:
         out = routed + (0 if res is None else res)
     return out, ids_o, w_o, flips

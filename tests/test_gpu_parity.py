@@ -431,6 +431,22 @@ def test_layer_runs_decode_shapes(cuda, quant, H, E, I, k, Is, dt):
     assert dn.startswith("runs-down:") or dn.startswith("mfma-down:"), dn
 
 
+# Laguna XS layer formats (crates/model/src/laguna/gguf_model.rs:808-860,
+# laguna_xs_gguf_moe_shared_device backend.rs:1754): routed Q4_K gate/up with
+# Q4_K or Q6_K down, shared expert Q4_K gate/up with the routed down format,
+# at c1's shape (H 2048, 64 experts, I 768, top-8 softmax, fp32 tokens),
+# one token (16 seeded inputs), 16 tokens, and 64 tokens (512 assignments:
+# the grouped GEMM path with the shared expert on the GEMV kernels).
+@pytest.mark.parametrize("down", [Q4_K, Q6_K])
+@pytest.mark.parametrize("T", [1, 16, 64])
+def test_layer_laguna_xs_q4k_shared(cuda, down, T):
+    c1 = cf.CONFIGS["c1"]
+    cfg = cf.Config(f"xs_q4k_down{down}", 60 + down, c1.hidden, c1.experts, c1.intermediate,
+                    c1.top_k, (Q4_K,), c1.score_fn, True, 1.0, 0.0, 1024, torch.float32, (T,),
+                    down_quant=down, shared_quant=Q4_K)
+    _layer_parity(cuda, cfg, T, variants=16 if T == 1 else 1)
+
+
 def test_layer_c3_glm_q3k_prefill_all_tokens(cuda):
     # every one of the 512 tokens, near-uniform expert load (~16 per expert)
     _layer_parity(cuda, "c3", 512)

@@ -269,6 +269,27 @@ def test_bf16_round_matches_torch_nearest_even():
     assert np.array_equal(ph.bf16_round(x).view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("sq,sdq", [(Q4_K, Q4_K), (Q4_K, Q6_K), (Q8_0, Q8_0)])
+def test_shared_ffn_matches_fp64(sq, sdq):
+    # the shared expert in the Laguna XS formats (Q4_K gate/up, Q4_K or Q6_K
+    # down) and Q8_0, against fp64 over the independently decoded weights
+    T, H, Is = 3, 512, 256
+    gb = 32 if sq == Q8_0 else 256
+    db = 32 if sdq == Q8_0 else 256
+    g = _random_blocks(sq, Is * H // gb)
+    u = _random_blocks(sq, Is * H // gb)
+    d = _random_blocks(sdq, H * Is // db)
+    x = (0.05 * rng.standard_normal((T, H))).astype(np.float32)
+    ra = rng.standard_normal((T, H)).astype(np.float32)
+    got = orc.shared_ffn(sq, sdq, g, u, d, x, Is, routed=ra)
+    x64 = x.astype(np.float64)
+    hs = rn.silu(x64 @ rn.dequant_matrix(sq, g, Is, H).T) * (x64 @ rn.dequant_matrix(sq, u, Is, H).T)
+    ref = ra + hs @ rn.dequant_matrix(sdq, d, H, Is).T
+    assert rn.rel_l2(got, ref) < 1e-5
+    if sq == Q8_0:  # the Q8_0 entry point is the same computation
+        assert np.array_equal(got, orc.shared_q8_0(g, u, d, x, Is, routed=ra))
+
+
 def test_oracle_batched_rows_match_per_token_calls():
     # the oracle dequantises each expert row once and dots it with all the
     # expert's tokens, four summation chains at a time; every token's result
