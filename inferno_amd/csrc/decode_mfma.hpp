@@ -10,15 +10,18 @@
 //     two bits of a nibble is the fp4 (e2m1) value q / 2, so one v_and_b32
 //     with 0x33333333 yields eight operand values (planes 0 and 2; after a
 //     shift by 2, planes 1 and 3).
-//   A (activations): row m of A is group m of the block (scale byte m,
-//     m = 8h + 2p + s), holding x only in the K positions of that group, so
-//     each group's 16-value dot product lands in its own row of C. x is two
-//     e4m3 terms (two MFMAs per B, E8M0 scales 2^e1 and 2^(e1 - 4)).
+//   A (activations): x is two e4m3 terms (E8M0 scales 2^e1 and 2^(e1 - 4)).
+//     In the MFMA of planes u, u + 2, row r of A is term r >> 3 of one of
+//     the 8 groups (scale bytes m = 8h + 2p + s) whose fields those planes
+//     hold, x only in the K positions of that group, so each (group, term)
+//     16-value dot product lands in its own row of C; the row's scale
+//     operand (one per lane, lane l for row l % 16, measured) is its term's.
 //   Operand K layout (gfx950, measured): A lane group qa holds k = 16 qa + t
 //     in bytes t < 16 and k = 64 + 16 qa + t in bytes 16 + t; B lane group q
 //     holds k = 32 q + nibble.
-//   C: lane (kq, n) holds groups 4kq .. 4kq + 3 of row n, whose scale bytes
-//     are the kq-th dword of the block's scales. The group scale and minimum
+//   C: lane (kq, n) holds term kq >> 1 of four groups of row n, all among
+//     groups 8 (kq & 1) .. + 7 (scale dwords 2 (kq & 1), + 1); the offset
+//     terms (minimum) enter once, on the term-0 lanes. The group scale and minimum
 //     enter with v_fma_mix: the 4-bit scale and min nibbles masked in place
 //     are f16 subnormals, so no byte-to-float conversion is needed.
 //
@@ -261,12 +264,21 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
       stage_run_lanes(silu(g) * u, p.stage_hs, p.Is, st);
     }
   }
-  // A operand (fp8 x): the group m of this lane's row sits in MFMA u =
-  // p(m) & 1 (the field planes 0, 2 or 1, 3 in B), in the two lanes whose K
-  // range covers B's lane group 2 (m >> 3) + (m & 1): kq >> 1 == m & 1, in
-  // operand bytes 16..31 for m >= 8; every other lane/MFMA reads zeros.
+  // A operand (fp8 x) of MFMA u (planes u, u + 2): row r holds term r >> 3
+  // of group g(j, u), j = r & 7 (g = 8 (j >> 2) + 4 ((j >> 1) & 1) + 2 u +
+  // (j & 1)), in the two lanes whose K range covers B's lane group
+  // 2 (g >> 3) + (g & 1): kq >> 1 == j & 1, in operand bytes 16..31 for
+  // g >= 8; every other lane reads zeros. The row's E8M0 scale (one per
+  // lane, for row n) is that of its term, so both terms of a group land in
+  // C already scaled and the final sum over lane groups adds them.
   const bool act = (q >> 1) == (n & 1);
-  const int uact = (n >> 1) & 1, hi16 = n >> 3;
+  const int hi16 = (n >> 2) & 1, tmA = n >> 3;
+  const int gA = 8 * ((n >> 2) & 1) + 4 * ((n >> 1) & 1) + (n & 1);  // g(j, 0); + 2 u
+  // C: lane (kq, n) holds rows 4 kq + i of weight row n: term kq >> 1 of
+  // groups 8 (kq & 1) + 4 (i >> 1) + 2 u + (i & 1); the offset terms (min,
+  // Q3_K's -4) enter once, on the term-0 lanes
+  const int hq = q & 1;
+  const bool term0 = q < 2;
   const float* sums = reinterpret_cast<const float*>(xs + H);
   const int* e1s = reinterpret_cast<const int*>(xs + H + H / 16);
   for (; t < ntiles; t += gridDim.x) {
@@ -284,22 +296,21 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
     const int slot = t / tiles_i, tile = t - slot * tiles_i;
     float acc[2] = {0.f, 0.f};
     for (int c = wave; c < NB; c += kWaves) {
-      const uint32_t* img = xs + c * 256 + n * 8 + (q & 1) * 4;
-      v8i A[2][2];  // [term][u]
+      v8i A[2];  // [u]
 #pragma unroll
-      for (int tm = 0; tm < 2; ++tm)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const bool on = act && u == uact;
-          const uint32_t* lo = (on && !hi16) ? img + tm * 128 : zero;
-          const uint32_t* hi = (on && hi16) ? img + tm * 128 : zero;
-          const uint4 a0 = *reinterpret_cast<const uint4*>(lo);
-          const uint4 a1 = *reinterpret_cast<const uint4*>(hi);
-          A[tm][u] = v8i{int(a0.x), int(a0.y), int(a0.z), int(a0.w),
-                         int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
-        }
-      const float4 xsum = *reinterpret_cast<const float4*>(sums + c * 16 + 4 * q);
-      const int sa1 = 127 + e1s[c], sa2 = sa1 - 4;  // E8M0 scales of the two x terms
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t* img = xs + c * 256 + (gA + 2 * u) * 8 + (q & 1) * 4 + tmA * 128;
+        const uint32_t* lo = (act && !hi16) ? img : zero;
+        const uint32_t* hi = (act && hi16) ? img : zero;
+        const uint4 a0 = *reinterpret_cast<const uint4*>(lo);
+        const uint4 a1 = *reinterpret_cast<const uint4*>(hi);
+        A[u] = v8i{int(a0.x), int(a0.y), int(a0.z), int(a0.w),
+                   int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
+      }
+      // x sums of this lane's groups 8 hq + 0..7
+      const float4 xa = *reinterpret_cast<const float4*>(sums + c * 16 + 8 * hq);
+      const float4 xb = *reinterpret_cast<const float4*>(sums + c * 16 + 8 * hq + 4);
+      const int sa = 127 + e1s[c] - 4 * tmA;  // E8M0 scale of this lane's A row's term
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const uint8_t* blk = tl + (m * 16 + n) * RS + c * kB;
@@ -307,7 +318,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
         // e2m1 value q / 2; planes 0 (low nibble) and 2 (high nibble) in
         // MFMA 0, planes 1 and 3 in MFMA 1
         const uint32_t F = 0x33333333u;
-        floatx4 C = {0.f, 0.f, 0.f, 0.f};
+        floatx4 C0 = {0.f, 0.f, 0.f, 0.f}, C1 = C0;
         if constexpr (Q == INFERNO_Q3_K) {
           const u32x4_a2 qs = *reinterpret_cast<const u32x4_a2*>(blk + 32 + 16 * q);
           const u32x4_a2 hm = *reinterpret_cast<const u32x4_a2*>(blk + 16 * (q & 1));
@@ -326,58 +337,74 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
                              int(((x1 >> 1) & L) | ((x1 << 1) & U)),
                              int(((x2 >> 1) & L) | ((x2 << 1) & U)),
                              int(((x3 >> 1) & L) | ((x3 << 1) & U)), 0, 0, 0, 0};
-          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][0], B0, C, 0, 4, 0, sa1, 0, 127);
-          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][1], B1, C, 0, 4, 0, sa1, 0, 127);
-          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][0], B0, C, 0, 4, 0, sa2, 0, 127);
-          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][1], B1, C, 0, 4, 0, sa2, 0, 127);
-          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][0], H0, C, 0, 4, 0, sa1 + 2, 0, 127);
-          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][1], H1, C, 0, 4, 0, sa1 + 2, 0, 127);
-          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][0], H0, C, 0, 4, 0, sa2 + 2, 0, 127);
-          C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][1], H1, C, 0, 4, 0, sa2 + 2, 0, 127);
-          // groups 4 q + j: 6-bit scale = low nibble of scales[(4 q + j) % 8]
-          // (high nibble for q >= 2) | high two bits of scales[8 + j] at bit 2 q
-          const uint32_t lo = *reinterpret_cast<const u32_a2*>(blk + 96 + 4 * (q & 1));
-          const uint32_t hi = *reinterpret_cast<const u32_a2*>(blk + 104);
-          const uint32_t s6 = ((lo >> (4 * (q >> 1))) & 0x0f0f0f0fu) |
-                              (((hi >> (2 * q)) & 0x03030303u) << 4);
+          C0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0], B0, C0, 0, 4, 0, sa, 0, 127);
+          C1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1], B1, C1, 0, 4, 0, sa, 0, 127);
+          C0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0], H0, C0, 0, 4, 0, sa + 2, 0, 127);
+          C1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1], H1, C1, 0, 4, 0, sa + 2, 0, 127);
+          // group 8 hq + k: 6-bit scale = nibble hq of scales[k] | bits
+          // 2 (2 hq + k / 4) .. + 1 of scales[8 + k % 4] at bit 4
+          const uint32_t l0 = *reinterpret_cast<const u32_a2*>(blk + 96);
+          const uint32_t l1 = *reinterpret_cast<const u32_a2*>(blk + 100);
+          const uint32_t hb = *reinterpret_cast<const u32_a2*>(blk + 104);
+          const uint32_t s6a = ((l0 >> (4 * hq)) & 0x0f0f0f0fu) | (((hb >> (4 * hq)) & 0x03030303u) << 4);
+          const uint32_t s6b = ((l1 >> (4 * hq)) & 0x0f0f0f0fu) | (((hb >> (4 * hq + 2)) & 0x03030303u) << 4);
           const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 108));
-          const float xs4[4] = {xsum.x, xsum.y, xsum.z, xsum.w};
-          float t = 0.f;
+          // C_u[i] is group k = 4 (i >> 1) + 2 u + (i & 1): bytes 2 u + (i & 1)
+          // of s6a (i < 2) or s6b
+          const float xsv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+          const float off = term0 ? -4.0f : 0.f;
+          float tt = 0.f;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float gs = float(int((s6 >> (8 * j)) & 0xffu) - 32);
-            t = fmaf(gs, fmaf(2.0f, C[j], -4.0f * xs4[j]), t);
-          }
-          acc[m] = fmaf(d, t, acc[m]);
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int k = 4 * (i >> 1) + 2 * u + (i & 1);
+              const uint32_t sw = (i < 2) ? s6a : s6b;
+              const float gs = float(int((sw >> (8 * (2 * u + (i & 1)))) & 0xffu) - 32);
+              const float cv = u ? C1[i] : C0[i];
+              tt = fmaf(gs, fmaf(2.0f, cv, off * xsv[k]), tt);
+            }
+          acc[m] = fmaf(d, tt, acc[m]);
           continue;
         }
         const u32x4_a4 qs = *reinterpret_cast<const u32x4_a4*>(blk + 16 + 16 * q);
-        const uint32_t scw = *reinterpret_cast<const uint32_t*>(blk + 4 * q);
+        const uint32_t sw0 = *reinterpret_cast<const uint32_t*>(blk + 8 * hq);
+        const uint32_t sw1 = *reinterpret_cast<const uint32_t*>(blk + 8 * hq + 4);
         const uint32_t dmw = *reinterpret_cast<const uint32_t*>(blk + 80);
         const v8i B0 = v8i{int(qs.x & F), int(qs.y & F), int(qs.z & F), int(qs.w & F), 0, 0, 0, 0};
         const v8i B1 = v8i{int((qs.x >> 2) & F), int((qs.y >> 2) & F), int((qs.z >> 2) & F),
                            int((qs.w >> 2) & F), 0, 0, 0, 0};
-        C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][0], B0, C, 0, 4, 0, sa1, 0, 127);
-        C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0][1], B1, C, 0, 4, 0, sa1, 0, 127);
-        C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][0], B0, C, 0, 4, 0, sa2, 0, 127);
-        C = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1][1], B1, C, 0, 4, 0, sa2, 0, 127);
-        // scale nibbles (bytes 0, 2 | 1, 3) and min nibbles as f16 subnormal pairs
-        const uint32_t sh = scw >> 8;
-        const half2v s02 = as_h2(scw & 0x000f000fu), s13 = as_h2(sh & 0x000f000fu);
-        const half2v m02 = as_h2(scw & 0x00f000f0u), m13 = as_h2(sh & 0x00f000f0u);
+        C0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[0], B0, C0, 0, 4, 0, sa, 0, 127);
+        C1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1], B1, C1, 0, 4, 0, sa, 0, 127);
+        // scale nibbles and min nibbles of groups 8 hq + k as f16 subnormal
+        // pairs: bytes (0, 2) and (1, 3) of scale dwords 2 hq (k < 4) and
+        // 2 hq + 1; C_u[i] is group k = 4 (i >> 1) + 2 u + (i & 1)
+        const uint32_t sh0 = sw0 >> 8, sh1 = sw1 >> 8;
+        const half2v a02 = as_h2(sw0 & 0x000f000fu), a13 = as_h2(sh0 & 0x000f000fu);
+        const half2v b02 = as_h2(sw1 & 0x000f000fu), b13 = as_h2(sh1 & 0x000f000fu);
+        const half2v ma02 = as_h2(sw0 & 0x00f000f0u), ma13 = as_h2(sh0 & 0x00f000f0u);
+        const half2v mb02 = as_h2(sw1 & 0x00f000f0u), mb13 = as_h2(sh1 & 0x00f000f0u);
         const half2v dm = as_h2(dmw);
-        float S = fmaf((float)s02.x, C[0], 0.f);
-        S = fmaf((float)s13.x, C[1], S);
-        S = fmaf((float)s02.y, C[2], S);
-        S = fmaf((float)s13.y, C[3], S);
-        float Mn = fmaf((float)m02.x, xsum.x, 0.f);
-        Mn = fmaf((float)m13.x, xsum.y, Mn);
-        Mn = fmaf((float)m02.y, xsum.z, Mn);
-        Mn = fmaf((float)m13.y, xsum.w, Mn);
+        float S = fmaf((float)a02.x, C0[0], 0.f);
+        S = fmaf((float)a13.x, C0[1], S);
+        S = fmaf((float)b02.x, C0[2], S);
+        S = fmaf((float)b13.x, C0[3], S);
+        S = fmaf((float)a02.y, C1[0], S);
+        S = fmaf((float)a13.y, C1[1], S);
+        S = fmaf((float)b02.y, C1[2], S);
+        S = fmaf((float)b13.y, C1[3], S);
+        float Mn = fmaf((float)ma02.x, xa.x, 0.f);
+        Mn = fmaf((float)ma13.x, xa.y, Mn);
+        Mn = fmaf((float)ma02.y, xa.z, Mn);
+        Mn = fmaf((float)ma13.y, xa.w, Mn);
+        Mn = fmaf((float)mb02.x, xb.x, Mn);
+        Mn = fmaf((float)mb13.x, xb.y, Mn);
+        Mn = fmaf((float)mb02.y, xb.z, Mn);
+        Mn = fmaf((float)mb13.y, xb.w, Mn);
         // value = d * sc * q - dmin * m: C holds sum (q / 2) x, S carries
         // 2^-24 (the scale nibble), Mn 2^-20 (the min nibble)
         acc[m] = fmaf((float)dm.x * 33554432.0f, S, acc[m]);
-        acc[m] = fmaf(-(float)dm.y * 1048576.0f, Mn, acc[m]);
+        acc[m] = fmaf(term0 ? -(float)dm.y * 1048576.0f : 0.f, Mn, acc[m]);
       }
     }
 #pragma unroll
