@@ -193,7 +193,7 @@ def main():
             "gate_up": {"label": labels[ops.TIMER_GATE_UP], "launch_us": gu_us,
                         "bytes_per_launch": gu_routed + (shared_gu if gu_kind in ("tiles", "ring") else 0),
                         "routed_bytes_per_launch": gu_routed,
-                        "traffic_file": {"mfma": "gate_up_mfma_q2k_c2_decode_traffic.txt",
+                        "traffic_file": {"mfma": "gate_up_fp4_q2k_c2_decode_traffic.txt",
                                          "tiles": "gate_up_q2k_c2_decode_traffic.txt"}.get(gu_kind)},
             "down": {"label": labels[ops.TIMER_DOWN], "launch_us": dn_us,
                      "bytes_per_launch": dn_routed + (shared_dn if dn_kind == "down8" else 0),

@@ -131,10 +131,10 @@ int run_routed(hipStream_t s, int quant, int down_quant, const void* gate, const
     }
     PrefillRouted p{quant, down_quant, gate, up, down, x16, m.offsets, m.sorted, m.active, w,
                     T, k, E, H, I, reinterpret_cast<uint16_t*>(m.h), m.y, m.plan};
-    if ((st = timed(s, kTimerGateUp, "prefill: gemm_kernel (routed gate/up, MFMA)",
+    if ((st = timed(s, kTimerGateUp, "prefill: grouped gate/up GEMMs (gemm_kernel / gemm2_kernel, MFMA)",
                     [&] { return launch_prefill_gate_up(s, p); })))
       return st;
-    return timed(s, kTimerDown, "prefill: gemm_kernel (routed down, MFMA)",
+    return timed(s, kTimerDown, "prefill: grouped down GEMMs (gemm_kernel / gemm2_kernel, MFMA)",
                  [&] { return launch_prefill_down(s, p); });
   }
   // gate/up writes h already staged for the down pass (when the down kind has a
