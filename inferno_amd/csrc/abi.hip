@@ -548,6 +548,7 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
     d.stage_xr = w.stage_xr;
     d.shared_gu = w.shared_gu;
     d.ys = w.ys;
+    d.y = w.moe.y;
     return launch_decode_layer(s, d, L->quant);
   }
   if ((st = launch_router_logits(s, x, x_dtype, L->router, T, H, E, w.logits))) return st;

@@ -23,6 +23,7 @@
 
 #include <cstdlib>
 #include "timing.hpp"
+#include "kernels.hpp"
 #include "dot2_formats.hpp"
 #include "routing_dev.hpp"
 
@@ -99,20 +100,20 @@ __global__ void __launch_bounds__(256) route_kernel(DecodeArgs p, int gx, int gy
       stage_run<kSplit>(v, p.stage_x + size_t(t) * staged_stride(H, kSplit), H, run);
     }
   }
-  // staging for the runs gate/up (bf16 tokens): a 16-lane group per 16-value
-  // run, scaled for the field offsets of format xr_quant (decode_runs.hpp)
-  if constexpr (std::is_same<XT, uint16_t>::value) {
-    if (p.stage_xr) {
-      const int runs = H / 16, run_id = (g * 256 + tid) >> 4;
-      if (run_id < T * runs) {  // uniform per 16-lane group
-        const int t = run_id / runs, run = run_id % runs;
-        const float v = to_f32(static_cast<const XT*>(p.x)[size_t(t) * H + run * 16 + (tid & 15)]);
-        const int r16 = run & 15;
-        const int shift = p.xr_quant == INFERNO_Q4_K ? runs_decode::RF<INFERNO_Q4_K>::run_shift(r16)
-                                                     : runs_decode::RF<INFERNO_Q2_K>::run_shift(r16);
-        runs_decode::stage_run16(v, p.stage_xr + size_t(t) * runs_decode::run_words(H), H, run,
-                                 shift);
-      }
+  // staging for the run gate/up kernels: a 16-lane group per 16-value run,
+  // scaled for the field offsets of format xr_quant (decode_runs.hpp); fp32
+  // tokens get the second (lo) f16 term
+  if (p.stage_xr) {
+    constexpr bool kSplit = !std::is_same<XT, uint16_t>::value;
+    const int runs = H / 16, run_id = (g * 256 + tid) >> 4;
+    if (run_id < T * runs) {  // uniform per 16-lane group
+      const int t = run_id / runs, run = run_id % runs;
+      const float v = to_f32(static_cast<const XT*>(p.x)[size_t(t) * H + run * 16 + (tid & 15)]);
+      const int r16 = run & 15;
+      const int shift = p.xr_quant == INFERNO_Q4_K ? runs_decode::RF<INFERNO_Q4_K>::run_shift(r16)
+                                                   : runs_decode::RF<INFERNO_Q2_K>::run_shift(r16);
+      runs_decode::stage_run16<kSplit>(
+          v, p.stage_xr + size_t(t) * runs_decode::xrun_words(H, kSplit), H, run, shift);
     }
   }
   // staging for the MFMA gate/up: one wavefront per 256-value column
@@ -765,13 +766,17 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
                         (a.Is == 0 || a.shared_gu != nullptr) && a.stage_xr != nullptr &&
                         a.I % kRows == 0 && runs_gate_up_covers(quant, a.H, a.x_dtype) &&
                         runs_down_covers(quant, a.H, a.I, a.k);
+  // several tokens, no shared expert: the run kernels grouped by expert
+  const bool use_multi = !use_fp4 && !use_runs && mfma_enabled() && a.T > 1 && a.Is == 0 &&
+                         a.y != nullptr && a.stage_xr != nullptr && a.I % kRows == 0 &&
+                         runs_multi_covers(quant, a.H, a.I, a.x_dtype);
   const bool use_mfma = use_fp4 || use_runs;
   // with a matrix-core gate/up the shared expert's gate/up runs in the route
   // launch and stages its own x; otherwise x is staged for the tile kernels
   a.shared_parts = shared_parts(a.H);
-  if (use_mfma) a.stage_x = nullptr;
+  if (use_mfma || use_multi) a.stage_x = nullptr;
   if (!use_fp4) a.stage_xm = nullptr;
-  if (!use_runs) a.stage_xr = nullptr;
+  if (!use_runs && !use_multi) a.stage_xr = nullptr;
   a.xr_quant = quant;
   // down after a matrix-core gate/up (h in the run layout): the Q2_K kernel
   // (I = 2048, k <= 8) or the run kernel; the shared down then runs in the
@@ -782,7 +787,7 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   const bool use_runs_down = !use_q2k_down && use_mfma && shared_down_ok &&
                              runs_down_covers(quant, a.H, a.I, a.k);
   const bool use_mfma_down = use_q2k_down || use_runs_down;
-  a.h_mfma = use_mfma_down ? 1 : 0;
+  a.h_mfma = (use_mfma_down || use_multi) ? 1 : 0;
   // the shared down output ys exists only with a shared expert on that path
   if (!use_mfma_down || a.Is == 0) a.ys = nullptr;
   if (!decode_supported(a.T, a.k, a.E, a.H, a.I, a.Is, a.x_dtype, quant, quant)) {
@@ -836,10 +841,12 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   const char* gu_label =
       use_fp4 ? "mfma: gate_up_fp4_kernel (routed tiles on fp8 x fp4 MFMA; shared gate/up in the route launch)"
       : use_runs ? "runs: gate_up_runs_kernel (routed tiles on f16 MFMA; shared gate/up in the route launch)"
-                 : "tiles: gate_up_kernel (routed + Q8_0 shared tiles)";
+      : use_multi ? "runs-multi: gate_up_runs_multi_kernel (each expert's routed tiles for all its tokens on f16 MFMA)"
+                  : "tiles: gate_up_kernel (routed + Q8_0 shared tiles)";
   int st = timed(s, kTimerGateUp, gu_label, [&]() -> int {
     if (use_fp4) return launch_gate_up_mfma(s, a, quant);
     if (use_runs) return launch_gate_up_runs(s, a, quant);
+    if (use_multi) return launch_gate_up_runs_multi(s, a, quant);
     switch (quant) {
       case INFERNO_Q2_K: xsplit ? launch_gate_up<INFERNO_Q2_K, true>(s, a) : launch_gate_up<INFERNO_Q2_K, false>(s, a); break;
       case INFERNO_Q3_K: xsplit ? launch_gate_up<INFERNO_Q3_K, true>(s, a) : launch_gate_up<INFERNO_Q3_K, false>(s, a); break;
@@ -854,6 +861,15 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
                  "mfma-down: down_q2k_kernel (routed Q2_K down on MFMA + combine; shared down "
                  "in the select launch)",
                  [&] { return launch_down_mfma(s, a); });
+  if (use_multi)
+    return timed(s, kTimerDown,
+                 "runs-multi-down: down_runs_multi_kernel (each expert's down rows for all its "
+                 "tokens on f16 MFMA) + combine_kernel (residual + ranks in order)",
+                 [&] {
+                   if (int st2 = launch_down_runs_multi(s, a, quant)) return st2;
+                   return launch_topk_combine(s, nullptr, a.residual, a.y, nullptr, size_t(a.T),
+                                              size_t(a.H), size_t(a.k), a.out);
+                 });
   if (use_runs_down)
     return timed(s, kTimerDown,
                  "runs-down: down_runs_kernel (routed down on f16 MFMA + combine; shared down "

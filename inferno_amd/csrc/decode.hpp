@@ -41,6 +41,7 @@ struct DecodeArgs {
   float* shared_gu;       // [shared_parts][2][Is]: shared gate/up partial sums (MFMA path, T = 1)
   int shared_parts;       // K parts of the shared gate/up in the route launch
   float* ys;              // [T, H]: shared down output (MFMA down path)
+  float* y;               // [T*k, H]: down rows per assignment (several-token run kernels)
   int h_mfma;             // gate/up writes h in the MFMA down layout
   // filled by launch_decode_layer
   int chunk, n_chunks, max_slots, routed_tiles;
@@ -64,6 +65,11 @@ bool runs_gate_up_covers(int quant, int H, int x_dtype);
 bool runs_down_covers(int quant, int H, int I, int k);
 int launch_gate_up_runs(hipStream_t s, const DecodeArgs& a, int quant);
 int launch_down_runs(hipStream_t s, const DecodeArgs& a, int quant);
+// The same kernels for T > 1 tokens (no shared expert): gate/up per expert
+// tile for all of the expert's tokens, down rows per assignment into a.y.
+bool runs_multi_covers(int quant, int H, int I, int x_dtype);
+int launch_gate_up_runs_multi(hipStream_t s, const DecodeArgs& a, int quant);
+int launch_down_runs_multi(hipStream_t s, const DecodeArgs& a, int quant);
 
 
 }  // namespace inferno

@@ -131,7 +131,7 @@ bool down_fits(int NB, int k) {
 
 }  // namespace
 
-size_t decode_runs_stage_words(size_t H) { return size_t(run_words(int(H))); }
+size_t decode_runs_stage_words(size_t H) { return size_t(xrun_words(int(H), true)); }
 
 bool runs_gate_up_covers(int quant, int H, int x_dtype) {
   if (H % kKBlock || x_dtype != INFERNO_BF16) return false;
@@ -170,6 +170,139 @@ int launch_down_runs(hipStream_t s, const DecodeArgs& a, int quant) {
     case INFERNO_Q2_K: return down_q<INFERNO_Q2_K>(s, a);
     case INFERNO_Q3_K: return down_q<INFERNO_Q3_K>(s, a);
     default: return down_q<INFERNO_Q4_K>(s, a);
+  }
+}
+
+// ------------------------------------------------- several tokens (T > 1)
+
+namespace {
+
+// Tokens per LDS pass of the gate/up: the most (8, 4 or 2) whose staged rows
+// fit beside the tile.
+template <int Q, int NB, bool SPLIT>
+constexpr int multi_nt() {
+  return gate_up_multi_lds<Q, NB, SPLIT, 8>() <= kLdsMax   ? 8
+         : gate_up_multi_lds<Q, NB, SPLIT, 4>() <= kLdsMax ? 4
+                                                           : 2;
+}
+
+// Down row groups per tile: 128, 64, 32 or 16 rows, the most whose weights
+// stay within 56 KB (H is a multiple of 256, so every choice divides it).
+template <int Q, int NB>
+constexpr int multi_rg() {
+  constexpr int rb = NB * RF<Q>::kBytes;
+  return 128 * rb <= 56 * 1024 ? 8 : 64 * rb <= 56 * 1024 ? 4 : 32 * rb <= 56 * 1024 ? 2 : 1;
+}
+constexpr int kDownNT = 8;
+
+template <int Q, int NB, bool SPLIT>
+int gate_up_multi_nb(hipStream_t s, const DecodeArgs& a) {
+  constexpr int NT = multi_nt<Q, NB, SPLIT>();
+  static bool attr = false;
+  auto* kern = gate_up_runs_multi_kernel<Q, NB, SPLIT, NT>;
+  if (int st = allow_lds(kern, attr)) return st;
+  const int ntiles = a.max_slots * (a.I / kRows);  // upper bound: active slots <= max_slots
+  const unsigned grid = unsigned(std::min(ntiles, cus_now()));
+  kern<<<grid, kThreads, gate_up_multi_lds<Q, NB, SPLIT, NT>(), s>>>(a);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+template <int Q, bool SPLIT>
+int gate_up_multi_q(hipStream_t s, const DecodeArgs& a) {
+  switch (a.H / kKBlock) {
+    case 4: return gate_up_multi_nb<Q, 4, SPLIT>(s, a);
+    case 8: return gate_up_multi_nb<Q, 8, SPLIT>(s, a);
+    case 12: return gate_up_multi_nb<Q, 12, SPLIT>(s, a);
+    case 16: return gate_up_multi_nb<Q, 16, SPLIT>(s, a);
+    default: return gate_up_multi_nb<Q, 24, SPLIT>(s, a);
+  }
+}
+
+template <int Q, bool SPLIT>
+size_t gate_up_multi_lds_q(int NB) {
+  switch (NB) {
+    case 4: return gate_up_multi_lds<Q, 4, SPLIT, multi_nt<Q, 4, SPLIT>()>();
+    case 8: return gate_up_multi_lds<Q, 8, SPLIT, multi_nt<Q, 8, SPLIT>()>();
+    case 12: return gate_up_multi_lds<Q, 12, SPLIT, multi_nt<Q, 12, SPLIT>()>();
+    case 16: return gate_up_multi_lds<Q, 16, SPLIT, multi_nt<Q, 16, SPLIT>()>();
+    case 24: return gate_up_multi_lds<Q, 24, SPLIT, multi_nt<Q, 24, SPLIT>()>();
+    default: return ~size_t(0);
+  }
+}
+
+template <int Q, int NB>
+int down_multi_nb(hipStream_t s, const DecodeArgs& a) {
+  constexpr int RG = multi_rg<Q, NB>();
+  static bool attr = false;
+  auto* kern = down_runs_multi_kernel<Q, NB, RG, kDownNT>;
+  if (int st = allow_lds(kern, attr)) return st;
+  const int ntiles = a.max_slots * (a.H / (16 * RG));
+  const unsigned grid = unsigned(std::min(ntiles, cus_now()));
+  kern<<<grid, kThreads, down_multi_lds<Q, NB, RG, kDownNT>(), s>>>(a);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+template <int Q>
+int down_multi_q(hipStream_t s, const DecodeArgs& a) {
+  switch (a.I / kKBlock) {
+    case 3: return down_multi_nb<Q, 3>(s, a);
+    case 4: return down_multi_nb<Q, 4>(s, a);
+    case 6: return down_multi_nb<Q, 6>(s, a);
+    default: return down_multi_nb<Q, 8>(s, a);
+  }
+}
+
+template <int Q>
+size_t down_multi_lds_q(int NB) {
+  switch (NB) {
+    case 3: return down_multi_lds<Q, 3, multi_rg<Q, 3>(), kDownNT>();
+    case 4: return down_multi_lds<Q, 4, multi_rg<Q, 4>(), kDownNT>();
+    case 6: return down_multi_lds<Q, 6, multi_rg<Q, 6>(), kDownNT>();
+    case 8: return down_multi_lds<Q, 8, multi_rg<Q, 8>(), kDownNT>();
+    default: return ~size_t(0);
+  }
+}
+
+template <int Q>
+bool multi_covers_q(int H, int I, bool split) {
+  const int NB = H / kKBlock, NBI = I / kKBlock;
+  const size_t gu = split ? gate_up_multi_lds_q<Q, true>(NB) : gate_up_multi_lds_q<Q, false>(NB);
+  return gu <= kLdsMax && down_multi_lds_q<Q>(NBI) <= kLdsMax;
+}
+
+}  // namespace
+
+bool runs_multi_covers(int quant, int H, int I, int x_dtype) {
+  if (H % kKBlock || I % kKBlock || H % 128 || cus_now() <= 0) return false;
+  if (x_dtype != INFERNO_BF16 && x_dtype != INFERNO_F32) return false;
+  const bool split = x_dtype == INFERNO_F32;
+  switch (quant) {
+    case INFERNO_Q2_K: return multi_covers_q<INFERNO_Q2_K>(H, I, split);
+    case INFERNO_Q3_K: return multi_covers_q<INFERNO_Q3_K>(H, I, split);
+    case INFERNO_Q4_K: return multi_covers_q<INFERNO_Q4_K>(H, I, split);
+    default: return false;
+  }
+}
+
+int launch_gate_up_runs_multi(hipStream_t s, const DecodeArgs& a, int quant) {
+  const bool split = a.x_dtype == INFERNO_F32;
+  switch (quant) {
+    case INFERNO_Q2_K:
+      return split ? gate_up_multi_q<INFERNO_Q2_K, true>(s, a) : gate_up_multi_q<INFERNO_Q2_K, false>(s, a);
+    case INFERNO_Q3_K:
+      return split ? gate_up_multi_q<INFERNO_Q3_K, true>(s, a) : gate_up_multi_q<INFERNO_Q3_K, false>(s, a);
+    default:
+      return split ? gate_up_multi_q<INFERNO_Q4_K, true>(s, a) : gate_up_multi_q<INFERNO_Q4_K, false>(s, a);
+  }
+}
+
+int launch_down_runs_multi(hipStream_t s, const DecodeArgs& a, int quant) {
+  switch (quant) {
+    case INFERNO_Q2_K: return down_multi_q<INFERNO_Q2_K>(s, a);
+    case INFERNO_Q3_K: return down_multi_q<INFERNO_Q3_K>(s, a);
+    default: return down_multi_q<INFERNO_Q4_K>(s, a);
   }
 }
 

@@ -213,19 +213,26 @@ struct RF<INFERNO_Q4_K> {
   __device__ static float epilogue(const uint8_t* blk, floatx4 C, float4 sums, float4 kk,
                                    int q) {
     // runs 4 q + j: groups 2 q (j < 2) and 2 q + 1 (j >= 2); 6-bit scale and
-    // min of group g (crates/gguf/src/lib.rs:1407-1416)
-    const uint8_t* sb = blk + 4;
+    // min of group g (crates/gguf/src/lib.rs:1407-1416), from the 12 scale
+    // bytes read as three dwords
+    const uint32_t w0 = *reinterpret_cast<const u32_a2*>(blk + 4);
+    const uint32_t w1 = *reinterpret_cast<const u32_a2*>(blk + 8);
+    const uint32_t w2 = *reinterpret_cast<const u32_a2*>(blk + 12);
+    auto sb = [&](int i) -> uint32_t {
+      const uint32_t w = i < 4 ? w0 : (i < 8 ? w1 : w2);
+      return (w >> (8 * (i & 3))) & 0xffu;
+    };
     float sc[2], mn[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int g = 2 * q + k;
       uint32_t s, m;
       if (g < 4) {
-        s = sb[g] & 63u;
-        m = sb[g + 4] & 63u;
+        s = sb(g) & 63u;
+        m = sb(g + 4) & 63u;
       } else {
-        s = (sb[g + 4] & 15u) | ((uint32_t(sb[g - 4]) >> 6) << 4);
-        m = (uint32_t(sb[g + 4]) >> 4) | ((uint32_t(sb[g]) >> 6) << 4);
+        s = (sb(g + 4) & 15u) | ((sb(g - 4) >> 6) << 4);
+        m = (sb(g + 4) >> 4) | ((sb(g) >> 6) << 4);
       }
       sc[k] = float(s);
       mn[k] = float(m);
@@ -240,9 +247,21 @@ struct RF<INFERNO_Q4_K> {
 
 // ------------------------------------------------------------- staging
 
+// Words per staged x row: one f16 term (bf16 tokens), or two (fp32 tokens:
+// the hi pairs, run sums and factors as above, then the lo pairs K/2).
+__host__ __device__ constexpr int xrun_words(int K, bool split) {
+  return run_words(K) + (split ? K / 2 : 0);
+}
+// Word offset of the lo pairs in a split row.
+__host__ __device__ constexpr int xrun_lo(int K) { return run_words(K); }
+// The lo term carries (v - hi) 2^11, so the products of one run add up as
+// C_hi + 2^-11 C_lo: about 22 significant bits of each fp32 value.
+constexpr float kLoScale = 2048.0f, kLoInv = 1.0f / 2048.0f;
+
 // Stages one 16-value run held one value per lane by a 16-lane group (lane i
 // of the group holds value i; all 16 call it) into the run row layout above,
-// values scaled by s_run 2^-shift.
+// values scaled by s_run 2^-shift; SPLIT also writes the lo term.
+template <bool SPLIT = false>
 __device__ __forceinline__ void stage_run16(float v, uint32_t* row, int K, int run, int shift) {
   const int lane = threadIdx.x & 63, i = lane & 15;
   float m = fabsf(v), sum = v;
@@ -257,15 +276,39 @@ __device__ __forceinline__ void stage_run16(float v, uint32_t* row, int K, int r
     frexpf(m, &e);
     s = ldexpf(1.0f, 15 - e);
   }
-  const _Float16 hv = (_Float16)(v * (s * ldexpf(1.0f, -shift)));
+  const float vs = v * (s * ldexpf(1.0f, -shift));
+  const _Float16 hv = (_Float16)vs;
   const uint32_t hb = __builtin_bit_cast(uint16_t, hv);
   const int j = i & 7, base = 4 * (j >> 1) + (j & 1);
   const uint32_t h0 = __shfl(hb, base, 16), h1 = __shfl(hb, base + 2, 16);
   if (i < 8) row[run * 8 + j] = h0 | (h1 << 16);
+  if constexpr (SPLIT) {
+    // vs - hv is exact in fp32 (hv is vs rounded), and below half an f16
+    // step of hv, so 2^11 times it stays in range
+    const _Float16 lv = (_Float16)((vs - (float)hv) * kLoScale);
+    const uint32_t lb = __builtin_bit_cast(uint16_t, lv);
+    const uint32_t l0 = __shfl(lb, base, 16), l1 = __shfl(lb, base + 2, 16);
+    if (i < 8) row[xrun_lo(K) + run * 8 + j] = l0 | (l1 << 16);
+  }
   if (i == 0) {
     float* sums = reinterpret_cast<float*>(row + K / 2);
     sums[run] = sum;
     sums[K / 16 + run] = 16777216.0f * 16777216.0f / s;
+  }
+}
+
+// LDS pitch of a tile row of rb bytes: rows of an even number of 16-byte
+// chunks get 16 bytes of padding (an odd pitch in 16-byte units puts the 16
+// rows a lane group reads on distinct banks); others stay packed (a tile is
+// then one contiguous run of chunks).
+__host__ __device__ constexpr int row_pitch(int rb) { return rb % 32 == 0 ? rb + 16 : rb; }
+// Stores 16-byte chunk i of a tile of rows of rb bytes at pitch row_pitch(rb).
+__device__ __forceinline__ void store_tile_chunk(uint8_t* tl, int rb, int i, const u32x4& v) {
+  if (rb % 32 == 0) {
+    const int cr = rb / 16, row = i / cr;
+    *reinterpret_cast<u32x4*>(tl + row * (rb + 16) + (i - row * cr) * 16) = v;
+  } else {
+    *reinterpret_cast<u32x4*>(tl + 16 * i) = v;
   }
 }
 
@@ -290,7 +333,7 @@ struct GateUpShape {
 template <int Q, int NB>
 __host__ __device__ constexpr size_t gate_up_runs_lds() {
   using S = GateUpShape<Q, NB>;
-  return size_t(S::Sx + 4) * 4 + size_t(2 * 16) * S::rb + size_t(kWaves * 2 * 16) * 4 +
+  return size_t(S::Sx + 4) * 4 + size_t(2 * 16) * row_pitch(S::rb) + size_t(kWaves * 2 * 16) * 4 +
          size_t(3 * kMaxExperts) * 4;
 }
 
@@ -302,8 +345,9 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_kernel(DecodeArgs p, in
   const int I = p.I;
   uint32_t* xs = smem;
   uint32_t* zero = smem + Sx;
-  uint8_t* tl = reinterpret_cast<uint8_t*>(zero + 4);                     // [2][16 rows of rb]
-  float* part = reinterpret_cast<float*>(tl + 2 * 16 * rb);              // [wave][2][16]
+  constexpr int RS = row_pitch(rb);
+  uint8_t* tl = reinterpret_cast<uint8_t*>(zero + 4);                     // [2][16 rows at pitch RS]
+  float* part = reinterpret_cast<float*>(tl + 2 * 16 * RS);              // [wave][2][16]
   uint32_t* slot_e = reinterpret_cast<uint32_t*>(part + kWaves * 2 * 16);
   uint32_t* slot_a = slot_e + kMaxExperts;
   float* slot_w = reinterpret_cast<float*>(slot_a + kMaxExperts);
@@ -340,7 +384,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_kernel(DecodeArgs p, in
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int i = j * kThreads + tid;
-      if (i < S::chunks) *reinterpret_cast<u32x4*>(tl + 16 * i) = v[j];  // tiles are contiguous
+      if (i < S::chunks) store_tile_chunk(tl, rb, i, v[j]);
     }
     __syncthreads();
     if (t + int(gridDim.x) < ntiles) fetch(t + gridDim.x, slot_e[(t + gridDim.x) / tiles_i]);
@@ -348,7 +392,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_kernel(DecodeArgs p, in
     float acc[2] = {0.f, 0.f};
     for (int u = wave; u < 2 * NB; u += kWaves) {
       const int mat = u & 1, c = u >> 1;
-      const uint8_t* blk = tl + (mat * 16 + n) * rb + c * RF<Q>::kBytes;
+      const uint8_t* blk = tl + (mat * 16 + n) * RS + c * RF<Q>::kBytes;
       const float4 xsum = *reinterpret_cast<const float4*>(sums + c * 16 + 4 * q);
       const float4 kk = *reinterpret_cast<const float4*>(kks + c * 16 + 4 * q);
       const uint32_t* const cols[1] = {xs + c * 128};
@@ -480,6 +524,300 @@ __global__ void __launch_bounds__(kThreads) down_runs_kernel(DecodeArgs p, int n
       const size_t o = size_t(t) * TR + tid;
       const float base = (p.residual ? p.residual[o] : 0.f) + (p.ys ? p.ys[o] : 0.f);
       p.out[o] = base + y;
+    }
+  }
+}
+
+// ------------------------------------------------- several tokens (T > 1)
+//
+// Below the prefill threshold with T > 1 the layer's assignments are grouped
+// by expert (the select launch's slots: expert, assignment range); each
+// expert tile is computed once for all of the expert's tokens. Workgroup b
+// takes tiles b, b + G, ... of the (slot, tile) list (G = grid size), so the
+// tiles in flight at any time are neighbours in HBM. With a tile's weights
+// the kernel prefetches, into registers, the staged rows (x for gate/up, h
+// for down) of the first NT tokens of the tile's slot; a slot with more
+// tokens runs its further chunks of NT with a synchronous load from L2.
+// Every token takes the same block dot (RF<Q>::dot against that token's run
+// row); fp32 tokens add the lo term's MFMAs (NA = 2).
+
+// Assignment c of slot sl (its first one is kept in the descriptor).
+__device__ __forceinline__ uint32_t slot_assignment(const DecodeArgs& p, const uint4& sl, uint32_t c) {
+  return c == sl.y ? sl.w : p.sorted[c];
+}
+
+// Copies the staged rows (words each) of nt entries into LDS rows of the
+// same width; `src(i)` gives entry i's row.
+template <typename Src>
+__device__ __forceinline__ void load_rows(uint32_t* dst, int words, int nt, Src src) {
+  const int w4 = words / 4;
+  for (int i = threadIdx.x; i < nt * w4; i += kThreads) {
+    const int e = i / w4, o = i - e * w4;
+    reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src(e))[o];
+  }
+}
+
+// Register prefetch of the first NT entries' staged rows (W4 16-byte words
+// each) of a slot: entry e = i / W4 of flat index i = x kThreads + tid.
+template <int NT, int W4>
+struct RowPrefetch {
+  static constexpr int XP = (NT * W4 + kThreads - 1) / kThreads;
+  u32x4 v[XP];
+  uint32_t a[XP];  // the entry's assignment (kept where i % W4 == 0)
+  // `row(a)` is assignment a's staged row
+  template <typename Row>
+  __device__ __forceinline__ void load(const DecodeArgs& p, const uint4& sl, int nt, Row row) {
+#pragma unroll
+    for (int x = 0; x < XP; ++x) {
+      const int i = x * kThreads + int(threadIdx.x);
+      if (i < nt * W4) {
+        const int e = i / W4;
+        a[x] = slot_assignment(p, sl, sl.y + uint32_t(e));
+        v[x] = reinterpret_cast<const u32x4*>(row(a[x]))[i - e * W4];
+      }
+    }
+  }
+  __device__ __forceinline__ void store(uint32_t* dst, uint32_t* tok_a, int nt) const {
+#pragma unroll
+    for (int x = 0; x < XP; ++x) {
+      const int i = x * kThreads + int(threadIdx.x);
+      if (i < nt * W4) {
+        reinterpret_cast<u32x4*>(dst)[i] = v[x];
+        if (i % W4 == 0) tok_a[i / W4] = a[x];
+      }
+    }
+  }
+};
+
+template <int Q, int NB, bool SPLIT, int NT>
+struct MultiGateUpShape {
+  static constexpr int H = NB * kKBlock;
+  static constexpr int rb = NB * RF<Q>::kBytes;
+  static constexpr int Sx = xrun_words(H, SPLIT);
+  static constexpr int chunks = 2 * 16 * rb / 16;
+  static constexpr int PER = (chunks + kThreads - 1) / kThreads;
+};
+
+template <int Q, int NB, bool SPLIT, int NT>
+__host__ __device__ constexpr size_t gate_up_multi_lds() {
+  using S = MultiGateUpShape<Q, NB, SPLIT, NT>;
+  return size_t(NT) * S::Sx * 4 + 16 + size_t(2 * 16) * row_pitch(S::rb) +
+         size_t(kWaves * NT * 16) * 4 + size_t(2 * NT) * 4;
+}
+
+template <int Q, int NB, bool SPLIT, int NT>
+__global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs p) {
+  using S = MultiGateUpShape<Q, NB, SPLIT, NT>;
+  constexpr int NA = SPLIT ? 2 : 1;
+  extern __shared__ uint32_t smem[];
+  constexpr int rb = S::rb, PER = S::PER, Sx = S::Sx, H = S::H, RS = row_pitch(rb);
+  const int I = p.I, k = p.k;
+  uint32_t* xs = smem;                                              // [NT][Sx]
+  uint32_t* zero = xs + NT * Sx;
+  uint8_t* tl = reinterpret_cast<uint8_t*>(zero + 4);               // [2][16 rows at pitch RS]
+  float* part = reinterpret_cast<float*>(tl + 2 * 16 * RS);         // [wave][NT][16]
+  uint32_t* tok_ab = reinterpret_cast<uint32_t*>(part + kWaves * NT * 16);  // [2][NT]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, q = lane >> 4;
+  const int tiles_i = I / kRows;
+  const int ntiles = int(p.active[0]) * tiles_i;
+  int t = blockIdx.x;
+  if (t >= ntiles) return;  // uniform per workgroup
+  u32x4 v[PER];
+  RowPrefetch<NT, Sx / 4> xr;
+  auto row_of = [&](uint32_t a) { return p.stage_xr + size_t(a / uint32_t(k)) * Sx; };
+  auto fetch = [&](int tt) {
+    const uint4 s2 = p.slots[tt / tiles_i];
+    const size_t off = size_t(s2.x) * p.gate_stride + size_t(tt % tiles_i) * 16 * size_t(rb);
+    const u32x4* g4 = reinterpret_cast<const u32x4*>(p.gate + off);
+    const u32x4* u4 = reinterpret_cast<const u32x4*>(p.up + off);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      int i = j * kThreads + tid;
+      i = i < S::chunks ? i : S::chunks - 1;  // clamped; the extra chunks are not stored
+      v[j] = i < S::chunks / 2 ? g4[i] : u4[i - S::chunks / 2];
+    }
+    xr.load(p, s2, min(NT, int(s2.z - s2.y)), row_of);
+  };
+  fetch(t);
+  if (tid < 4) zero[tid] = 0;
+  const int mat = wave & 1;  // units (mat, c) = wave + 16 j: the matrix is the wave's parity
+  for (int it = 0; t < ntiles; t += gridDim.x, ++it) {
+    const int slot = t / tiles_i, tile = t - slot * tiles_i;
+    const uint4 sl = p.slots[slot];
+    // the assignments of the chunk in LDS; two buffers, so this store does
+    // not race the previous tile's h staging (which reads the other one)
+    uint32_t* tok_a = tok_ab + (it & 1) * NT;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = j * kThreads + tid;
+      if (i < S::chunks) store_tile_chunk(tl, rb, i, v[j]);
+    }
+    xr.store(xs, tok_a, min(NT, int(sl.z - sl.y)));
+    __syncthreads();
+    if (t + int(gridDim.x) < ntiles) fetch(t + gridDim.x);
+    for (int c0 = int(sl.y); c0 < int(sl.z); c0 += NT) {
+      const int nt = min(NT, int(sl.z) - c0);
+      if (c0 != int(sl.y)) {  // a later chunk of a slot with more than NT tokens
+        __syncthreads();      // the previous chunk's readers of tok_a / part / xs are done
+        if (tid < nt) tok_a[tid] = slot_assignment(p, sl, uint32_t(c0 + tid));
+        __syncthreads();
+        load_rows(xs, Sx, nt, [&](int e) { return row_of(tok_a[e]); });
+        __syncthreads();
+      }
+      // one token at a time (the tile's blocks are read from LDS again per
+      // token; a register array over the tokens would spill)
+      for (int ti = 0; ti < nt; ++ti) {
+        const uint32_t* row = xs + ti * Sx;
+        const float* sums = reinterpret_cast<const float*>(row + H / 2);
+        float acc = 0.f;
+        for (int c = wave >> 1; c < NB; c += kWaves / 2) {
+          const uint8_t* blk = tl + (mat * 16 + n) * RS + c * RF<Q>::kBytes;
+          const float4 xsum = *reinterpret_cast<const float4*>(sums + c * 16 + 4 * q);
+          const float4 kk = *reinterpret_cast<const float4*>(sums + H / 16 + c * 16 + 4 * q);
+          uint32_t const* cols[NA];
+          cols[0] = row + c * 128;
+          if constexpr (SPLIT) cols[NA - 1] = row + xrun_lo(H) + c * 128;
+          floatx4 C[NA];
+#pragma unroll
+          for (int a = 0; a < NA; ++a) C[a] = floatx4{0.f, 0.f, 0.f, 0.f};
+          RF<Q>::template dot<NA>(blk, cols, zero, n, q, C);
+          floatx4 Ce = C[0];
+          if constexpr (SPLIT) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Ce[i] = fmaf(C[NA - 1][i], kLoInv, Ce[i]);
+          }
+          acc += RF<Q>::epilogue(blk, Ce, xsum, kk, q);
+        }
+        acc += __shfl_xor(acc, 16, kWave);
+        acc += __shfl_xor(acc, 32, kWave);
+        if (q == 0) part[(wave * NT + ti) * 16 + n] = acc;
+      }
+      __syncthreads();
+      // a 16-lane group per token: gate rows from the even wavefronts, up
+      // rows from the odd ones, in wavefront order
+      if (tid < 16 * nt) {
+        const int ti = tid >> 4, row = tid & 15;
+        float g = 0.f, u = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w += 2) {
+          g += part[(w * NT + ti) * 16 + row];
+          u += part[((w + 1) * NT + ti) * 16 + row];
+        }
+        const uint32_t a = tok_a[ti];
+        const float h = silu(g) * u * p.weights[a];
+        stage_run16(h, p.stage_h + size_t(a) * run_words(I), I, tile, RF<Q>::run_shift(tile & 15));
+      }
+      // the next writes of part and xs come after a barrier these lanes reach
+    }
+  }
+}
+
+// Down for T > 1: tile = (slot, 16 RG rows of H); unit (row group g, column
+// c) = one block dot per token of the slot against its h row; the column
+// partials meet in LDS and are summed in column order into y[a] (fp32 rows per
+// assignment, combined over the ranks by the combine launch).
+template <int Q, int NB, int RG, int NT>
+struct MultiDownShape {
+  static constexpr int K = NB * kKBlock;  // the expert intermediate I
+  static constexpr int rb = NB * RF<Q>::kBytes;
+  static constexpr int Sh = run_words(K);
+  static constexpr int rows = 16 * RG;
+  static constexpr int chunks = rows * rb / 16;
+  static constexpr int PER = (chunks + kThreads - 1) / kThreads;
+  static_assert(rows * rb % 16 == 0, "a down tile must be whole 16-byte chunks");
+};
+
+template <int Q, int NB, int RG, int NT>
+__host__ __device__ constexpr size_t down_multi_lds() {
+  using S = MultiDownShape<Q, NB, RG, NT>;
+  return size_t(NT) * S::Sh * 4 + 16 + size_t(S::rows) * row_pitch(S::rb) +
+         size_t(RG * NB * NT * 16) * 4 + size_t(2 * NT) * 4;
+}
+
+template <int Q, int NB, int RG, int NT>
+__global__ void __launch_bounds__(kThreads) down_runs_multi_kernel(DecodeArgs p) {
+  using S = MultiDownShape<Q, NB, RG, NT>;
+  extern __shared__ uint32_t smem[];
+  constexpr int K = S::K, rb = S::rb, Sh = S::Sh, PER = S::PER, RS = row_pitch(rb);
+  const int H = p.H;
+  uint32_t* hs = smem;                                              // [NT][Sh]
+  uint32_t* zero = hs + NT * Sh;
+  uint8_t* tl = reinterpret_cast<uint8_t*>(zero + 4);               // [rows at pitch RS]
+  float* part = reinterpret_cast<float*>(tl + S::rows * RS);        // [RG * NB][NT][16]
+  uint32_t* tok_ab = reinterpret_cast<uint32_t*>(part + RG * NB * NT * 16);  // [2][NT]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, q = lane >> 4;
+  const int tiles_h = H / S::rows;
+  const int ntiles = int(p.active[0]) * tiles_h;
+  int t = blockIdx.x;
+  if (t >= ntiles) return;  // uniform per workgroup
+  u32x4 v[PER];
+  RowPrefetch<NT, Sh / 4> hr_pf;
+  auto row_of = [&](uint32_t a) { return p.stage_h + size_t(a) * Sh; };
+  auto fetch = [&](int tt) {
+    const uint4 s2 = p.slots[tt / tiles_h];
+    const u32x4* src = reinterpret_cast<const u32x4*>(
+        p.down + size_t(s2.x) * p.down_stride + size_t(tt % tiles_h) * S::rows * size_t(rb));
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      int i = j * kThreads + tid;
+      i = i < S::chunks ? i : S::chunks - 1;  // clamped; the extra chunks are not stored
+      v[j] = src[i];
+    }
+    hr_pf.load(p, s2, min(NT, int(s2.z - s2.y)), row_of);
+  };
+  fetch(t);
+  if (tid < 4) zero[tid] = 0;
+  for (int it = 0; t < ntiles; t += gridDim.x, ++it) {
+    const int slot = t / tiles_h, rt = t - slot * tiles_h;
+    const uint4 sl = p.slots[slot];
+    uint32_t* tok_a = tok_ab + (it & 1) * NT;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = j * kThreads + tid;
+      if (i < S::chunks) store_tile_chunk(tl, rb, i, v[j]);
+    }
+    hr_pf.store(hs, tok_a, min(NT, int(sl.z - sl.y)));
+    __syncthreads();
+    if (t + int(gridDim.x) < ntiles) fetch(t + gridDim.x);
+    for (int c0 = int(sl.y); c0 < int(sl.z); c0 += NT) {
+      const int nt = min(NT, int(sl.z) - c0);
+      if (c0 != int(sl.y)) {  // a later chunk of a slot with more than NT tokens
+        __syncthreads();      // the previous chunk's readers of tok_a / part / hs are done
+        if (tid < nt) tok_a[tid] = slot_assignment(p, sl, uint32_t(c0 + tid));
+        __syncthreads();
+        load_rows(hs, Sh, nt, [&](int e) { return row_of(tok_a[e]); });
+        __syncthreads();
+      }
+      for (int u = wave; u < RG * NB; u += kWaves) {
+        const int g = u / NB, c = u - g * NB;
+        const uint8_t* blk = tl + (g * 16 + n) * RS + c * RF<Q>::kBytes;
+        for (int ti = 0; ti < nt; ++ti) {
+          const uint32_t* hr = hs + ti * Sh;
+          const float* sums = reinterpret_cast<const float*>(hr + K / 2);
+          const float4 hsum = *reinterpret_cast<const float4*>(sums + c * 16 + 4 * q);
+          const float4 kk = *reinterpret_cast<const float4*>(sums + K / 16 + c * 16 + 4 * q);
+          const uint32_t* const cols[1] = {hr + c * 128};
+          floatx4 C[1] = {{0.f, 0.f, 0.f, 0.f}};
+          RF<Q>::template dot<1>(blk, cols, zero, n, q, C);
+          float r = RF<Q>::epilogue(blk, C[0], hsum, kk, q);
+          r += __shfl_xor(r, 16, kWave);
+          r += __shfl_xor(r, 32, kWave);
+          if (q == 0) part[(u * NT + ti) * 16 + n] = r;
+        }
+      }
+      __syncthreads();
+      for (int i = tid; i < RG * nt * 16; i += kThreads) {
+        const int g = i / (nt * 16), ti = (i >> 4) % nt, row = i & 15;
+        float y = 0.f;
+#pragma unroll
+        for (int c = 0; c < NB; ++c) y += part[((g * NB + c) * NT + ti) * 16 + row];
+        p.y[size_t(tok_a[ti]) * H + size_t(rt) * S::rows + g * 16 + row] = y;
+      }
+      // the next writes of part and hs come after a barrier these threads reach
     }
   }
 }

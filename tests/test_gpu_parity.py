@@ -431,6 +431,37 @@ def test_layer_runs_decode_shapes(cuda, quant, H, E, I, k, Is, dt):
     assert dn.startswith("runs-down:") or dn.startswith("mfma-down:"), dn
 
 
+# Several-token decode layers (T > 1, below 256 assignments, no shared
+# expert) on the f16-run matrix-core kernels grouped by expert: every routed
+# format, bf16 and fp32 tokens (the two-term f16 runs), and loads from ~2 to
+# ~30 tokens per expert (the latter past the kernels' per-pass token count, so
+# an expert's tiles run in several token chunks).
+@pytest.mark.parametrize("quant,H,E,I,k,T,dt", [
+    (Q4_K, 2048, 64, 768, 8, 16, torch.float32),     # c1 at T = 16
+    (Q2_K, 4096, 128, 1536, 10, 16, torch.bfloat16),  # Laguna-S shape, 160 assignments
+    (Q3_K, 3072, 16, 2048, 4, 32, torch.bfloat16),    # ~8 tokens per expert
+    (Q4_K, 1024, 4, 768, 2, 60, torch.float32),       # ~30 tokens per expert
+    (Q2_K, 1024, 4, 1024, 2, 60, torch.bfloat16),
+    (Q3_K, 2048, 8, 768, 3, 40, torch.float32),
+    (Q2_K, 6144, 256, 2048, 8, 16, torch.bfloat16)])  # GLM shape without the shared expert
+def test_layer_runs_multi_decode(cuda, quant, H, E, I, k, T, dt):
+    cfg = cf.Config(f"runs_multi_q{quant}_h{H}_e{E}_i{I}_k{k}_t{T}", 70 + H // 1024 + quant, H, E,
+                    I, k, (quant,), cf.SCORE_SOFTMAX if k == 10 else cf.SCORE_SIGMOID, True, 2.5,
+                    0.0 if k == 10 else 0.1, 0, dt, (T,))
+    _layer_parity(cuda, cfg, T, variants=2)
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
+    ops.kernel_timing(True)
+    try:
+        lt.layer.forward(cf.make_input(cfg, T, device=cuda), None)
+        torch.cuda.synchronize()
+        gu = ops.kernel_timing_label(ops.TIMER_GATE_UP)
+        dn = ops.kernel_timing_label(ops.TIMER_DOWN)
+    finally:
+        ops.kernel_timing(False)
+    assert gu.startswith("runs-multi:"), gu
+    assert dn.startswith("runs-multi-down:"), dn
+
+
 # Laguna XS layer formats (crates/model/src/laguna/gguf_model.rs:808-860,
 # laguna_xs_gguf_moe_shared_device backend.rs:1754): routed Q4_K gate/up with
 # Q4_K or Q6_K down, shared expert Q4_K gate/up with the routed down format,
