@@ -286,28 +286,16 @@ __device__ __forceinline__ void shared_down_rows(const DecodeArgs& p, int g) {
 }
 
 // T = 1: the k selected ids are distinct, so the dispatch is the k ids
-// sorted ascending (one assignment each); wavefront 0 does top-k and the
-// dispatch after the workgroup has summed the partials. On the MFMA down
-// path workgroups 1.. of this launch run the shared expert's down.
-__global__ void __launch_bounds__(256) select1_kernel(DecodeArgs p) {
-  if (blockIdx.x > 0) {
-    shared_down_rows(p, int(blockIdx.x) - 1);
-    return;
-  }
-  __shared__ float logit_row[kMaxExperts];
-  __shared__ float bias[kMaxExperts];
-  const int tid = threadIdx.x, lane = tid & 63;
+// sorted ascending (one assignment each). Run by one full wavefront once the
+// token's logits (and bias) are in LDS: exact top-k, then the dispatch and
+// the slot descriptors.
+__device__ __forceinline__ void select1_tail(const DecodeArgs& p, const float* logit_row,
+                                             const float* bias) {
+  const int lane = threadIdx.x & 63;
   const int E = p.E, k = p.k;
-  // the bias load is issued before the partials' loads and stored after
-  // them, so the two round trips overlap (E <= 256: one expert per thread)
-  const float bv = (p.bias && tid < E) ? p.bias[tid] : 0.f;
-  sum_partials(p, 0, logit_row, tid, 256);
-  if (p.bias && tid < E) bias[tid] = bv;
-  __syncthreads();
-  if (tid >= 64) return;
   uint32_t all[kMaxTopK];  // the k selected ids, held by every lane
-  topk_row_wave(logit_row, p.bias ? bias : nullptr, E, k, p.score_fn, p.norm, p.scale, 0, p.ids,
-                p.weights, nullptr, all);
+  topk_row_wave(logit_row, bias, E, k, p.score_fn, p.norm, p.scale, 0, p.ids, p.weights, nullptr,
+                all);
   uint32_t id = 0xffffffffu;
 #pragma unroll
   for (int j = 0; j < kMaxTopK; ++j)
@@ -329,6 +317,27 @@ __global__ void __launch_bounds__(256) select1_kernel(DecodeArgs p) {
     for (int j = 0; j < kMaxTopK; ++j) below += (j < k && all[j] < uint32_t(e)) ? 1u : 0u;
     p.offsets[e] = below;
   }
+}
+
+// Workgroup 0 sums the partials and runs select1_tail; on the MFMA down path
+// workgroups 1.. of this launch run the shared expert's down.
+__global__ void __launch_bounds__(256) select1_kernel(DecodeArgs p) {
+  if (blockIdx.x > 0) {
+    shared_down_rows(p, int(blockIdx.x) - 1);
+    return;
+  }
+  __shared__ float logit_row[kMaxExperts];
+  __shared__ float bias[kMaxExperts];
+  const int tid = threadIdx.x;
+  const int E = p.E;
+  // the bias load is issued before the partials' loads and stored after
+  // them, so the two round trips overlap (E <= 256: one expert per thread)
+  const float bv = (p.bias && tid < E) ? p.bias[tid] : 0.f;
+  sum_partials(p, 0, logit_row, tid, 256);
+  if (p.bias && tid < E) bias[tid] = bv;
+  __syncthreads();
+  if (tid >= 64) return;
+  select1_tail(p, logit_row, p.bias ? bias : nullptr);
 }
 
 __global__ void __launch_bounds__(1024) select_kernel(DecodeArgs p) {
@@ -759,24 +768,30 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   const bool shared_down_ok = a.H % kSharedDownRows == 0 && a.Is % kKBlock == 0 &&
                               (a.Is == 0 || a.ys != nullptr);
   const bool use_fp4 = mfma_gate_up_covers(a, quant);
-  // (fp32 tokens stay on the tile kernels: the run gate/up carries them as two
-  // f16 terms, twice the matrix-core work, and measured slower there)
+  // (bf16 tokens here; one fp32 token takes the grouped run gate/up below)
   const bool use_runs = !use_fp4 && mfma_enabled() && a.T == 1 && a.x_dtype == INFERNO_BF16 &&
                         shared_down_ok &&
                         (a.Is == 0 || a.shared_gu != nullptr) && a.stage_xr != nullptr &&
                         a.I % kRows == 0 && runs_gate_up_covers(quant, a.H, a.x_dtype) &&
                         runs_down_covers(quant, a.H, a.I, a.k);
+  // one fp32 token: the grouped run gate/up (two f16 terms per run; it takes
+  // the one-token slots as they are) with the one-token run down
+  const bool use_runs32 = !use_fp4 && mfma_enabled() && !switch_off("INFERNO_DECODE_RUNS_F32") &&
+                          a.T == 1 && a.x_dtype == INFERNO_F32 && shared_down_ok &&
+                          (a.Is == 0 || a.shared_gu != nullptr) && a.stage_xr != nullptr &&
+                          a.I % kRows == 0 && runs_multi_covers(quant, a.H, a.I, a.x_dtype) &&
+                          runs_down_covers(quant, a.H, a.I, a.k);
   // several tokens, no shared expert: the run kernels grouped by expert
   const bool use_multi = !use_fp4 && !use_runs && mfma_enabled() && a.T > 1 && a.Is == 0 &&
                          a.y != nullptr && a.stage_xr != nullptr && a.I % kRows == 0 &&
                          runs_multi_covers(quant, a.H, a.I, a.x_dtype);
-  const bool use_mfma = use_fp4 || use_runs;
+  const bool use_mfma = use_fp4 || use_runs || use_runs32;
   // with a matrix-core gate/up the shared expert's gate/up runs in the route
   // launch and stages its own x; otherwise x is staged for the tile kernels
   a.shared_parts = shared_parts(a.H);
   if (use_mfma || use_multi) a.stage_x = nullptr;
   if (!use_fp4) a.stage_xm = nullptr;
-  if (!use_runs && !use_multi) a.stage_xr = nullptr;
+  if (!use_runs && !use_runs32 && !use_multi) a.stage_xr = nullptr;
   a.xr_quant = quant;
   // down after a matrix-core gate/up (h in the run layout): the Q2_K kernel
   // (I = 2048, k <= 8) or the run kernel; the shared down then runs in the
@@ -841,12 +856,13 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   const char* gu_label =
       use_fp4 ? "mfma: gate_up_fp4_kernel (routed tiles on fp8 x fp4 MFMA; shared gate/up in the route launch)"
       : use_runs ? "runs: gate_up_runs_kernel (routed tiles on f16 MFMA; shared gate/up in the route launch)"
+      : use_runs32 ? "runs32: gate_up_runs_multi_kernel (routed tiles on f16 MFMA, fp32 token as two f16 terms; shared gate/up in the route launch)"
       : use_multi ? "runs-multi: gate_up_runs_multi_kernel (each expert's routed tiles for all its tokens on f16 MFMA)"
                   : "tiles: gate_up_kernel (routed + Q8_0 shared tiles)";
   int st = timed(s, kTimerGateUp, gu_label, [&]() -> int {
     if (use_fp4) return launch_gate_up_mfma(s, a, quant);
     if (use_runs) return launch_gate_up_runs(s, a, quant);
-    if (use_multi) return launch_gate_up_runs_multi(s, a, quant);
+    if (use_multi || use_runs32) return launch_gate_up_runs_multi(s, a, quant);
     switch (quant) {
       case INFERNO_Q2_K: xsplit ? launch_gate_up<INFERNO_Q2_K, true>(s, a) : launch_gate_up<INFERNO_Q2_K, false>(s, a); break;
       case INFERNO_Q3_K: xsplit ? launch_gate_up<INFERNO_Q3_K, true>(s, a) : launch_gate_up<INFERNO_Q3_K, false>(s, a); break;

@@ -400,13 +400,14 @@ def test_layer_q2k_decode_mfma_shapes(cuda, H, E, I, k, Is):
 # every routed format: bf16 tokens, 3 to 8 down columns, 4 to 16 ranks, with
 # and without a shared expert. Q2_K keeps the fp8 x fp4 gate/up and takes the
 # run down, as does Q3_K when its rows are whole 16-byte chunks (H a multiple
-# of 2048); fp32 tokens keep the tile kernels.
+# of 2048); fp32 tokens take the grouped run gate/up with two f16 terms.
 @pytest.mark.parametrize("quant", [Q2_K, Q3_K, Q4_K])
 @pytest.mark.parametrize("H,E,I,k,Is,dt", [(2048, 64, 768, 8, 0, torch.float32),
                                            (4096, 128, 1536, 10, 1536, torch.bfloat16),
                                            (1024, 32, 1024, 16, 256, torch.bfloat16),
                                            (3072, 16, 2048, 4, 512, torch.bfloat16),
-                                           (2048, 64, 768, 8, 0, torch.bfloat16)])
+                                           (2048, 64, 768, 8, 0, torch.bfloat16),
+                                           (3072, 16, 2048, 4, 512, torch.float32)])
 def test_layer_runs_decode_shapes(cuda, quant, H, E, I, k, Is, dt):
     cfg = cf.Config(f"runs_decode_q{quant}_h{H}_i{I}_k{k}_s{Is}", 40 + H // 1024 + quant, H, E, I,
                     k, (quant,), cf.SCORE_SOFTMAX if k == 10 else cf.SCORE_SIGMOID, True, 2.5,
@@ -421,8 +422,9 @@ def test_layer_runs_decode_shapes(cuda, quant, H, E, I, k, Is, dt):
         dn = ops.kernel_timing_label(ops.TIMER_DOWN)
     finally:
         ops.kernel_timing(False)
-    if dt == torch.float32:
-        assert gu.startswith("tiles:"), gu
+    if dt == torch.float32:  # two f16 terms per run on the grouped run gate/up
+        assert gu.startswith("runs32:"), gu
+        assert dn.startswith("runs-down:"), dn
         return
     if quant == Q2_K or (quant == Q3_K and (H // 256) % 8 == 0):
         assert gu.startswith("mfma:"), gu  # the fp8 x fp4 gate/up
@@ -671,6 +673,35 @@ def test_layer_decode_tile_kernel_variant(cuda, switches, key):
     finally:
         ops.kernel_timing(False)
     assert label.startswith("tiles:"), label
+
+
+def _labels_of_one_step(cfg, cuda, T=1):
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
+    ops.kernel_timing(True)
+    try:
+        lt.layer.forward(cf.make_input(cfg, T, device=cuda), None)
+        torch.cuda.synchronize()
+        timers = (ops.TIMER_ROUTE, ops.TIMER_SELECT, ops.TIMER_GATE_UP, ops.TIMER_DOWN)
+        labels = {tm: ops.kernel_timing_label(tm) for tm in timers}
+        counts = {tm: ops.kernel_timing_read(tm)[1] for tm in timers}
+    finally:
+        ops.kernel_timing(False)
+    return labels, counts
+
+
+@pytest.mark.parametrize("runs", [True, False])
+def test_layer_c1_fp32_token_kernels(cuda, switches, runs):
+    """One fp32 token (c1): the f16 run kernels with two f16 terms per run
+    (default) or the packed-f16 tile kernels (INFERNO_DECODE_RUNS_F32=0); 16
+    seeded tokens against the oracle; the launch labels confirm which ran."""
+    if not runs:
+        switches(INFERNO_DECODE_RUNS_F32="0")
+    _layer_parity(cuda, "c1", 1, variants=16)
+    labels, counts = _labels_of_one_step(cf.CONFIGS["c1"], cuda)
+    assert all(n == 1 for n in counts.values()), counts
+    want = ("runs32:", "runs-down:") if runs else ("tiles:", "down8:")
+    assert labels[ops.TIMER_GATE_UP].startswith(want[0]), labels[ops.TIMER_GATE_UP]
+    assert labels[ops.TIMER_DOWN].startswith(want[1]), labels[ops.TIMER_DOWN]
 
 
 def test_kernel_timing_hook_counts_decode_launches(cuda):
