@@ -451,7 +451,9 @@ struct LayerScratch {
 };
 LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   LayerScratch s;
-  s.logits = c.take<float>(T * L->experts);
+  // router logits, or their K-chunk partials for a small bf16 batch
+  s.logits = c.take<float>(T * L->experts *
+                           size_t(router_logit_parts_max(T, L->hidden, L->experts)));
   s.ids = c.take<uint32_t>(T * L->top_k);
   s.weights = c.take<float>(T * L->top_k);
   s.hs = c.take<float>(T * (L->shared_intermediate ? L->shared_intermediate : 1));
@@ -551,9 +553,12 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
     d.y = w.moe.y;
     return launch_decode_layer(s, d, L->quant);
   }
-  if ((st = launch_router_logits(s, x, x_dtype, L->router, T, H, E, w.logits))) return st;
+  const int parts = router_logit_parts(T, H, E, x_dtype);
+  if ((st = launch_router_logit_parts(s, x, x_dtype, L->router, T, H, E, w.logits, parts)))
+    return st;
   if ((st = launch_router_topk(s, w.logits, L->router_bias, T, E, k, L->score_fn,
-                               L->norm_topk_prob, L->routed_scaling_factor, ids, wts, nullptr)))
+                               L->norm_topk_prob, L->routed_scaling_factor, ids, wts, nullptr,
+                               parts)))
     return st;
   // shared expert on the GEMV kernels: gate/up from x staged in moe.stage_x
   // (h staged for the down when its format has a packed-f16 kernel), down

@@ -16,7 +16,15 @@ int launch_router_logits(hipStream_t s, const void* x, int x_dtype, const float*
                          size_t H, size_t E, float* logits);
 int launch_router_topk(hipStream_t s, const float* logits, const float* bias, size_t T, size_t E,
                        size_t k, int score_fn, int norm, float scale, uint32_t* ids,
-                       float* weights, uint32_t* token_idx);
+                       float* weights, uint32_t* token_idx, int parts = 1);
+// Router logits of bf16 tokens split over K chunks for small batches (more
+// workgroups): router_logit_parts() chunks of partials [parts][T][E], summed
+// by launch_router_topk(..., parts); router_logit_parts_max() bounds it for
+// any token type and switch setting (workspace sizing).
+int router_logit_parts(size_t T, size_t H, size_t E, int x_dtype);
+int router_logit_parts_max(size_t T, size_t H, size_t E);
+int launch_router_logit_parts(hipStream_t s, const void* x, int x_dtype, const float* w, size_t T,
+                              size_t H, size_t E, float* parts_out, int parts);
 
 int launch_dispatch(hipStream_t s, const uint32_t* ids, size_t T, size_t k, size_t E,
                     uint32_t* offsets, uint32_t* sorted, uint32_t* active);

@@ -951,12 +951,33 @@ int launch_tiled(hipStream_t s, int quant, GemmArgs a, const PlanView& v) {
   return launch_gemm_q<NMAT, 32>(s, quant, a, unsigned(v.n32));
 }
 
+// Dense Q8_0 GEMM over a small batch with 32 weight rows per workgroup (one
+// wavefront per matrix): the 128-row tiles of a 1536-row shared expert over
+// 32 tokens make only 12 workgroups, and one CU takes in roughly 17 GB/s.
+template <int NMAT>
+int launch_dense_narrow(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
+  const dim3 grid(unsigned(a.N / 32), grid_y);
+  if constexpr (NMAT == 2)
+    gemm2_kernel<INFERNO_Q8_0, 2, 32, 1, 1, 1, 2, 1, 1>
+        <<<grid, 128, gemm2_lds_bytes<INFERNO_Q8_0, 2, 32, 1, 1>(), s>>>(a);
+  else
+    gemm2_kernel<INFERNO_Q8_0, 1, 32, 2, 1, 1, 2, 1>
+        <<<grid, 64, gemm2_lds_bytes<INFERNO_Q8_0, 1, 32, 1, 1>(), s>>>(a);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
 // Dense GEMMs: tiles of TM rows over all T rows; TM from T so that small
-// batches still spread over the chip.
+// batches still spread over the chip (Q8_0 below 128 workgroups of 128-row
+// tiles: 32-row tiles).
 template <int NMAT>
 int launch_dense(hipStream_t s, int quant, GemmArgs a, size_t T) {
   if (T >= 2048) return launch_gemm_q<NMAT, 128>(s, quant, a, unsigned((T + 127) / 128));
-  return launch_gemm_q<NMAT, 32>(s, quant, a, unsigned((T + 31) / 32));
+  const unsigned gy = unsigned((T + 31) / 32);
+  if (quant == INFERNO_Q8_0 && a.N % 32 == 0 && size_t(a.N / 128) * gy < 128 && gemm2_enabled() &&
+      !switch_off("INFERNO_PREFILL_NARROW"))
+    return launch_dense_narrow<NMAT>(s, a, gy);
+  return launch_gemm_q<NMAT, 32>(s, quant, a, gy);
 }
 
 }  // namespace

@@ -225,6 +225,10 @@ __device__ __forceinline__ void split3(const float4& a, const float4& b, u32x4v 
 // bound by bytes moved into each CU, about 17 GB/s per CU, not by the access
 // pattern.) Rows past E or T read row 0 and are never stored: MFMA output
 // rows and columns are independent, so the loads need no masks.
+// blockIdx.z splits K into gridDim.z chunks of whole 32-deep blocks (every
+// chunk a multiple of 2 KS of them): chunk z writes its partial logits to
+// logits + z T E, summed in chunk order by the top-k kernel; a small batch
+// then spreads over enough workgroups to draw on every CU.
 template <int NTB, int KS>
 __global__ void __launch_bounds__(256 * KS)
     logits_bf16x3_kernel(const uint16_t* __restrict__ x, const float* __restrict__ w, int T,
@@ -244,7 +248,10 @@ __global__ void __launch_bounds__(256 * KS)
   float4v acc[NTB];
 #pragma unroll
   for (int b = 0; b < NTB; ++b) acc[b] = float4v{0.f, 0.f, 0.f, 0.f};
-  const int nkb = H / 32;
+  const int nkz = H / 32 / int(gridDim.z);  // blocks in this chunk
+  const int kz0 = int(blockIdx.z) * nkz;
+  const int nkb = kz0 + nkz;
+  logits += size_t(blockIdx.z) * size_t(T) * E;
   struct Buf {
     float4 wa, wb;
     u32x4v xv[NTB];
@@ -268,11 +275,11 @@ __global__ void __launch_bounds__(256 * KS)
                                                          __builtin_bit_cast(bf16x8, u.xv[b]),
                                                          acc[b], 0, 0, 0);
   };
-  // the host launches this kernel only when 2 * KS divides H / 32
+  // the host launches this kernel only when 2 * KS divides the chunk's blocks
   Buf u0, u1;
-  load(s, u0);
-  load(s + KS, u1);
-  for (int kb = s; kb < nkb; kb += 2 * KS) {
+  load(kz0 + s, u0);
+  load(kz0 + s + KS, u1);
+  for (int kb = kz0 + s; kb < nkb; kb += 2 * KS) {
     compute(u0);
     load(kb + 2 * KS, u0);
     compute(u1);
@@ -301,6 +308,7 @@ __global__ void __launch_bounds__(256 * KS)
   }
 }
 
+// One wavefront per token.
 __global__ void __launch_bounds__(256)
     topk_kernel(const float* __restrict__ logits, const float* __restrict__ bias, int T, int E,
                 int k, int score_fn, int norm, float scale, uint32_t* __restrict__ ids,
@@ -312,11 +320,69 @@ __global__ void __launch_bounds__(256)
                 token_idx, sel);
 }
 
+// K-chunk partial logits [parts][T][E] (parts <= kMaxRouterParts): one token
+// per workgroup; thread e sums expert e's partials in chunk order (all loads
+// issued together) into an LDS row, then wavefront 0 selects.
+constexpr int kMaxRouterParts = 16;
+__global__ void __launch_bounds__(256)
+    topk_parts_kernel(const float* __restrict__ parts_in, const float* __restrict__ bias, int T,
+                      int E, int k, int score_fn, int norm, float scale, uint32_t* __restrict__ ids,
+                      float* __restrict__ weights, uint32_t* __restrict__ token_idx, int parts) {
+  __shared__ float row[kMaxExperts];
+  const int t = blockIdx.x, e = threadIdx.x;
+  if (e < E) {
+    const float* src = parts_in + size_t(t) * E + e;
+    const size_t stride = size_t(T) * E;
+    float v[kMaxRouterParts];
+#pragma unroll
+    for (int z = 0; z < kMaxRouterParts; ++z) v[z] = z < parts ? src[size_t(z) * stride] : 0.f;
+    float sum = 0.f;
+#pragma unroll
+    for (int z = 0; z < kMaxRouterParts; ++z)
+      if (z < parts) sum += v[z];
+    row[e] = sum;
+  }
+  __syncthreads();
+  if (threadIdx.x >= 64) return;
+  uint32_t sel[kMaxTopK];
+  topk_row_wave(row, bias, E, k, score_fn, norm, scale, t, ids, weights, token_idx, sel);
+}
+
 }  // namespace
 
 // INFERNO_ROUTER_BF16X3=0 keeps the fp32 matrix-core logits for bf16 tokens.
 static bool bf16x3_enabled() {
   return !switch_off("INFERNO_ROUTER_BF16X3");
+}
+
+// K chunks for the bf16 x router logits of a T-token batch: 1 when the
+// batch alone gives the kernel enough workgroups; else the most (a power of
+// two, up to kMaxRouterParts) that keeps at most kRouterSplitGroups
+// workgroups of the one-group kernel and a whole number of 32-deep block
+// pairs per chunk.
+constexpr size_t kRouterSplitGroups = 256;
+int router_logit_parts_max(size_t T, size_t H, size_t E) {
+  if (T <= 16 || H % 256) return 1;
+  const size_t base = ((E + 63) / 64) * ((T + 15) / 16);
+  if (base * 2 > kRouterSplitGroups) return 1;
+  int z = 1;
+  while (z < kMaxRouterParts && base * size_t(2 * z) <= kRouterSplitGroups && (H / 32) % size_t(4 * z) == 0) z *= 2;
+  return z;
+}
+int router_logit_parts(size_t T, size_t H, size_t E, int x_dtype) {
+  if (x_dtype != INFERNO_BF16 || !bf16x3_enabled()) return 1;
+  return router_logit_parts_max(T, H, E);
+}
+
+int launch_router_logit_parts(hipStream_t s, const void* x, int x_dtype, const float* w, size_t T,
+                              size_t H, size_t E, float* parts_out, int parts) {
+  if (parts <= 1) return launch_router_logits(s, x, x_dtype, w, T, H, E, parts_out);
+  if (T == 0 || E == 0) return INFERNO_OK;
+  const dim3 grid(unsigned((E + 63) / 64), unsigned((T + 15) / 16), unsigned(parts));
+  logits_bf16x3_kernel<1, 1><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x), w, int(T),
+                                                  int(H), int(E), parts_out);
+  INF_LAUNCHED();
+  return INFERNO_OK;
 }
 
 int launch_router_logits(hipStream_t s, const void* x, int x_dtype, const float* w, size_t T,
@@ -375,11 +441,15 @@ int launch_router_logits(hipStream_t s, const void* x, int x_dtype, const float*
 
 int launch_router_topk(hipStream_t s, const float* logits, const float* bias, size_t T, size_t E,
                        size_t k, int score_fn, int norm, float scale, uint32_t* ids,
-                       float* weights, uint32_t* token_idx) {
+                       float* weights, uint32_t* token_idx, int parts) {
   if (T == 0) return INFERNO_OK;
-  topk_kernel<<<unsigned((T + 3) / 4), 256, 0, s>>>(logits, bias, int(T), int(E), int(k),
-                                                    score_fn, norm, scale, ids, weights,
-                                                    token_idx);
+  if (parts > 1)
+    topk_parts_kernel<<<unsigned(T), 256, 0, s>>>(logits, bias, int(T), int(E), int(k), score_fn,
+                                                   norm, scale, ids, weights, token_idx, parts);
+  else
+    topk_kernel<<<unsigned((T + 3) / 4), 256, 0, s>>>(logits, bias, int(T), int(E), int(k),
+                                                      score_fn, norm, scale, ids, weights,
+                                                      token_idx);
   INF_LAUNCHED();
   return INFERNO_OK;
 }
