@@ -164,6 +164,11 @@ def main():
     prefill = labels[ops.TIMER_GATE_UP].startswith("prefill")
     if prefill:
         timers = [ops.TIMER_GATE_UP, ops.TIMER_DOWN]
+    # one token on the fp8 x fp4 gate/up: the selection (and the shared down)
+    # run in the gate/up launch, so there is no select launch
+    sel_in_gu = labels[ops.TIMER_GATE_UP].startswith("mfma+select")
+    if sel_in_gu:
+        timers = [ops.TIMER_GATE_UP, ops.TIMER_DOWN, ops.TIMER_ROUTE]
     for tm in timers:
         if timed[tm][1] != launches:
             raise RuntimeError(f"kernel timer {tm} saw {timed[tm][1]} launches for {launches}")
@@ -184,16 +189,17 @@ def main():
         # a stack mixes formats: the label is the last layer's, so the shared
         # bytes follow the kind of each layer's launch, read per layer below
         gu_kind, dn_kind = kinds[ops.TIMER_GATE_UP], kinds[ops.TIMER_DOWN]
-        rt_kind, sl_kind = kinds[ops.TIMER_ROUTE], kinds[ops.TIMER_SELECT]
+        rt_kind = kinds[ops.TIMER_ROUTE]
+        sl_kind = kinds.get(ops.TIMER_SELECT)
         kernels = {
             "route": {"label": labels[ops.TIMER_ROUTE], "launch_us": us[ops.TIMER_ROUTE],
                       "bytes_per_launch": E * H * 4 + (shared_gu if rt_kind == "route+shared" else 0)},
-            "select": {"label": labels[ops.TIMER_SELECT], "launch_us": us[ops.TIMER_SELECT],
-                       "bytes_per_launch": shared_dn if sl_kind == "select+shared-down" else None},
             "gate_up": {"label": labels[ops.TIMER_GATE_UP], "launch_us": gu_us,
-                        "bytes_per_launch": gu_routed + (shared_gu if gu_kind in ("tiles", "ring") else 0),
+                        "bytes_per_launch": gu_routed + (shared_gu if gu_kind in ("tiles", "ring") else 0)
+                        + (shared_dn if gu_kind == "mfma+select" else 0),
                         "routed_bytes_per_launch": gu_routed,
                         "traffic_file": {"mfma": "gate_up_fp4_q2k_c2_decode_traffic.txt",
+                                         "mfma+select": "gate_up_sel_fp4_q2k_c2_decode_traffic.txt",
                                          "tiles": "gate_up_q2k_c2_decode_traffic.txt"}.get(gu_kind)},
             "down": {"label": labels[ops.TIMER_DOWN], "launch_us": dn_us,
                      "bytes_per_launch": dn_routed + (shared_dn if dn_kind == "down8" else 0),
@@ -201,6 +207,9 @@ def main():
                      "traffic_file": {"down8": "down8_q2k_c2_decode_traffic.txt",
                                       "mfma-down": "down_mfma_q2k_c2_decode_traffic.txt"}.get(dn_kind)},
         }
+        if not sel_in_gu:
+            kernels["select"] = {"label": labels[ops.TIMER_SELECT], "launch_us": us[ops.TIMER_SELECT],
+                                 "bytes_per_launch": shared_dn if sl_kind == "select+shared-down" else None}
         if stacked:
             for kd in kernels.values():
                 kd["label"] = f"{kd['label']} [last of {n_sub} layers; times and bytes averaged per launch]"
@@ -256,7 +265,7 @@ def main():
     # terms times Q2_K fields as e2m1, down on f16 MFMA; prefill: f16 MFMA;
     # packed-f16 tile kernels otherwise), always fp32 accumulation
     gu_label = labels[ops.TIMER_GATE_UP]
-    if gu_label.startswith("mfma:"):
+    if gu_label.startswith("mfma"):
         dtype = "e4m3x2*e2m1 MFMA gate/up, f16 MFMA down, f32 acc"
     elif gu_label.startswith("prefill"):
         dtype = "f16 MFMA, f32 acc"

@@ -20,6 +20,7 @@
 #include "decode.hpp"
 #include "decode_mfma.hpp"
 #include "decode_runs.hpp"
+#include "decode_select.hpp"
 
 #include <cstdlib>
 #include "timing.hpp"
@@ -207,64 +208,7 @@ __device__ __forceinline__ void shared_down_rows(const DecodeArgs& p, int g) {
 #pragma unroll
   for (int grp = 0; grp < kGroups; ++grp)
     if (q_first < ubs) FS::load(srow(grp) + size_t(q_first) * FS::kBytes, sub, sraw[grp]);
-  // h = silu(sum of gate partials) * (sum of up partials), formed and staged
-  // by lane quads: lane holds values 4 (v4 & 3) .. + 3 of run v4 / 4 (the
-  // parts are added in order 0, 1, ... as the gate/up kernels do); every
-  // part's loads are issued before the sums. The quad gives the run's
-  // maximum, its sum in value order (as stage_run forms it) and the hi pair
-  // words 2 (v4 & 3), + 1, which take only this lane's values.
-  const int parts = p.shared_parts;
-  constexpr int kIt = 2;  // float4 steps per thread issued together
-  for (int v0 = tid; v0 < Is / 4; v0 += 256 * kIt) {
-    float4 gv[kIt][4], uv[kIt][4];
-#pragma unroll
-    for (int it = 0; it < kIt; ++it)
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (k < parts && v0 + 256 * it < Is / 4) {
-          gv[it][k] = reinterpret_cast<const float4*>(p.shared_gu + (size_t(k) * 2) * Is)[v0 + 256 * it];
-          uv[it][k] = reinterpret_cast<const float4*>(p.shared_gu + (size_t(k) * 2 + 1) * Is)[v0 + 256 * it];
-        }
-#pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-      const int v4 = v0 + 256 * it;
-      if (v4 >= Is / 4) break;  // uniform: Is / 4 is a multiple of 64
-      float4 gs = make_float4(0.f, 0.f, 0.f, 0.f), us = gs;
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (k < parts) {
-          gs.x += gv[it][k].x; gs.y += gv[it][k].y; gs.z += gv[it][k].z; gs.w += gv[it][k].w;
-          us.x += uv[it][k].x; us.y += uv[it][k].y; us.z += uv[it][k].z; us.w += uv[it][k].w;
-        }
-      const float h0 = silu(gs.x) * us.x, h1 = silu(gs.y) * us.y;
-      const float h2 = silu(gs.z) * us.z, h3 = silu(gs.w) * us.w;
-      float m = fmaxf(fmaxf(fabsf(h0), fabsf(h1)), fmaxf(fabsf(h2), fabsf(h3)));
-      m = fmaxf(m, __shfl_xor(m, 1, kWave));
-      m = fmaxf(m, __shfl_xor(m, 2, kWave));
-      const int q0 = lane & ~3;
-      float sum = 0.f;
-#pragma unroll
-      for (int qq = 0; qq < 4; ++qq) sum = __shfl((((sum + h0) + h1) + h2) + h3, q0 + qq, kWave);
-      float scale = 1.0f;  // zero or non-finite runs keep scale 1
-      if (m > 0.f && m < 3.0e38f) {
-        int e;
-        frexpf(m, &e);
-        scale = ldexpf(1.0f, 15 - e);
-      }
-      auto pack = [](float a, float b) {
-        const _Float16 ah = (_Float16)a, bh = (_Float16)b;
-        return uint32_t(__builtin_bit_cast(uint16_t, ah)) | (uint32_t(__builtin_bit_cast(uint16_t, bh)) << 16);
-      };
-      const int run = v4 >> 2, qi = v4 & 3;
-      *reinterpret_cast<uint2*>(xss + run * 8 + 2 * qi) =
-          make_uint2(pack(h0 * scale, h2 * scale), pack(h1 * scale, h3 * scale));
-      if (qi == 0) {
-        float* sums = reinterpret_cast<float*>(xss + Is / 2);
-        sums[run] = sum;
-        sums[Is / 16 + run] = 1.0f / scale;
-      }
-    }
-  }
+  form_shared_h<256>(p, xss, tid);
   __syncthreads();
 #pragma unroll
   for (int grp = 0; grp < kGroups; ++grp) {
@@ -285,42 +229,8 @@ __device__ __forceinline__ void shared_down_rows(const DecodeArgs& p, int g) {
   }
 }
 
-// T = 1: the k selected ids are distinct, so the dispatch is the k ids
-// sorted ascending (one assignment each). Run by one full wavefront once the
-// token's logits (and bias) are in LDS: exact top-k, then the dispatch and
-// the slot descriptors.
-__device__ __forceinline__ void select1_tail(const DecodeArgs& p, const float* logit_row,
-                                             const float* bias) {
-  const int lane = threadIdx.x & 63;
-  const int E = p.E, k = p.k;
-  uint32_t all[kMaxTopK];  // the k selected ids, held by every lane
-  topk_row_wave(logit_row, bias, E, k, p.score_fn, p.norm, p.scale, 0, p.ids, p.weights, nullptr,
-                all);
-  uint32_t id = 0xffffffffu;
-#pragma unroll
-  for (int j = 0; j < kMaxTopK; ++j)
-    if (j == lane) id = all[j];
-  // rank of each id among the k (distinct) ids
-  uint32_t rank = 0;
-#pragma unroll
-  for (int j = 0; j < kMaxTopK; ++j) rank += (j < k && all[j] < id) ? 1u : 0u;
-  if (lane < k) {
-    p.sorted[rank] = uint32_t(lane);  // assignment index t*k + r with t = 0
-    p.active[1 + rank] = id;
-    p.slots[rank] = make_uint4(id, rank, rank + 1, uint32_t(lane));
-  }
-  if (lane == 0) p.active[0] = uint32_t(k);
-  // offsets[e] = number of ids below e
-  for (int e = lane; e <= E; e += 64) {
-    uint32_t below = 0;
-#pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j) below += (j < k && all[j] < uint32_t(e)) ? 1u : 0u;
-    p.offsets[e] = below;
-  }
-}
-
-// Workgroup 0 sums the partials and runs select1_tail; on the MFMA down path
-// workgroups 1.. of this launch run the shared expert's down.
+// Workgroup 0 sums the partials and selects; on the MFMA down path
+// workgroups 1.. run the shared expert's down (shared_down_rows).
 __global__ void __launch_bounds__(256) select1_kernel(DecodeArgs p) {
   if (blockIdx.x > 0) {
     shared_down_rows(p, int(blockIdx.x) - 1);
@@ -328,16 +238,28 @@ __global__ void __launch_bounds__(256) select1_kernel(DecodeArgs p) {
   }
   __shared__ float logit_row[kMaxExperts];
   __shared__ float bias[kMaxExperts];
+  __shared__ Top1Lds tk;
+  // the selection is a serial chain: its waves go first on SIMDs shared with
+  // shared-down workgroups
+  __builtin_amdgcn_s_setprio(3);
   const int tid = threadIdx.x;
   const int E = p.E;
   // the bias load is issued before the partials' loads and stored after
   // them, so the two round trips overlap (E <= 256: one expert per thread)
   const float bv = (p.bias && tid < E) ? p.bias[tid] : 0.f;
   sum_partials(p, 0, logit_row, tid, 256);
-  if (p.bias && tid < E) bias[tid] = bv;
+  bias[tid] = bv;
   __syncthreads();
   if (tid >= 64) return;
-  select1_tail(p, logit_row, p.bias ? bias : nullptr);
+  float lg[4], bs[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = tid + 64 * j;
+    lg[j] = e < E ? logit_row[e] : 0.f;
+    bs[j] = bias[e];
+  }
+  topk1_wave(lg, bs, E, p.k, p.score_fn, p.norm, p.scale, &tk);
+  select1_write(p, &tk);
 }
 
 __global__ void __launch_bounds__(1024) select_kernel(DecodeArgs p) {
@@ -651,10 +573,10 @@ bool mfma_gate_up_covers(const DecodeArgs& a, int quant) {
          device_cus() > 0;
 }
 
-template <int Q, int NB>
+template <int Q, int NB, bool SEL>
 int launch_gate_up_mfma_nb(hipStream_t s, const DecodeArgs& a, int ntiles) {
   static bool attr = false;
-  auto* kern = mfma_decode::gate_up_fp4_kernel<Q, NB>;
+  auto* kern = mfma_decode::gate_up_fp4_kernel<Q, NB, SEL>;
   if (!attr) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                             160 * 1024) != hipSuccess) {
@@ -664,31 +586,62 @@ int launch_gate_up_mfma_nb(hipStream_t s, const DecodeArgs& a, int ntiles) {
     attr = true;
   }
   const unsigned grid = unsigned(std::min(ntiles, device_cus()));
-  kern<<<grid, mfma_decode::kThreads, mfma_decode::lds_bytes(a.H, Q), s>>>(a, ntiles);
+  kern<<<grid, mfma_decode::kThreads, mfma_decode::lds_bytes(a.H, Q, SEL ? a.Is : 0), s>>>(a, ntiles);
   INF_LAUNCHED();
   return INFERNO_OK;
 }
 
-// The routed tiles of the k slots on the fp8 x fp4 kernel (the shared
-// expert's gate/up already ran in the route launch).
-int launch_gate_up_mfma(hipStream_t s, const DecodeArgs& a0, int quant) {
-  const int ntiles = a0.max_slots * (a0.I / kRows);
-  if (quant == INFERNO_Q3_K) {
+template <int Q, bool SEL>
+int launch_gate_up_mfma_q(hipStream_t s, const DecodeArgs& a0, int ntiles) {
+  if constexpr (Q == INFERNO_Q3_K) {
     switch (a0.H / kKBlock) {
-      case 8: return launch_gate_up_mfma_nb<INFERNO_Q3_K, 8>(s, a0, ntiles);
-      case 16: return launch_gate_up_mfma_nb<INFERNO_Q3_K, 16>(s, a0, ntiles);
-      default: return launch_gate_up_mfma_nb<INFERNO_Q3_K, 24>(s, a0, ntiles);
+      case 8: return launch_gate_up_mfma_nb<Q, 8, SEL>(s, a0, ntiles);
+      case 16: return launch_gate_up_mfma_nb<Q, 16, SEL>(s, a0, ntiles);
+      default: return launch_gate_up_mfma_nb<Q, 24, SEL>(s, a0, ntiles);
+    }
+  } else {
+    switch (a0.H / kKBlock) {
+      case 4: return launch_gate_up_mfma_nb<Q, 4, SEL>(s, a0, ntiles);
+      case 8: return launch_gate_up_mfma_nb<Q, 8, SEL>(s, a0, ntiles);
+      case 12: return launch_gate_up_mfma_nb<Q, 12, SEL>(s, a0, ntiles);
+      case 16: return launch_gate_up_mfma_nb<Q, 16, SEL>(s, a0, ntiles);
+      case 20: return launch_gate_up_mfma_nb<Q, 20, SEL>(s, a0, ntiles);
+      case 24: return launch_gate_up_mfma_nb<Q, 24, SEL>(s, a0, ntiles);
+      default: return launch_gate_up_mfma_nb<Q, 28, SEL>(s, a0, ntiles);
     }
   }
-  switch (a0.H / kKBlock) {
-    case 4: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 4>(s, a0, ntiles);
-    case 8: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 8>(s, a0, ntiles);
-    case 12: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 12>(s, a0, ntiles);
-    case 16: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 16>(s, a0, ntiles);
-    case 20: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 20>(s, a0, ntiles);
-    case 24: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 24>(s, a0, ntiles);
-    default: return launch_gate_up_mfma_nb<INFERNO_Q2_K, 28>(s, a0, ntiles);
-  }
+}
+
+// The routed tiles of the k slots on the fp8 x fp4 kernel (the shared
+// expert's gate/up already ran in the route launch); with sel, the kernel
+// also selects and runs the shared down (no select launch).
+int launch_gate_up_mfma(hipStream_t s, const DecodeArgs& a0, int quant, bool sel) {
+  const int ntiles = a0.max_slots * (a0.I / kRows);
+  if (quant == INFERNO_Q3_K)
+    return sel ? launch_gate_up_mfma_q<INFERNO_Q3_K, true>(s, a0, ntiles)
+               : launch_gate_up_mfma_q<INFERNO_Q3_K, false>(s, a0, ntiles);
+  return sel ? launch_gate_up_mfma_q<INFERNO_Q2_K, true>(s, a0, ntiles)
+             : launch_gate_up_mfma_q<INFERNO_Q2_K, false>(s, a0, ntiles);
+}
+
+// The selection (and the shared down) in the fp8 x fp4 gate/up launch: one
+// token, at most three shared-down octets per workgroup (kSdWpo wavefronts
+// each, one 256-value unit per lane), staged through the tile registers and
+// tile area; INFERNO_DECODE_SEL=0 keeps the select launch.
+bool sel_in_gate_up(const DecodeArgs& a, bool shared_down_here) {
+  if (a.T != 1 || switch_off("INFERNO_DECODE_SEL")) return false;
+  const int ntiles = a.max_slots * (a.I / kRows);
+  const int grid = std::min(ntiles, device_cus());
+  if (!shared_down_here) return true;
+  // the workgroup's rows (whole octets) fit the tile registers and area
+  const int NB = a.H / kKBlock, kB = mfma_decode::fp4_block_bytes(a.xr_quant);
+  const int rw = 8 * ((a.H / 8 + grid - 1) / grid);
+  const size_t sd_bytes = size_t(rw) * size_t(a.Is / 32) * 34;
+  const size_t tile_regs = size_t(mfma_decode::chunks_per_thread(NB, kB)) * mfma_decode::kThreads * 16;
+  const size_t tile_lds = size_t(2 * 16) * size_t(NB * kB + mfma_decode::kRowPad);
+  return a.Is % kKBlock == 0 && a.Is <= 2 * kKBlock * kSdWpo && a.H % 8 == 0 &&
+         rw <= 8 * kSdMaxOctets && sd_bytes <= tile_regs && sd_bytes <= tile_lds &&
+         mfma_decode::lds_bytes(a.H, a.xr_quant, a.Is) <= 160 * 1024;
 }
 
 template <int TR, int PER>
@@ -833,7 +786,10 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
                          });
     if (st) return st;
   }
-  {
+  // one token on the fp8 x fp4 gate/up: the selection and the shared down
+  // run in the gate/up launch (no select launch)
+  const bool use_sel = use_fp4 && sel_in_gate_up(a, use_mfma_down && a.Is);
+  if (!use_sel) {
     const int sd_wgs = (use_mfma_down && a.Is) ? a.H / kSharedDownRows : 0;
     const size_t sd_lds = sd_wgs ? (size_t(staged_stride(a.Is, false)) + 32) * 4 : 0;
     const char* label = a.T != 1 ? "select: select_kernel"
@@ -854,13 +810,14 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   // residual folded in: one stream, no events
   a.routed_tiles = a.max_slots * (a.I / kRows);
   const char* gu_label =
-      use_fp4 ? "mfma: gate_up_fp4_kernel (routed tiles on fp8 x fp4 MFMA; shared gate/up in the route launch)"
+      use_sel ? "mfma+select: gate_up_fp4_kernel (top-k and Q8_0 shared down in every workgroup's prologue; routed tiles on fp8 x fp4 MFMA; shared gate/up in the route launch)"
+      : use_fp4 ? "mfma: gate_up_fp4_kernel (routed tiles on fp8 x fp4 MFMA; shared gate/up in the route launch)"
       : use_runs ? "runs: gate_up_runs_kernel (routed tiles on f16 MFMA; shared gate/up in the route launch)"
       : use_runs32 ? "runs32: gate_up_runs_multi_kernel (routed tiles on f16 MFMA, fp32 token as two f16 terms; shared gate/up in the route launch)"
       : use_multi ? "runs-multi: gate_up_runs_multi_kernel (each expert's routed tiles for all its tokens on f16 MFMA)"
                   : "tiles: gate_up_kernel (routed + Q8_0 shared tiles)";
   int st = timed(s, kTimerGateUp, gu_label, [&]() -> int {
-    if (use_fp4) return launch_gate_up_mfma(s, a, quant);
+    if (use_fp4) return launch_gate_up_mfma(s, a, quant, use_sel);
     if (use_runs) return launch_gate_up_runs(s, a, quant);
     if (use_multi || use_runs32) return launch_gate_up_runs_multi(s, a, quant);
     switch (quant) {

@@ -41,6 +41,7 @@
 // No workgroup waits on another.
 #pragma once
 #include "decode.hpp"
+#include "decode_select.hpp"
 #include "dot2_formats.hpp"
 
 namespace inferno {
@@ -218,7 +219,18 @@ __host__ __device__ constexpr int chunks_per_thread(int NB, int bytes = kQ2Bytes
 // hmask byte i into the low bit of the nibble that holds plane p of qs byte
 // i, a second fp4 B (value hbit / 2) whose MFMAs take the A scale + 2 (x 4),
 // so C = sum x (low + 4 hbit) / 2 = sum x q3 / 2; value = gs (q3 - 4).
-template <int Q, int NB>
+//
+// SEL (one token): the launch also does the select launch's work, so the
+// layer takes three launches. Every workgroup selects the token's experts
+// itself (wavefront 15: the route launch's logit partials, topk1_wave) into
+// its slot table, and workgroup 0 writes the ids, weights and dispatch for
+// the down launch; meanwhile the other wavefronts form the shared expert's
+// h from the route launch's partials and load the shared down rows of this
+// workgroup's 8-row octets (octet o = blockIdx.x + w gridDim.x for wavefront
+// w), whose dot products run while the first routed tile's loads are in
+// flight. The selection is the select launch's (same function), so the
+// result does not depend on which launch ran it.
+template <int Q, int NB, bool SEL>
 __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int ntiles) {
   extern __shared__ uint32_t smem[];
   constexpr int kB = fp4_block_bytes(Q);
@@ -234,22 +246,61 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
   uint32_t* slot_e = reinterpret_cast<uint32_t*>(part + kWaves * 2 * 16);  // [max_slots]
   uint32_t* slot_a = slot_e + kMaxExperts;
   float* slot_w = reinterpret_cast<float*>(slot_a + kMaxExperts);
+  Top1Lds* tk = reinterpret_cast<Top1Lds*>(slot_w + kMaxExperts);
+  float* sdpart = reinterpret_cast<float*>(tk + 1);  // [wave][8] shared down parts (SEL)
+  uint32_t* hsd = reinterpret_cast<uint32_t*>(sdpart + kWaves * 8);  // shared h (SEL)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, q = lane >> 4;
   const int tiles_i = I / kRows;
   u32x4 v[PER];
   int t = blockIdx.x;
-  if (t < ntiles) fetch_tile<PER>(v, p, tiles_i, rb, t, p.slots[t / tiles_i].x);
-  for (int i = tid; i < Sm / 4; i += kThreads)
-    reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(p.stage_xm)[i];
-  if (tid < 4) zero[tid] = 0;
-  // per-slot expert, assignment and routing weight, read once
-  for (int j = tid; j < p.max_slots; j += kThreads) {
-    const uint4 sl = p.slots[j];
-    slot_e[j] = sl.x;
-    slot_a[j] = sl.w;
-    slot_w[j] = p.weights[sl.w];
+  // SEL: this workgroup's shared down rows [sd_row0, sd_row0 + sd_rows)
+  int sd_rows = 0, sd_row0 = 0;
+  if constexpr (SEL) {
+    constexpr int kSelWave = kWaves - 1;
+    const bool sdown = p.Is && p.ys;  // else the shared down runs in the down launch
+    if (sdown) {
+      const int G = int(gridDim.x), rw = 8 * ((p.H / 8 + G - 1) / G);
+      sd_row0 = int(blockIdx.x) * rw;
+      sd_rows = max(0, min(rw, p.H - sd_row0));
+    }
+    if (wave == kSelWave) {
+      // the selection: the longest chain of the prologue, so nothing else,
+      // and first in issue on its SIMD
+      __builtin_amdgcn_s_setprio(3);
+      float lg[4], bs[4];
+      load_logits1(p, lg, bs);
+      topk1_wave(lg, bs, p.E, p.k, p.score_fn, p.norm, p.scale, tk);
+      if (lane < p.k) {  // slot j = j-th smallest id, assignment = its rank
+        const uint32_t rank = tk->rank[lane];
+        slot_e[lane] = tk->id[lane];
+        slot_a[lane] = rank;
+        slot_w[lane] = tk->w[rank];
+      }
+      __builtin_amdgcn_s_setprio(0);
+      if (blockIdx.x == 0) select1_write(p, tk);
+    } else {
+      constexpr int kT = kSelWave * kWave;  // threads of the other wavefronts
+      if (sd_rows) form_shared_h<kT>(p, hsd, tid);  // used after the routed tiles
+      for (int i = tid; i < Sm / 4; i += kT)
+        reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(p.stage_xm)[i];
+      if (tid < 4) zero[tid] = 0;
+    }
+    __syncthreads();
+    if (t < ntiles) fetch_tile<PER>(v, p, tiles_i, rb, t, slot_e[t / tiles_i]);
+  } else {
+    if (t < ntiles) fetch_tile<PER>(v, p, tiles_i, rb, t, p.slots[t / tiles_i].x);
+    for (int i = tid; i < Sm / 4; i += kThreads)
+      reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(p.stage_xm)[i];
+    if (tid < 4) zero[tid] = 0;
+    // per-slot expert, assignment and routing weight, read once
+    for (int j = tid; j < p.max_slots; j += kThreads) {
+      const uint4 sl = p.slots[j];
+      slot_e[j] = sl.x;
+      slot_a[j] = sl.w;
+      slot_w[j] = p.weights[sl.w];
+    }
   }
   // the shared expert's gate/up partial sums (split over K in the route
   // launch) -> SwiGLU -> staged h rows for down8_kernel, one 16-row tile per
@@ -291,8 +342,22 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
       }
     }
     __syncthreads();
-    if (t + int(gridDim.x) < ntiles)
+    if (t + int(gridDim.x) < ntiles) {
       fetch_tile<PER>(v, p, tiles_i, rb, t + gridDim.x, slot_e[(t + gridDim.x) / tiles_i]);
+    } else if constexpr (SEL) {
+      // after the last routed tile: this workgroup's shared down rows,
+      // contiguous, in flight while the tile is computed
+      if (sd_rows) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(
+            p.sdown + size_t(sd_row0) * SharedDownSlice::row_bytes(p.Is));
+        const int nc = int(size_t(sd_rows) * SharedDownSlice::row_bytes(p.Is) / 16);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const int i = j * kThreads + tid;
+          v[j] = src[i < nc ? i : nc - 1];
+        }
+      }
+    }
     const int slot = t / tiles_i, tile = t - slot * tiles_i;
     float acc[2] = {0.f, 0.f};
     for (int c = wave; c < NB; c += kWaves) {
@@ -431,6 +496,24 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
         else
           stage_run_lanes(h, p.stage_h + size_t(a) * staged_stride(I, true), I, tile);
       }
+    }
+  }
+  if constexpr (SEL) {
+    // the shared down of rows [sd_row0, sd_row0 + sd_rows): the rows (in v
+    // since the last tile's barrier) to the free tile area, dot products
+    // against the shared h formed in the prologue, parts summed in order
+    if (sd_rows) {
+      const int nc = int(size_t(sd_rows) * SharedDownSlice::row_bytes(p.Is) / 16);
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int i = j * kThreads + tid;
+        if (i < nc) reinterpret_cast<u32x4*>(tl)[i] = v[j];
+      }
+      __syncthreads();
+      if (wave < (sd_rows / 8) * kSdWpo)
+        SharedDownSlice::dot(p, reinterpret_cast<const uint32_t*>(tl), hsd, wave, sdpart);
+      __syncthreads();
+      if (tid < sd_rows) SharedDownSlice::store(p, sdpart, tid, sd_row0);
     }
   }
 }
@@ -595,10 +678,11 @@ inline bool covers_width(int H) {
   return H % kKBlock == 0 && NB % 4 == 0 && NB >= 4 && NB <= 28;
 }
 
-inline size_t lds_bytes(int H, int quant = INFERNO_Q2_K) {
+inline size_t lds_bytes(int H, int quant = INFERNO_Q2_K, int Is_sel = 0) {
   const int rb = H / kKBlock * fp4_block_bytes(quant);
   return size_t(stage_words(H) + 4) * 4 + size_t(2 * 16) * (rb + kRowPad) +
-         size_t(kWaves * 2 * 16) * 4 + size_t(3 * kMaxExperts) * 4;
+         size_t(kWaves * 2 * 16) * 4 + size_t(3 * kMaxExperts) * 4 + sizeof(Top1Lds) +
+         size_t(kWaves * 8) * 4 + size_t(staged_stride(Is_sel, false)) * 4;
 }
 
 }  // namespace mfma_decode

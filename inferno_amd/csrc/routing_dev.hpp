@@ -170,6 +170,134 @@ __device__ __forceinline__ void topk_row_wave(const float* row, const float* __r
 }
 
 
+// LDS scratch of topk1_wave.
+struct Top1Lds {
+  uint64_t rk[kMaxTopK];    // selected rank keys, ascending expert id
+  uint32_t id[kMaxTopK];    // selected ids, ascending
+  float sc[kMaxTopK];       // their scores
+  uint32_t rank[kMaxTopK];  // rank of id-ordered entry j
+  uint32_t rid[kMaxTopK];   // ids in rank order
+  float w[kMaxTopK];        // routing weights in rank order
+};
+
+// Exact top-k of one token by one full wavefront, the semantics of
+// topk_row_wave with a shorter dependency chain: lane holds the logits of
+// experts lane + 64 j in lg[j] (anything for e >= E). The k-th largest
+// selection key K is found bit by bit on 32-bit compares; every key above
+// K wins, and of the keys equal to K the lowest ids fill the remaining
+// places. The k winners are
+// compacted into LDS in expert-id order with ballot prefix counts, and each
+// winner's rank comes from comparing it with the k compacted (key, id)
+// pairs. On return (after a wave barrier) s holds the winners in id order
+// with their ranks, and ids and weights in rank order; weights are
+// renormalised by the rank-order sum of the scores (as topk_row_wave).
+__device__ __forceinline__ void topk1_wave(const float (&lgin)[4], const float (&bs)[4], int E,
+                                           int k, int score_fn, int norm, float scale,
+                                           Top1Lds* __restrict__ s) {
+  constexpr int PER = kMaxExperts / kWave;
+  const int lane = threadIdx.x & 63;
+  float score[PER];
+  uint32_t key[PER];
+  bool live[PER];
+  float lmax = 0.f;
+  if (score_fn == INFERNO_SCORE_SOFTMAX) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) m = fmaxf(m, lane + j * kWave < E ? lgin[j] : -INFINITY);
+    lmax = wave_max(m);
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int e = lane + j * kWave;
+    live[j] = e < E;
+    const float l = live[j] ? lgin[j] : -INFINITY;
+    float sv, sel;
+    if (score_fn == INFERNO_SCORE_SIGMOID) {
+      sv = 1.0f / (1.0f + expf(-l));
+      sel = sv;
+    } else {
+      sv = live[j] ? expf(l - lmax) : 0.f;
+      sel = l;
+    }
+    score[j] = sv;
+    // dead candidates get key 0, the lowest; they also have the highest ids,
+    // so a live key of 0 still goes first
+    key[j] = live[j] ? total_order_key(sel + bs[j]) : 0u;
+  }
+  float denom_all = 0.f;
+  if (score_fn == INFERNO_SCORE_SOFTMAX && !norm) {
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) part += score[j];
+    denom_all = wave_sum(part);
+  }
+  // K: the largest value with at least k keys at or above it, one bit per
+  // step from the top (four ballot counts each; measured faster than two
+  // bits per step, whose extra compares each cost a VALU -> SGPR round trip)
+  uint32_t kth = 0;
+#pragma unroll 4
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t c = kth | (1u << b);
+    uint32_t n = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) n += uint32_t(__popcll(__ballot(key[j] >= c)));
+    kth = n >= uint32_t(k) ? c : kth;
+  }
+  // winners: keys above K, then the lowest ids among keys equal to K
+  uint32_t above = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) above += uint32_t(__popcll(__ballot(key[j] > kth)));
+  uint32_t rem = uint32_t(k) - above;
+  bool win[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const bool eq = key[j] == kth;
+    const uint64_t em = __ballot(eq);
+    const uint32_t before = __builtin_amdgcn_mbcnt_hi(uint32_t(em >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo(uint32_t(em), 0u));
+    win[j] = key[j] > kth || (eq && before < rem);
+    const uint32_t ne = uint32_t(__popcll(em));
+    rem = rem > ne ? rem - ne : 0u;
+  }
+  // compact the k winners in expert-id order (j major, then lane); rank key
+  // (key << 8 | 255 - id): larger is better
+  uint32_t base = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint64_t m = __ballot(win[j]);
+    if (win[j]) {
+      const uint32_t e = uint32_t(lane + j * kWave);
+      const uint32_t pos = base + uint32_t(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
+      s->rk[pos] = (uint64_t(key[j]) << 8) | uint64_t(255u - (e & 255u));
+      s->id[pos] = e;
+      s->sc[pos] = score[j];
+    }
+    base += uint32_t(__popcll(m));
+  }
+  __builtin_amdgcn_wave_barrier();  // LDS is in order within a wavefront
+  uint32_t my_rank = 0;
+  if (lane < k) {
+    const uint64_t mine = s->rk[lane];
+    for (int i = 0; i < k; ++i) my_rank += s->rk[i] > mine ? 1u : 0u;
+    s->rank[lane] = my_rank;
+    s->rid[my_rank] = s->id[lane];
+    s->w[my_rank] = s->sc[lane];
+  }
+  __builtin_amdgcn_wave_barrier();
+  float sum = 0.f;
+  if (norm)
+    for (int r = 0; r < k; ++r) sum += s->w[r];  // rank order, every lane
+  if (!norm && score_fn == INFERNO_SCORE_SOFTMAX) sum = denom_all;
+  const bool divide = (norm || score_fn == INFERNO_SCORE_SOFTMAX) && sum > 0.f && isfinite(sum);
+  if (lane < k) {
+    float wv = s->w[lane];
+    if (divide) wv /= sum;
+    s->w[lane] = wv * scale;
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
 constexpr int kDispatchThreads = 1024;
 constexpr int kDispatchWaves = kDispatchThreads / kWave;
 

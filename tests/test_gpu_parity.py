@@ -385,6 +385,35 @@ def test_layer_c2_glm_q2k_decode_full_size(cuda):
     _layer_parity(cuda, "c2", 1, variants=16)
 
 
+# Exact ties in the one-token decode selection: a zero router makes every
+# logit 0, so the selection keys are the bias tiers (sigmoid) or all equal
+# (softmax, no bias); the k winners must be the oracle's (key desc, id asc),
+# in rank order, with the oracle's weights. E = 64 and 256 (four candidates
+# per lane), Q2_K (fp8 x fp4 gate/up) and Q4_K (run gate/up).
+@pytest.mark.parametrize("score_fn", [SCORE_SIGMOID, SCORE_SOFTMAX])
+@pytest.mark.parametrize("E,k,quant", [(64, 8, Q2_K), (256, 8, Q2_K), (256, 16, Q4_K)])
+def test_layer_decode_selection_ties(cuda, score_fn, E, k, quant):
+    cfg = cf.Config(f"ties_e{E}_k{k}", 90 + E // 64, 1024, E, 512, k, (quant,), score_fn, True,
+                    2.5, 0.0, 256, torch.bfloat16, (1,))
+    bias = None
+    if score_fn == SCORE_SIGMOID:
+        tiers = np.array([0.0, 0.25, 0.5], np.float32)
+        bias = torch.from_numpy(tiers[np.arange(E) % 3].copy()).to(cuda)
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=1, bias=bias)
+    lt.router.zero_()
+    x = cf.make_input(cfg, 1, device=cuda)
+    ids = torch.empty(k, dtype=torch.int32, device=cuda)
+    w = torch.empty(k, device=cuda)
+    out = lt.layer.forward(x, None, ids=ids, weights=w)
+    torch.cuda.synchronize()
+    oid, ow = orc.router_topk(np.zeros((1, E), np.float32),
+                              None if bias is None else ph.to_np(bias), k, score_fn, True, 2.5)
+    got = ph.to_np(ids).view(np.uint32)
+    assert np.array_equal(got, oid), (got, oid)
+    np.testing.assert_allclose(ph.to_np(w), ow, rtol=2e-6, atol=0)
+    assert torch.isfinite(out).all()
+
+
 # One-token Q2_K bf16 layers of other shapes: the MFMA gate/up at 4, 8 and 12
 # super-block columns, the MFMA down (I = 2048) with 4 ranks, the tile-kernel
 # down after the MFMA gate/up (I != 2048), with and without a shared expert.
@@ -427,7 +456,7 @@ def test_layer_runs_decode_shapes(cuda, quant, H, E, I, k, Is, dt):
         assert dn.startswith("runs-down:"), dn
         return
     if quant == Q2_K or (quant == Q3_K and (H // 256) % 8 == 0):
-        assert gu.startswith("mfma:"), gu  # the fp8 x fp4 gate/up
+        assert gu.startswith("mfma"), gu  # the fp8 x fp4 gate/up (with or without the selection)
     else:
         assert gu.startswith("runs:"), gu
     assert dn.startswith("runs-down:") or dn.startswith("mfma-down:"), dn
@@ -704,6 +733,35 @@ def test_layer_c1_fp32_token_kernels(cuda, switches, runs):
     assert labels[ops.TIMER_DOWN].startswith(want[1]), labels[ops.TIMER_DOWN]
 
 
+@pytest.mark.parametrize("key", ["c2", "c4"])
+def test_layer_decode_select_launch_variant(cuda, switches, key):
+    """INFERNO_DECODE_SEL=0 keeps the separate select launch (top-k, dispatch
+    and the shared down in their own launch) on the one-token fp8 x fp4 path:
+    same oracle bound, and the same ids and weights as the default path,
+    whose gate/up launch selects; the launch labels say which ran."""
+    cfg = cf.CONFIGS[key]
+    lt = cf.build_layer(cfg, 0 if key == "c2" else 2, cuda, max_tokens=1)
+    x = cf.make_input(cfg, 1, device=cuda)
+    got = {}
+    for sel in ("1", "0"):
+        switches(INFERNO_DECODE_SEL=sel)
+        ids = torch.empty(cfg.top_k, dtype=torch.int32, device=cuda)
+        w = torch.empty(cfg.top_k, device=cuda)
+        out = lt.layer.forward(x, None, ids=ids, weights=w)
+        torch.cuda.synchronize()
+        got[sel] = (ph.to_np(ids).copy(), ph.to_np(w).copy(), ph.to_np(out).copy())
+        labels, counts = _labels_of_one_step(cfg, cuda)
+        assert labels[ops.TIMER_GATE_UP].startswith("mfma+select:" if sel == "1" else "mfma:")
+        assert counts[ops.TIMER_SELECT] == (0 if sel == "1" else 1), counts
+    assert np.array_equal(got["1"][0], got["0"][0])
+    assert np.array_equal(got["1"][1], got["0"][1])
+    err = rn.rel_l2(got["1"][2], got["0"][2])
+    print(f"{key}: select in gate/up vs select launch rel_l2={err:.3e}")
+    assert err < 1e-5  # only the shared down's summation order differs
+    switches(INFERNO_DECODE_SEL="0")
+    _layer_parity(cuda, cfg, 1, variants=4)
+
+
 def test_kernel_timing_hook_counts_decode_launches(cuda):
     """The measurement hook: events recorded around each timed launch without
     waiting, summed when read; two decode steps give two launches per timer,
@@ -722,8 +780,14 @@ def test_kernel_timing_hook_counts_decode_launches(cuda):
         labels = {tm: ops.kernel_timing_label(tm) for tm in timers}
     finally:
         ops.kernel_timing(False)
+    # one token on the fp8 x fp4 gate/up: the selection runs in the gate/up
+    # launch and the select launch is skipped
+    assert labels[ops.TIMER_GATE_UP].startswith("mfma+select:"), labels[ops.TIMER_GATE_UP]
     for tm in timers:
         ms, n = got[tm]
+        if tm == ops.TIMER_SELECT:
+            assert n == 0, (tm, ms, n)
+            continue
         assert n == 2 and ms > 0, (tm, ms, n)
         assert ":" in labels[tm]
     assert ops.kernel_timing_read(ops.TIMER_GATE_UP)[1] == 0  # read resets
