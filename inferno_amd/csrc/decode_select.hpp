@@ -43,32 +43,35 @@ __device__ __forceinline__ void select1_write(const DecodeArgs& p, const Top1Lds
 
 // The token's logits from the route launch's chunk partials (summed in chunk
 // order, as sum_partials) and the bias, lane holding experts lane + 64 j; all
-// loads are issued before the sums. One full wavefront.
+// loads are issued before the sums, unconditionally (indices clamped, values
+// past the ends replaced by zero afterwards): a load under a branch makes the
+// join wait for its data. One full wavefront.
 __device__ __forceinline__ void load_logits1(const DecodeArgs& p, float (&lg)[4], float (&bs)[4]) {
   const int lane = threadIdx.x & 63;
   const int E = p.E, nc = p.n_chunks;
+  const float* bp = p.bias ? p.bias : p.partials;  // uniform
+  float bv[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = lane + 64 * j;
-    bs[j] = (p.bias && e < E) ? p.bias[e] : 0.f;
-  }
+  for (int j = 0; j < 4; ++j) bv[j] = bp[min(lane + 64 * j, E - 1)];
   for (int c0 = 0; c0 < nc; c0 += 8) {
     float v[4][8];  // 32 loads in flight
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const int e = lane + 64 * j;
-        v[j][c] = (c0 + c < nc && e < E) ? p.partials[size_t(c0 + c) * E + e] : 0.f;
-      }
+      for (int c = 0; c < 8; ++c)
+        v[j][c] = p.partials[size_t(min(c0 + c, nc - 1)) * E + min(lane + 64 * j, E - 1)];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const bool live = lane + 64 * j < E;
       float s = c0 == 0 ? 0.f : lg[j];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) s += v[j][c];  // zeros past the last chunk, as sum_partials
+      for (int c = 0; c < 8; ++c)  // zeros past the last chunk, as sum_partials
+        s += (live && c0 + c < nc) ? v[j][c] : 0.f;
       lg[j] = s;
     }
   }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bs[j] = (p.bias && lane + 64 * j < E) ? bv[j] : 0.f;
 }
 
 // h = silu(sum of gate partials) * (sum of up partials) of the shared expert,
@@ -80,14 +83,16 @@ __device__ __forceinline__ void load_logits1(const DecodeArgs& p, float (&lg)[4]
 // of the wavefront must take part (quad shuffles).
 struct SharedHQuad {
   float4 gv[4], uv[4];
+  // unconditional loads (part and position clamped; stage() drops the
+  // extra parts): a load under a branch makes the join wait for its data
   __device__ __forceinline__ void load(const DecodeArgs& p, int v4, bool live) {
-    const int Is = p.Is;
+    const int Is = p.Is, v = live ? v4 : 0;
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (live && k < p.shared_parts) {
-        gv[k] = reinterpret_cast<const float4*>(p.shared_gu + (size_t(k) * 2) * Is)[v4];
-        uv[k] = reinterpret_cast<const float4*>(p.shared_gu + (size_t(k) * 2 + 1) * Is)[v4];
-      }
+    for (int k = 0; k < 4; ++k) {
+      const size_t kk = size_t(min(k, p.shared_parts - 1));
+      gv[k] = reinterpret_cast<const float4*>(p.shared_gu + (kk * 2) * Is)[v];
+      uv[k] = reinterpret_cast<const float4*>(p.shared_gu + (kk * 2 + 1) * Is)[v];
+    }
   }
   __device__ __forceinline__ void stage(const DecodeArgs& p, uint32_t* xss, int v4, bool live) {
     const int lane = threadIdx.x & 63;
