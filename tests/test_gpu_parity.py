@@ -4,6 +4,7 @@ Bars: dequantised weights bit-exact; selected
 expert ids exact except near-ties within 1e-6 of the k-th selection value
 (counted and reported); MoE outputs within relative L2 2e-3.
 """
+import dataclasses
 from types import SimpleNamespace
 
 import numpy as np
@@ -278,10 +279,11 @@ def test_rms_norm(cuda):
     assert np.allclose(got, ref, rtol=2e-6, atol=1e-6)
 
 
-def _layer_parity(cuda, key, T, tokens=None, variants=1):
+def _layer_parity(cuda, key, T, tokens=None, variants=1, tol=None):
     """Layer output against the oracle on `variants` seeded inputs of T tokens
     (rows `tokens` of each; all rows by default). The MoE part's relative L2
-    error is taken over all checked rows together."""
+    error is taken over all checked rows together and must stay below `tol`
+    (default); returns it."""
     cfg = cf.CONFIGS[key] if isinstance(key, str) else key
     lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
     tokens = np.arange(T) if tokens is None else np.asarray(tokens)
@@ -310,7 +312,8 @@ def _layer_parity(cuda, key, T, tokens=None, variants=1):
     err = rn.rel_l2(np.concatenate(got_all), np.concatenate(ref_all))
     print(f"{cfg.name} T={T} x{variants} inputs, {len(tokens)} rows each: "
           f"rel_l2(moe part)={err:.3e} near-tie tokens={flips}")
-    assert err < ph.TOL_REL_L2
+    assert err < (ph.TOL_REL_L2 if tol is None else tol)
+    return err
 
 
 @pytest.mark.parametrize("quant", [Q2_K, Q3_K, Q4_K])
@@ -760,6 +763,23 @@ def test_layer_decode_select_launch_variant(cuda, switches, key):
     assert err < 1e-5  # only the shared down's summation order differs
     switches(INFERNO_DECODE_SEL="0")
     _layer_parity(cuda, cfg, 1, variants=4)
+
+
+@pytest.mark.parametrize("sel", ["1", "0"])
+def test_layer_decode_shared_expert_alone(cuda, switches, sel):
+    """c2's shape with the routed part scaled to zero (routing scale 0): the
+    output is the residual plus the Q8_0 shared expert alone, so its decode
+    path is checked without the routed experts' error. Its gate/up runs in
+    the route launch (K parts); its down in the selecting gate/up launch
+    (default) or the select launch (INFERNO_DECODE_SEL=0), both against h
+    staged as f16 runs with a power-of-two scale per 16 values: ~2^-12
+    relative per value, measured ~4e-4 rel-L2 on this part, bound 1e-3."""
+    switches(INFERNO_DECODE_SEL=sel)
+    cfg = dataclasses.replace(cf.CONFIGS["c2"], name="c2_shared_alone", scale=0.0)
+    labels, _ = _labels_of_one_step(cfg, cuda)
+    want = "mfma+select:" if sel == "1" else "mfma:"
+    assert labels[ops.TIMER_GATE_UP].startswith(want), labels[ops.TIMER_GATE_UP]
+    _layer_parity(cuda, cfg, 1, variants=4, tol=1e-3)
 
 
 def test_kernel_timing_hook_counts_decode_launches(cuda):
