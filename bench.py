@@ -166,7 +166,7 @@ def main():
         timers = [ops.TIMER_GATE_UP, ops.TIMER_DOWN]
     # one token on the fp8 x fp4 gate/up: the selection (and the shared down)
     # run in the gate/up launch, so there is no select launch
-    sel_in_gu = labels[ops.TIMER_GATE_UP].startswith("mfma+select")
+    sel_in_gu = labels[ops.TIMER_GATE_UP].split(":")[0].endswith("+select")
     if sel_in_gu:
         timers = [ops.TIMER_GATE_UP, ops.TIMER_DOWN, ops.TIMER_ROUTE]
     for tm in timers:

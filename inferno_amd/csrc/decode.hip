@@ -788,7 +788,11 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   }
   // one token on the fp8 x fp4 gate/up: the selection and the shared down
   // run in the gate/up launch (no select launch)
-  const bool use_sel = use_fp4 && sel_in_gate_up(a, use_mfma_down && a.Is);
+  // one fp32 token on the grouped run gate/up without a shared expert: the
+  // selection moves into that launch too
+  const bool use_sel32 = use_runs32 && a.T == 1 && a.Is == 0 && !switch_off("INFERNO_DECODE_SEL") &&
+                         runs_multi_sel_covers(quant, a.H, a.x_dtype);
+  const bool use_sel = use_sel32 || (use_fp4 && sel_in_gate_up(a, use_mfma_down && a.Is));
   if (!use_sel) {
     const int sd_wgs = (use_mfma_down && a.Is) ? a.H / kSharedDownRows : 0;
     const size_t sd_lds = sd_wgs ? (size_t(staged_stride(a.Is, false)) + 32) * 4 : 0;
@@ -810,16 +814,17 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   // residual folded in: one stream, no events
   a.routed_tiles = a.max_slots * (a.I / kRows);
   const char* gu_label =
-      use_sel ? "mfma+select: gate_up_fp4_kernel (top-k and Q8_0 shared down in every workgroup's prologue; routed tiles on fp8 x fp4 MFMA; shared gate/up in the route launch)"
+      (use_sel && use_fp4) ? "mfma+select: gate_up_fp4_kernel (top-k and Q8_0 shared down in every workgroup's prologue; routed tiles on fp8 x fp4 MFMA; shared gate/up in the route launch)"
       : use_fp4 ? "mfma: gate_up_fp4_kernel (routed tiles on fp8 x fp4 MFMA; shared gate/up in the route launch)"
       : use_runs ? "runs: gate_up_runs_kernel (routed tiles on f16 MFMA; shared gate/up in the route launch)"
+      : use_sel32 ? "runs32+select: gate_up_runs_multi_kernel (top-k in every workgroup's prologue; routed tiles on f16 MFMA, fp32 token as two f16 terms)"
       : use_runs32 ? "runs32: gate_up_runs_multi_kernel (routed tiles on f16 MFMA, fp32 token as two f16 terms; shared gate/up in the route launch)"
       : use_multi ? "runs-multi: gate_up_runs_multi_kernel (each expert's routed tiles for all its tokens on f16 MFMA)"
                   : "tiles: gate_up_kernel (routed + Q8_0 shared tiles)";
   int st = timed(s, kTimerGateUp, gu_label, [&]() -> int {
     if (use_fp4) return launch_gate_up_mfma(s, a, quant, use_sel);
     if (use_runs) return launch_gate_up_runs(s, a, quant);
-    if (use_multi || use_runs32) return launch_gate_up_runs_multi(s, a, quant);
+    if (use_multi || use_runs32) return launch_gate_up_runs_multi(s, a, quant, use_sel32);
     switch (quant) {
       case INFERNO_Q2_K: xsplit ? launch_gate_up<INFERNO_Q2_K, true>(s, a) : launch_gate_up<INFERNO_Q2_K, false>(s, a); break;
       case INFERNO_Q3_K: xsplit ? launch_gate_up<INFERNO_Q3_K, true>(s, a) : launch_gate_up<INFERNO_Q3_K, false>(s, a); break;

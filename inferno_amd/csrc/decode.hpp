@@ -68,7 +68,9 @@ int launch_down_runs(hipStream_t s, const DecodeArgs& a, int quant);
 // The same kernels for T > 1 tokens (no shared expert): gate/up per expert
 // tile for all of the expert's tokens, down rows per assignment into a.y.
 bool runs_multi_covers(int quant, int H, int I, int x_dtype);
-int launch_gate_up_runs_multi(hipStream_t s, const DecodeArgs& a, int quant);
+// sel: one token, the selection inside the launch (no select launch before)
+int launch_gate_up_runs_multi(hipStream_t s, const DecodeArgs& a, int quant, bool sel = false);
+bool runs_multi_sel_covers(int quant, int H, int x_dtype);
 int launch_down_runs_multi(hipStream_t s, const DecodeArgs& a, int quant);
 
 

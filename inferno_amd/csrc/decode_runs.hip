@@ -195,27 +195,28 @@ constexpr int multi_rg() {
 }
 constexpr int kDownNT = 8;
 
-template <int Q, int NB, bool SPLIT>
+// SEL: one token, the selection in the launch (one token per LDS pass)
+template <int Q, int NB, bool SPLIT, bool SEL>
 int gate_up_multi_nb(hipStream_t s, const DecodeArgs& a) {
-  constexpr int NT = multi_nt<Q, NB, SPLIT>();
+  constexpr int NT = SEL ? 1 : multi_nt<Q, NB, SPLIT>();
   static bool attr = false;
-  auto* kern = gate_up_runs_multi_kernel<Q, NB, SPLIT, NT>;
+  auto* kern = gate_up_runs_multi_kernel<Q, NB, SPLIT, NT, SEL>;
   if (int st = allow_lds(kern, attr)) return st;
   const int ntiles = a.max_slots * (a.I / kRows);  // upper bound: active slots <= max_slots
   const unsigned grid = unsigned(std::min(ntiles, cus_now()));
-  kern<<<grid, kThreads, gate_up_multi_lds<Q, NB, SPLIT, NT>(), s>>>(a);
+  kern<<<grid, kThreads, gate_up_multi_lds<Q, NB, SPLIT, NT, SEL>(), s>>>(a);
   INF_LAUNCHED();
   return INFERNO_OK;
 }
 
-template <int Q, bool SPLIT>
+template <int Q, bool SPLIT, bool SEL>
 int gate_up_multi_q(hipStream_t s, const DecodeArgs& a) {
   switch (a.H / kKBlock) {
-    case 4: return gate_up_multi_nb<Q, 4, SPLIT>(s, a);
-    case 8: return gate_up_multi_nb<Q, 8, SPLIT>(s, a);
-    case 12: return gate_up_multi_nb<Q, 12, SPLIT>(s, a);
-    case 16: return gate_up_multi_nb<Q, 16, SPLIT>(s, a);
-    default: return gate_up_multi_nb<Q, 24, SPLIT>(s, a);
+    case 4: return gate_up_multi_nb<Q, 4, SPLIT, SEL>(s, a);
+    case 8: return gate_up_multi_nb<Q, 8, SPLIT, SEL>(s, a);
+    case 12: return gate_up_multi_nb<Q, 12, SPLIT, SEL>(s, a);
+    case 16: return gate_up_multi_nb<Q, 16, SPLIT, SEL>(s, a);
+    default: return gate_up_multi_nb<Q, 24, SPLIT, SEL>(s, a);
   }
 }
 
@@ -286,17 +287,46 @@ bool runs_multi_covers(int quant, int H, int I, int x_dtype) {
   }
 }
 
-int launch_gate_up_runs_multi(hipStream_t s, const DecodeArgs& a, int quant) {
+template <bool SEL>
+int gate_up_multi_sel(hipStream_t s, const DecodeArgs& a, int quant) {
   const bool split = a.x_dtype == INFERNO_F32;
   switch (quant) {
     case INFERNO_Q2_K:
-      return split ? gate_up_multi_q<INFERNO_Q2_K, true>(s, a) : gate_up_multi_q<INFERNO_Q2_K, false>(s, a);
+      return split ? gate_up_multi_q<INFERNO_Q2_K, true, SEL>(s, a) : gate_up_multi_q<INFERNO_Q2_K, false, SEL>(s, a);
     case INFERNO_Q3_K:
-      return split ? gate_up_multi_q<INFERNO_Q3_K, true>(s, a) : gate_up_multi_q<INFERNO_Q3_K, false>(s, a);
+      return split ? gate_up_multi_q<INFERNO_Q3_K, true, SEL>(s, a) : gate_up_multi_q<INFERNO_Q3_K, false, SEL>(s, a);
     default:
-      return split ? gate_up_multi_q<INFERNO_Q4_K, true>(s, a) : gate_up_multi_q<INFERNO_Q4_K, false>(s, a);
+      return split ? gate_up_multi_q<INFERNO_Q4_K, true, SEL>(s, a) : gate_up_multi_q<INFERNO_Q4_K, false, SEL>(s, a);
   }
 }
+
+int launch_gate_up_runs_multi(hipStream_t s, const DecodeArgs& a, int quant, bool sel) {
+  return sel ? gate_up_multi_sel<true>(s, a, quant) : gate_up_multi_sel<false>(s, a, quant);
+}
+
+// The selecting variant's LDS fits (one token per pass).
+bool runs_multi_sel_covers(int quant, int H, int x_dtype) {
+  const bool split = x_dtype == INFERNO_F32;
+  const int NB = H / kKBlock;
+  auto lds = [&](auto q_c) -> size_t {
+    constexpr int Q = decltype(q_c)::value;
+    switch (NB) {
+      case 4: return split ? gate_up_multi_lds<Q, 4, true, 1, true>() : gate_up_multi_lds<Q, 4, false, 1, true>();
+      case 8: return split ? gate_up_multi_lds<Q, 8, true, 1, true>() : gate_up_multi_lds<Q, 8, false, 1, true>();
+      case 12: return split ? gate_up_multi_lds<Q, 12, true, 1, true>() : gate_up_multi_lds<Q, 12, false, 1, true>();
+      case 16: return split ? gate_up_multi_lds<Q, 16, true, 1, true>() : gate_up_multi_lds<Q, 16, false, 1, true>();
+      case 24: return split ? gate_up_multi_lds<Q, 24, true, 1, true>() : gate_up_multi_lds<Q, 24, false, 1, true>();
+      default: return ~size_t(0);
+    }
+  };
+  switch (quant) {
+    case INFERNO_Q2_K: return lds(std::integral_constant<int, INFERNO_Q2_K>{}) <= kLdsMax;
+    case INFERNO_Q3_K: return lds(std::integral_constant<int, INFERNO_Q3_K>{}) <= kLdsMax;
+    case INFERNO_Q4_K: return lds(std::integral_constant<int, INFERNO_Q4_K>{}) <= kLdsMax;
+    default: return false;
+  }
+}
+
 
 int launch_down_runs_multi(hipStream_t s, const DecodeArgs& a, int quant) {
   switch (quant) {

@@ -598,14 +598,24 @@ struct MultiGateUpShape {
   static constexpr int PER = (chunks + kThreads - 1) / kThreads;
 };
 
-template <int Q, int NB, bool SPLIT, int NT>
+// LDS of the selecting variant's additions: topk1_wave's scratch and the
+// slot table (expert, assignment, routing weight per slot)
+constexpr size_t kSelMultiLds = 8 + sizeof(Top1Lds) + size_t(3 * kMaxTopK) * 4;
+
+template <int Q, int NB, bool SPLIT, int NT, bool SEL = false>
 __host__ __device__ constexpr size_t gate_up_multi_lds() {
   using S = MultiGateUpShape<Q, NB, SPLIT, NT>;
   return size_t(NT) * S::Sx * 4 + 16 + size_t(2 * 16) * row_pitch(S::rb) +
-         size_t(kWaves * NT * 16) * 4 + size_t(2 * NT) * 4;
+         size_t(kWaves * NT * 16) * 4 + size_t(2 * NT) * 4 + (SEL ? kSelMultiLds : 0);
 }
 
-template <int Q, int NB, bool SPLIT, int NT>
+// SEL (one token, no shared expert in this launch's epilogue): the kernel
+// selects itself, as gate_up_fp4_kernel's prologue does (wavefront 15 of
+// every workgroup: the route launch's logit partials, topk1_wave) into an
+// LDS slot table (slot j = the j-th smallest selected id, its one
+// assignment = its rank, its routing weight), and workgroup 0 writes the
+// ids, weights and dispatch for the down launch: no select launch.
+template <int Q, int NB, bool SPLIT, int NT, bool SEL = false>
 __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs p) {
   using S = MultiGateUpShape<Q, NB, SPLIT, NT>;
   constexpr int NA = SPLIT ? 2 : 1;
@@ -617,18 +627,54 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
   uint8_t* tl = reinterpret_cast<uint8_t*>(zero + 4);               // [2][16 rows at pitch RS]
   float* part = reinterpret_cast<float*>(tl + 2 * 16 * RS);         // [wave][NT][16]
   uint32_t* tok_ab = reinterpret_cast<uint32_t*>(part + kWaves * NT * 16);  // [2][NT]
+  // SEL: topk1_wave's scratch (8-byte aligned: every region above is a
+  // whole number of 8-byte words) and the slot table
+  Top1Lds* tk = reinterpret_cast<Top1Lds*>(tok_ab + 2 * NT);
+  uint32_t* sel_e = reinterpret_cast<uint32_t*>(tk + 1);
+  uint32_t* sel_a = sel_e + kMaxTopK;
+  float* sel_w = reinterpret_cast<float*>(sel_a + kMaxTopK);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, q = lane >> 4;
   const int tiles_i = I / kRows;
-  const int ntiles = int(p.active[0]) * tiles_i;
+  int ntiles;
+  if constexpr (SEL) {
+    if (wave == kWaves - 1) {
+      __builtin_amdgcn_s_setprio(3);
+      float lg[4], bs[4];
+      load_logits1(p, lg, bs);
+      topk1_wave(lg, bs, p.E, k, p.score_fn, p.norm, p.scale, tk);
+      if (lane < k) {  // slot j = j-th smallest id, assignment = its rank
+        const uint32_t rank = tk->rank[lane];
+        sel_e[lane] = tk->id[lane];
+        sel_a[lane] = rank;
+        sel_w[lane] = tk->w[rank];
+      }
+      __builtin_amdgcn_s_setprio(0);
+      if (blockIdx.x == 0) select1_write(p, tk);
+    }
+    __syncthreads();
+    ntiles = k * tiles_i;  // one token: every slot is a distinct expert
+  } else {
+    ntiles = int(p.active[0]) * tiles_i;
+  }
+  // slot j's descriptor {expert, first, end, first assignment} and the
+  // routing weight of assignment a (of slot j)
+  auto slot_of = [&](int j) -> uint4 {
+    if constexpr (SEL) return make_uint4(sel_e[j], uint32_t(j), uint32_t(j + 1), sel_a[j]);
+    else return p.slots[j];
+  };
+  auto weight_of = [&](int j, uint32_t a) -> float {
+    if constexpr (SEL) return sel_w[j];
+    else return p.weights[a];
+  };
   int t = blockIdx.x;
   if (t >= ntiles) return;  // uniform per workgroup
   u32x4 v[PER];
   RowPrefetch<NT, Sx / 4> xr;
   auto row_of = [&](uint32_t a) { return p.stage_xr + size_t(a / uint32_t(k)) * Sx; };
   auto fetch = [&](int tt) {
-    const uint4 s2 = p.slots[tt / tiles_i];
+    const uint4 s2 = slot_of(tt / tiles_i);
     const size_t off = size_t(s2.x) * p.gate_stride + size_t(tt % tiles_i) * 16 * size_t(rb);
     const u32x4* g4 = reinterpret_cast<const u32x4*>(p.gate + off);
     const u32x4* u4 = reinterpret_cast<const u32x4*>(p.up + off);
@@ -645,7 +691,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
   const int mat = wave & 1;  // units (mat, c) = wave + 16 j: the matrix is the wave's parity
   for (int it = 0; t < ntiles; t += gridDim.x, ++it) {
     const int slot = t / tiles_i, tile = t - slot * tiles_i;
-    const uint4 sl = p.slots[slot];
+    const uint4 sl = slot_of(slot);
     // the assignments of the chunk in LDS; two buffers, so this store does
     // not race the previous tile's h staging (which reads the other one)
     uint32_t* tok_a = tok_ab + (it & 1) * NT;
@@ -706,7 +752,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
           u += part[((w + 1) * NT + ti) * 16 + row];
         }
         const uint32_t a = tok_a[ti];
-        const float h = silu(g) * u * p.weights[a];
+        const float h = silu(g) * u * weight_of(slot, a);
         stage_run16(h, p.stage_h + size_t(a) * run_words(I), I, tile, RF<Q>::run_shift(tile & 15));
       }
       // the next writes of part and xs come after a barrier these lanes reach

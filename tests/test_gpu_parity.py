@@ -455,7 +455,8 @@ def test_layer_runs_decode_shapes(cuda, quant, H, E, I, k, Is, dt):
     finally:
         ops.kernel_timing(False)
     if dt == torch.float32:  # two f16 terms per run on the grouped run gate/up
-        assert gu.startswith("runs32:"), gu
+        # which selects itself when no shared expert needs the select launch
+        assert gu.startswith("runs32+select:" if Is == 0 else "runs32:"), gu
         assert dn.startswith("runs-down:"), dn
         return
     if quant == Q2_K or (quant == Q3_K and (H // 256) % 8 == 0):
@@ -730,20 +731,23 @@ def test_layer_c1_fp32_token_kernels(cuda, switches, runs):
         switches(INFERNO_DECODE_RUNS_F32="0")
     _layer_parity(cuda, "c1", 1, variants=16)
     labels, counts = _labels_of_one_step(cf.CONFIGS["c1"], cuda)
-    assert all(n == 1 for n in counts.values()), counts
-    want = ("runs32:", "runs-down:") if runs else ("tiles:", "down8:")
+    # the grouped run gate/up selects itself (no select launch)
+    assert counts == {ops.TIMER_ROUTE: 1, ops.TIMER_SELECT: 0 if runs else 1,
+                      ops.TIMER_GATE_UP: 1, ops.TIMER_DOWN: 1}, counts
+    want = ("runs32+select:", "runs-down:") if runs else ("tiles:", "down8:")
     assert labels[ops.TIMER_GATE_UP].startswith(want[0]), labels[ops.TIMER_GATE_UP]
     assert labels[ops.TIMER_DOWN].startswith(want[1]), labels[ops.TIMER_DOWN]
 
 
-@pytest.mark.parametrize("key", ["c2", "c4"])
+@pytest.mark.parametrize("key", ["c2", "c4", "c1"])
 def test_layer_decode_select_launch_variant(cuda, switches, key):
     """INFERNO_DECODE_SEL=0 keeps the separate select launch (top-k, dispatch
-    and the shared down in their own launch) on the one-token fp8 x fp4 path:
-    same oracle bound, and the same ids and weights as the default path,
-    whose gate/up launch selects; the launch labels say which ran."""
+    and the shared down in their own launch) on the one-token fp8 x fp4 path
+    (c2, c4 layer 2) and the one-fp32-token grouped run path (c1): same
+    oracle bound, and the same ids and weights as the default path, whose
+    gate/up launch selects; the launch labels say which ran."""
     cfg = cf.CONFIGS[key]
-    lt = cf.build_layer(cfg, 0 if key == "c2" else 2, cuda, max_tokens=1)
+    lt = cf.build_layer(cfg, 2 if key == "c4" else 0, cuda, max_tokens=1)
     x = cf.make_input(cfg, 1, device=cuda)
     got = {}
     for sel in ("1", "0"):
@@ -754,7 +758,8 @@ def test_layer_decode_select_launch_variant(cuda, switches, key):
         torch.cuda.synchronize()
         got[sel] = (ph.to_np(ids).copy(), ph.to_np(w).copy(), ph.to_np(out).copy())
         labels, counts = _labels_of_one_step(cfg, cuda)
-        assert labels[ops.TIMER_GATE_UP].startswith("mfma+select:" if sel == "1" else "mfma:")
+        kind = "runs32" if key == "c1" else "mfma"
+        assert labels[ops.TIMER_GATE_UP].startswith(kind + ("+select:" if sel == "1" else ":"))
         assert counts[ops.TIMER_SELECT] == (0 if sel == "1" else 1), counts
     assert np.array_equal(got["1"][0], got["0"][0])
     assert np.array_equal(got["1"][1], got["0"][1])
