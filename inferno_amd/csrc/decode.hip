@@ -678,10 +678,14 @@ int launch_down_mfma_tr(hipStream_t s, const DecodeArgs& a) {
 // Routed down for one token on the MFMA kernel (I = 2048: 8 super-block
 // columns; k <= 8 ranks). 12-row tiles when they split H into a whole
 // number of rounds of one tile per CU, else 16-row tiles.
-int launch_down_mfma(hipStream_t s, const DecodeArgs& a) {
+// Rows per tile of the Q2_K MFMA down for a layer of width H.
+int down_tile_rows(int H) {
   const int cus = device_cus();
-  if (a.H % 12 == 0 && (a.H / 12) % cus == 0 && (a.H / 16) % cus != 0)
-    return launch_down_mfma_tr<12>(s, a);
+  return (H % 12 == 0 && (H / 12) % cus == 0 && (H / 16) % cus != 0) ? 12 : 16;
+}
+
+int launch_down_mfma(hipStream_t s, const DecodeArgs& a) {
+  if (down_tile_rows(a.H) == 12) return launch_down_mfma_tr<12>(s, a);
   return launch_down_mfma_tr<16>(s, a);
 }
 
@@ -756,6 +760,18 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
                              runs_down_covers(quant, a.H, a.I, a.k);
   const bool use_mfma_down = use_q2k_down || use_runs_down;
   a.h_mfma = (use_mfma_down || use_multi) ? 1 : 0;
+  // the down launch's first tiles, warmed in L2 by the selecting gate/up
+  // launch (INFERNO_DECODE_WARM_DOWN=0: off)
+  a.dpf_rows = a.dpf_row_bytes = 0;
+  if (a.T == 1 && !switch_off("INFERNO_DECODE_WARM_DOWN")) {
+    if (use_q2k_down) {
+      a.dpf_rows = down_tile_rows(a.H);
+      a.dpf_row_bytes = a.I / kKBlock * mfma_decode::kQ2Bytes;
+    } else if (use_runs_down) {
+      a.dpf_rows = runs_down_tile_rows(quant, a.I, a.k);
+      a.dpf_row_bytes = runs_down_row_bytes(quant, a.I);
+    }
+  }
   // the shared down output ys exists only with a shared expert on that path
   if (!use_mfma_down || a.Is == 0) a.ys = nullptr;
   if (!decode_supported(a.T, a.k, a.E, a.H, a.I, a.Is, a.x_dtype, quant, quant)) {

@@ -43,6 +43,9 @@ struct DecodeArgs {
   float* ys;              // [T, H]: shared down output (MFMA down path)
   float* y;               // [T*k, H]: down rows per assignment (several-token run kernels)
   int h_mfma;             // gate/up writes h in the MFMA down layout
+  // the down launch's first tile per workgroup index (rows, bytes per row;
+  // 0: none): the selecting gate/up launch warms its XCD's L2 with it
+  int dpf_rows, dpf_row_bytes;
   // filled by launch_decode_layer
   int chunk, n_chunks, max_slots, routed_tiles;
 };
@@ -65,6 +68,9 @@ bool runs_gate_up_covers(int quant, int H, int x_dtype);
 bool runs_down_covers(int quant, int H, int I, int k);
 int launch_gate_up_runs(hipStream_t s, const DecodeArgs& a, int quant);
 int launch_down_runs(hipStream_t s, const DecodeArgs& a, int quant);
+// Rows per tile and bytes per row of the run down kernel for this layer.
+int runs_down_tile_rows(int quant, int I, int k);
+int runs_down_row_bytes(int quant, int I);
 // The same kernels for T > 1 tokens (no shared expert): gate/up per expert
 // tile for all of the expert's tokens, down rows per assignment into a.y.
 bool runs_multi_covers(int quant, int H, int I, int x_dtype);

@@ -499,9 +499,29 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
     }
   }
   if constexpr (SEL) {
+    // The down launch's workgroup of this index (on the same XCD) starts
+    // with its tile blockIdx.x: its rows of the k selected experts, known
+    // here, are copied by the LDS DMA into the free x area (the data is not
+    // used; the copy leaves them in this XCD's L2; every wavefront writes
+    // the same first KB, stage_words(H) >= 256 words) while the shared down
+    // below computes. Issued after every load this kernel waits for.
+    auto warm_down = [&]() {
+      if (!p.dpf_rows || int(blockIdx.x) >= p.H / p.dpf_rows) return;  // uniform
+      const size_t rbd = size_t(p.dpf_row_bytes);
+      const int cr = int(size_t(p.dpf_rows) * rbd / 16), nc = p.k * cr;
+      uint8_t* dst = reinterpret_cast<uint8_t*>(xs);  // every wavefront: the x area's first KB
+      for (int b = wave * kWave; b < nc; b += kThreads) {
+        const int i = min(b + lane, nc - 1), r = i / cr, w = i - r * cr;
+        const u32x4* src = reinterpret_cast<const u32x4*>(
+            p.down + size_t(slot_e[r]) * p.down_stride + size_t(blockIdx.x) * p.dpf_rows * rbd) + w;
+        __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) const void*)src,
+                                         (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+      }
+    };
     // the shared down of rows [sd_row0, sd_row0 + sd_rows): the rows (in v
     // since the last tile's barrier) to the free tile area, dot products
     // against the shared h formed in the prologue, parts summed in order
+    if (!sd_rows) warm_down();
     if (sd_rows) {
       const int nc = int(size_t(sd_rows) * SharedDownSlice::row_bytes(p.Is) / 16);
 #pragma unroll
@@ -510,6 +530,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
         if (i < nc) reinterpret_cast<u32x4*>(tl)[i] = v[j];
       }
       __syncthreads();
+      warm_down();
       if (wave < (sd_rows / 8) * kSdWpo)
         SharedDownSlice::dot(p, reinterpret_cast<const uint32_t*>(tl), hsd, wave, sdpart);
       __syncthreads();

@@ -165,6 +165,32 @@ int launch_gate_up_runs(hipStream_t s, const DecodeArgs& a, int quant) {
   }
 }
 
+int runs_down_tile_rows(int quant, int I, int k) {
+  auto pick = [&](auto q_c) {
+    constexpr int Q = decltype(q_c)::value;
+    switch (I / kKBlock) {
+      case 3: return down_tr_fits<Q, 3, 16>(k) ? 16 : 8;
+      case 4: return down_tr_fits<Q, 4, 16>(k) ? 16 : 8;
+      case 6: return down_tr_fits<Q, 6, 16>(k) ? 16 : 8;
+      default: return down_tr_fits<Q, 8, 16>(k) ? 16 : 8;
+    }
+  };
+  switch (quant) {
+    case INFERNO_Q2_K: return pick(std::integral_constant<int, INFERNO_Q2_K>{});
+    case INFERNO_Q3_K: return pick(std::integral_constant<int, INFERNO_Q3_K>{});
+    default: return pick(std::integral_constant<int, INFERNO_Q4_K>{});
+  }
+}
+
+int runs_down_row_bytes(int quant, int I) {
+  const int NB = I / kKBlock;
+  switch (quant) {
+    case INFERNO_Q2_K: return NB * RF<INFERNO_Q2_K>::kBytes;
+    case INFERNO_Q3_K: return NB * RF<INFERNO_Q3_K>::kBytes;
+    default: return NB * RF<INFERNO_Q4_K>::kBytes;
+  }
+}
+
 int launch_down_runs(hipStream_t s, const DecodeArgs& a, int quant) {
   switch (quant) {
     case INFERNO_Q2_K: return down_q<INFERNO_Q2_K>(s, a);

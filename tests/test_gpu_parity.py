@@ -787,6 +787,34 @@ def test_layer_decode_shared_expert_alone(cuda, switches, sel):
     _layer_parity(cuda, cfg, 1, variants=4, tol=1e-3)
 
 
+@pytest.mark.parametrize("key", ["c2", "c4", "small"])
+def test_layer_decode_warm_down_has_no_effect_on_results(cuda, switches, key):
+    """The selecting gate/up launch warms L2 with the down launch's first
+    tiles through the LDS DMA into its free x area (data unused there): the
+    outputs must be bitwise those of INFERNO_DECODE_WARM_DOWN=0, on c2
+    (Q2_K MFMA down), c4 layer 2 (Q3_K run down) and a 1024-wide layer whose
+    x area is the smallest (4 KB)."""
+    if key == "small":
+        cfg = cf.Config("warm_small_h1024", 27, 1024, 16, 2048, 4, (cf.Q2_K,), cf.SCORE_SIGMOID,
+                        True, 2.5, 0.1, 256, torch.bfloat16, (1,))
+    else:
+        cfg = cf.CONFIGS[key]
+    lt = cf.build_layer(cfg, 2 if key == "c4" else 0, cuda, max_tokens=1)
+    inputs = [(cf.make_input(cfg, 1, variant=v, device=cuda), torch.randn(1, cfg.hidden, device=cuda))
+              for v in range(3)]
+    got = {}
+    for warm in ("1", "0"):
+        switches(INFERNO_DECODE_WARM_DOWN=warm)
+        outs = []
+        for x, residual in inputs:
+            outs.append(ph.to_np(lt.layer.forward(x, residual)).copy())
+        torch.cuda.synchronize()
+        got[warm] = outs
+    for a, b in zip(got["1"], got["0"]):
+        assert np.isfinite(a).all()
+        assert np.array_equal(a, b)
+
+
 def test_kernel_timing_hook_counts_decode_launches(cuda):
     """The measurement hook: events recorded around each timed launch without
     waiting, summed when read; two decode steps give two launches per timer,
