@@ -760,11 +760,14 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
                              runs_down_covers(quant, a.H, a.I, a.k);
   const bool use_mfma_down = use_q2k_down || use_runs_down;
   a.h_mfma = (use_mfma_down || use_multi) ? 1 : 0;
-  // the down launch's first tiles, warmed in L2 by the selecting gate/up
-  // launch (INFERNO_DECODE_WARM_DOWN=0: off)
+  // the run down's first tiles, warmed in L2 by the selecting gate/up
+  // launch (INFERNO_DECODE_WARM_DOWN=0: off; =2: also before the Q2_K MFMA
+  // down, where the gate/up launch's longer end ate the gain: c2 49.2
+  // against 48.9 µs)
   a.dpf_rows = a.dpf_row_bytes = 0;
+  const char* warm_env = std::getenv("INFERNO_DECODE_WARM_DOWN");
   if (a.T == 1 && !switch_off("INFERNO_DECODE_WARM_DOWN")) {
-    if (use_q2k_down) {
+    if (use_q2k_down && warm_env && warm_env[0] == '2') {
       a.dpf_rows = down_tile_rows(a.H);
       a.dpf_row_bytes = a.I / kKBlock * mfma_decode::kQ2Bytes;
     } else if (use_runs_down) {
