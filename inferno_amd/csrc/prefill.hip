@@ -148,19 +148,28 @@ struct Frag<INFERNO_Q3_K> {
       const uint32_t hs = hshift >= 2 ? (h >> (hshift - 2)) : (h << (2 - hshift));
       return (qs & 0x03030303u) | (hs & ~0x03030303u);
     };
-    const uint32_t w0 = field3((s & 1) ? r[2] : r[0], (s & 1) ? r[6] : r[4]);
-    const uint32_t w1 = field3((s & 1) ? r[3] : r[1], (s & 1) ? r[7] : r[5]);
-    // the four 6-bit scales of this chunk, one per byte, then byte s as an
-    // f16 subnormal s6 * 2^-24; dl = d (s6 - 32): mult = dl 2^24 and
-    // off = -4 dl are each one v_fma_mix_f32 with an fp32 addend, rounded
-    // once as d * float(s6 - 32) is
+    const uint32_t w0 = field3((s & 1) ? r[2] : r[0], (s & 1) ? r[6] : r[4]) & 0x07070707u;
+    const uint32_t w1 = field3((s & 1) ? r[3] : r[1], (s & 1) ? r[7] : r[5]) & 0x07070707u;
+    // the group's 6-bit scale (byte s of this chunk's four) and dl = d (s6 -
+    // 32) in f16, as the reference's half dequantisation forms it (the fp32
+    // product of two f16 values is exact, so one rounding)
     const uint32_t lo = QC < 2 ? (r[8] & 0x0f0f0f0fu) : ((r[8] >> 4) & 0x0f0f0f0fu);
     const uint32_t s6 = lo | (((r[9] >> (2 * QC)) & 0x03030303u) << 4);
-    const uint32_t f6 = ((s & 1) ? (s6 >> 8) : s6) & 0x00ff00ffu;
+    const int sc = int((s6 >> (8 * ((s & 1) + 2 * (s >> 1)))) & 0xffu);
     const float d = f16_bits_to_f32_fast(uint16_t(r[10]));
-    const float mult = mix_mul(f6, s >> 1, __builtin_amdgcn_ldexpf(d, 48), -32.0f * __builtin_amdgcn_ldexpf(d, 24));
-    const float off = mix_mul(f6, s >> 1, -4.0f * __builtin_amdgcn_ldexpf(d, 24), 128.0f * d);
-    return dequant8(w0, w1, 0x00070007u, mult, off);
+    const _Float16 dlh = (_Float16)(d * float(sc - 32));
+    const half2v dl2 = {dlh, dlh};
+    const half2v m4 = {(_Float16)-1028.0f, (_Float16)-1028.0f};
+    // q + 4 hbit (0..7) in the low mantissa byte under the f16 exponent of
+    // 1024 (byte 0x64 above it, one v_perm per pair): 1024 + u, exactly;
+    // minus 1028 is u - 4 exactly, times dl rounds once. Pairs (bytes 0, 2)
+    // and (1, 3): value order 0 2 1 3 4 6 5 7.
+    auto pair = [&](uint32_t w, uint32_t sel) {
+      const half2v f = as_h2(__builtin_amdgcn_perm(0x64646464u, w, sel));
+      return as_u32((f + m4) * dl2);
+    };
+    return __builtin_bit_cast(half8, make_uint4(pair(w0, 0x04020400u), pair(w0, 0x04030401u),
+                                                pair(w1, 0x04020400u), pair(w1, 0x04030401u)));
   }
 };
 
