@@ -108,7 +108,10 @@ __device__ __forceinline__ void topk_row_wave(const float* row, const float* __r
     uint32_t cnt = 0;
 #pragma unroll
     for (int j = 0; j < PER; ++j) cnt += uint32_t(__popcll(__ballot(rk[j] >= cand)));
-    if (cnt >= uint32_t(k)) kth = cand;
+    if (cnt >= uint32_t(k)) {
+      kth = cand;
+      if (cnt == uint32_t(k)) break;  // exactly the k winners are at or above kth
+    }
   }
   // the selected candidates, gathered in lane order into lanes 0..k-1
   // (source lanes are wavefront-uniform: readlane, no LDS round trips)
@@ -234,14 +237,21 @@ __device__ __forceinline__ void topk1_wave(const float (&lgin)[4], const float (
   // K: the largest value with at least k keys at or above it, one bit per
   // step from the top (four ballot counts each; measured faster than two
   // bits per step, whose extra compares each cost a VALU -> SGPR round trip)
+  // The search stops as soon as exactly k keys are at or above the prefix
+  // found so far: those k are the winners whatever the remaining bits of K
+  // (with distinct-ish keys that is after ~log2(E) + a few steps, not 32);
+  // kth is then a lower bound of K that no loser reaches, which the winner
+  // rule below handles as it does K itself.
   uint32_t kth = 0;
-#pragma unroll 4
   for (int b = 31; b >= 0; --b) {
     const uint32_t c = kth | (1u << b);
     uint32_t n = 0;
 #pragma unroll
     for (int j = 0; j < PER; ++j) n += uint32_t(__popcll(__ballot(key[j] >= c)));
-    kth = n >= uint32_t(k) ? c : kth;
+    if (n >= uint32_t(k)) {
+      kth = c;
+      if (n == uint32_t(k)) break;  // uniform
+    }
   }
   // winners: keys above K, then the lowest ids among keys equal to K
   uint32_t above = 0;
