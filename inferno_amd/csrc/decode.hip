@@ -626,22 +626,16 @@ int launch_gate_up_mfma(hipStream_t s, const DecodeArgs& a0, int quant, bool sel
 
 // The selection (and the shared down) in the fp8 x fp4 gate/up launch: one
 // token, at most three shared-down octets per workgroup (kSdWpo wavefronts
-// each, one 256-value unit per lane), staged through the tile registers and
-// tile area; INFERNO_DECODE_SEL=0 keeps the select launch.
+// each, one 256-value unit per lane, each wavefront's rows copied to its own
+// LDS area during the selection); INFERNO_DECODE_SEL=0 keeps the select launch.
 bool sel_in_gate_up(const DecodeArgs& a, bool shared_down_here) {
   if (a.T != 1 || switch_off("INFERNO_DECODE_SEL")) return false;
   const int ntiles = a.max_slots * (a.I / kRows);
   const int grid = std::min(ntiles, device_cus());
   if (!shared_down_here) return true;
-  // the workgroup's rows (whole octets) fit the tile registers and area
-  const int NB = a.H / kKBlock, kB = mfma_decode::fp4_block_bytes(a.xr_quant);
-  const int rw = 8 * ((a.H / 8 + grid - 1) / grid);
-  const size_t sd_bytes = size_t(rw) * size_t(a.Is / 32) * 34;
-  const size_t tile_regs = size_t(mfma_decode::chunks_per_thread(NB, kB)) * mfma_decode::kThreads * 16;
-  const size_t tile_lds = size_t(2 * 16) * size_t(NB * kB + mfma_decode::kRowPad);
+  const int rw = 8 * ((a.H / 8 + grid - 1) / grid);  // the workgroup's rows, whole octets
   return a.Is % kKBlock == 0 && a.Is <= 2 * kKBlock * kSdWpo && a.H % 8 == 0 &&
-         rw <= 8 * kSdMaxOctets && sd_bytes <= tile_regs && sd_bytes <= tile_lds &&
-         mfma_decode::lds_bytes(a.H, a.xr_quant, a.Is) <= 160 * 1024;
+         rw <= 8 * kSdMaxOctets && mfma_decode::lds_bytes(a.H, a.xr_quant, a.Is) <= 160 * 1024;
 }
 
 template <int TR, int PER>

@@ -249,6 +249,8 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
   Top1Lds* tk = reinterpret_cast<Top1Lds*>(slot_w + kMaxExperts);
   float* sdpart = reinterpret_cast<float*>(tk + 1);  // [wave][8] shared down parts (SEL)
   uint32_t* hsd = reinterpret_cast<uint32_t*>(sdpart + kWaves * 8);  // shared h (SEL)
+  // shared down rows (SEL), kWaveLds bytes per wavefront, 16-byte aligned
+  uint32_t* sdl = smem + ((int(hsd - smem) + int(staged_stride(p.Is, false)) + 3) & ~3);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, q = lane >> 4;
@@ -282,13 +284,22 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
       if (blockIdx.x == 0) select1_write(p, tk);
     } else {
       constexpr int kT = kSelWave * kWave;  // threads of the other wavefronts
-      if (sd_rows) form_shared_h<kT>(p, hsd, tid);  // used after the routed tiles
+      if (sd_rows) form_shared_h<kT>(p, hsd, tid);
       for (int i = tid; i < Sm / 4; i += kT)
         reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(p.stage_xm)[i];
       if (tid < 4) zero[tid] = 0;
+      // the shared down rows this wavefront dots, copied to LDS while the
+      // selection runs (HBM is idle until the first routed tile is known)
+      if (wave < (sd_rows / 8) * kSdWpo)
+        SharedDownSlice::fetch_lds(p, sdl + wave * (SharedDownSlice::kWaveLds / 4), wave, sd_row0);
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wavefront's copies are in LDS
     }
     __syncthreads();
     if (t < ntiles) fetch_tile<PER>(v, p, tiles_i, rb, t, slot_e[t / tiles_i]);
+    // the shared down, while the first routed tile's loads are in flight;
+    // its parts are summed into ys after the next barrier
+    if (wave < (sd_rows / 8) * kSdWpo)
+      SharedDownSlice::dot_lds(p, sdl + wave * (SharedDownSlice::kWaveLds / 4), hsd, wave, sdpart);
   } else {
     if (t < ntiles) fetch_tile<PER>(v, p, tiles_i, rb, t, p.slots[t / tiles_i].x);
     for (int i = tid; i < Sm / 4; i += kThreads)
@@ -342,21 +353,11 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
       }
     }
     __syncthreads();
-    if (t + int(gridDim.x) < ntiles) {
+    if (t + int(gridDim.x) < ntiles)
       fetch_tile<PER>(v, p, tiles_i, rb, t + gridDim.x, slot_e[(t + gridDim.x) / tiles_i]);
-    } else if constexpr (SEL) {
-      // after the last routed tile: this workgroup's shared down rows,
-      // contiguous, in flight while the tile is computed
-      if (sd_rows) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(
-            p.sdown + size_t(sd_row0) * SharedDownSlice::row_bytes(p.Is));
-        const int nc = int(size_t(sd_rows) * SharedDownSlice::row_bytes(p.Is) / 16);
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-          const int i = j * kThreads + tid;
-          v[j] = src[i < nc ? i : nc - 1];
-        }
-      }
+    if constexpr (SEL) {  // once: the shared down parts (written before this barrier)
+      if (sd_rows && tid < sd_rows) SharedDownSlice::store(p, sdpart, tid, sd_row0);
+      sd_rows = 0;
     }
     const int slot = t / tiles_i, tile = t - slot * tiles_i;
     float acc[2] = {0.f, 0.f};
@@ -503,8 +504,8 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
     // with its tile blockIdx.x: its rows of the k selected experts, known
     // here, are copied by the LDS DMA into the free x area (the data is not
     // used; the copy leaves them in this XCD's L2; every wavefront writes
-    // the same first KB, stage_words(H) >= 256 words) while the shared down
-    // below computes. Issued after every load this kernel waits for.
+    // the same first KB, stage_words(H) >= 256 words). Issued after every
+    // load this kernel waits for.
     auto warm_down = [&]() {
       if (!p.dpf_rows || int(blockIdx.x) >= p.H / p.dpf_rows) return;  // uniform
       const size_t rbd = size_t(p.dpf_row_bytes);
@@ -518,21 +519,9 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
                                          (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
       }
     };
-    // the shared down of rows [sd_row0, sd_row0 + sd_rows): the rows (in v
-    // since the last tile's barrier) to the free tile area, dot products
-    // against the shared h formed in the prologue, parts summed in order
-    if (!sd_rows) warm_down();
+    warm_down();
+    // a workgroup without routed tiles sums its shared down parts here
     if (sd_rows) {
-      const int nc = int(size_t(sd_rows) * SharedDownSlice::row_bytes(p.Is) / 16);
-#pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        const int i = j * kThreads + tid;
-        if (i < nc) reinterpret_cast<u32x4*>(tl)[i] = v[j];
-      }
-      __syncthreads();
-      warm_down();
-      if (wave < (sd_rows / 8) * kSdWpo)
-        SharedDownSlice::dot(p, reinterpret_cast<const uint32_t*>(tl), hsd, wave, sdpart);
       __syncthreads();
       if (tid < sd_rows) SharedDownSlice::store(p, sdpart, tid, sd_row0);
     }
@@ -703,7 +692,9 @@ inline size_t lds_bytes(int H, int quant = INFERNO_Q2_K, int Is_sel = 0) {
   const int rb = H / kKBlock * fp4_block_bytes(quant);
   return size_t(stage_words(H) + 4) * 4 + size_t(2 * 16) * (rb + kRowPad) +
          size_t(kWaves * 2 * 16) * 4 + size_t(3 * kMaxExperts) * 4 + sizeof(Top1Lds) +
-         size_t(kWaves * 8) * 4 + size_t(staged_stride(Is_sel, false)) * 4;
+         size_t(kWaves * 8) * 4 +
+         size_t(staged_stride(Is_sel, false)) * 4 +
+         (Is_sel ? 12 + size_t(kSdMaxOctets * kSdWpo * SharedDownSlice::kWaveLds) : 0);
 }
 
 }  // namespace mfma_decode

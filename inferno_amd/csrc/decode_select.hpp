@@ -188,6 +188,52 @@ struct SharedDownSlice {
     acc += __shfl_xor(acc, 32, kWave);
     if ((lane & 35) == 0) part[w * 8 + r] = acc;
   }
+  // The same dot with the wavefront's own rows in LDS, copied there by
+  // fetch_lds: row r of the octet at r * nu units (nu = units(w, Is)).
+  __device__ __forceinline__ static int units(int w, int Is) {
+    return max(0, min(2, Is / kKBlock - 2 * (w % kSdWpo)));
+  }
+  __device__ __forceinline__ static void dot_lds(const DecodeArgs& p, const uint32_t* wrows,
+                                                 const uint32_t* xss, int w, float* part) {
+    const int lane = threadIdx.x & 63;
+    const int r = (lane >> 2) & 7, sub = lane & 3, cp = lane >> 5;
+    const int Is = p.Is, nu = units(w, Is), q = cp + 2 * (w % kSdWpo);
+    float acc = 0.f;
+    if (cp < nu) {
+      const uint32_t* src = wrows + (size_t(r * nu + cp) * FS::kBytes + size_t(sub) * 68) / 4;
+      uint32_t raw[FS::kDw];
+#pragma unroll
+      for (int i = 0; i < FS::kDw; ++i) raw[i] = src[i];
+      acc = FS::dot(raw, sub, xrow_at<false>(xss, Is, q));
+    }
+    acc += __shfl_xor(acc, 1, kWave);
+    acc += __shfl_xor(acc, 2, kWave);
+    acc += __shfl_xor(acc, 32, kWave);
+    if ((lane & 35) == 0) part[w * 8 + r] = acc;
+  }
+  // LDS bytes per wavefront for fetch_lds: 8 rows x 2 units
+  static constexpr int kWaveLds = 8 * 2 * FS::kBytes;
+  // Wavefront w's rows of its octet (its units only) into wrows by the LDS
+  // DMA (64 consecutive 16-byte chunks per copy, counted in vmcnt; the
+  // caller waits). The last copy ends at the last chunk (it starts inside
+  // the previous one: those chunks are written twice with the same bytes).
+  __device__ __forceinline__ static void fetch_lds(const DecodeArgs& p, uint32_t* wrows, int w,
+                                                   int row0) {
+    const int lane = threadIdx.x & 63, Is = p.Is, nu = units(w, Is);
+    if (nu == 0) return;  // uniform
+    const int cpr = nu * (FS::kBytes / 16), nch = 8 * cpr;  // 16-byte chunks
+    const uint8_t* base = p.sdown + size_t(row0 + (w / kSdWpo) * 8) * row_bytes(Is) +
+                          size_t(2 * (w % kSdWpo)) * FS::kBytes;
+    static_assert(8 * (FS::kBytes / 16) >= kWave, "one copy fits a one-unit octet");
+    for (int b0 = 0; b0 < nch; b0 += kWave) {
+      const int b = min(b0, nch - kWave), c = b + lane, r = c / cpr, cc = c - r * cpr;
+      const uint8_t* src = base + size_t(r) * row_bytes(Is) + size_t(cc) * 16;
+      __builtin_amdgcn_global_load_lds(
+          (__attribute__((address_space(1))) const void*)src,
+          (__attribute__((address_space(3))) void*)(reinterpret_cast<uint8_t*>(wrows) + b * 16), 16,
+          0, 0);
+    }
+  }
   // thread i < nrows: row row0 + i
   __device__ __forceinline__ static void store(const DecodeArgs& p, const float* part, int i,
                                                int row0) {
