@@ -586,7 +586,7 @@ int launch_gate_up_mfma_nb(hipStream_t s, const DecodeArgs& a, int ntiles) {
     attr = true;
   }
   const unsigned grid = unsigned(std::min(ntiles, device_cus()));
-  kern<<<grid, mfma_decode::kThreads, mfma_decode::lds_bytes(a.H, Q, SEL ? a.Is : 0), s>>>(a, ntiles);
+  kern<<<grid, mfma_decode::kThreads, mfma_decode::lds_bytes(a.H, Q, SEL, (a.Is && a.ys) ? a.Is : 0), s>>>(a, ntiles);
   INF_LAUNCHED();
   return INFERNO_OK;
 }
@@ -632,10 +632,10 @@ bool sel_in_gate_up(const DecodeArgs& a, bool shared_down_here) {
   if (a.T != 1 || switch_off("INFERNO_DECODE_SEL")) return false;
   const int ntiles = a.max_slots * (a.I / kRows);
   const int grid = std::min(ntiles, device_cus());
-  if (!shared_down_here) return true;
+  if (!shared_down_here) return mfma_decode::lds_bytes(a.H, a.xr_quant, true, 0) <= 160 * 1024;
   const int rw = 8 * ((a.H / 8 + grid - 1) / grid);  // the workgroup's rows, whole octets
   return a.Is % kKBlock == 0 && a.Is <= 2 * kKBlock * kSdWpo && a.H % 8 == 0 &&
-         rw <= 8 * kSdMaxOctets && mfma_decode::lds_bytes(a.H, a.xr_quant, a.Is) <= 160 * 1024;
+         rw <= 8 * kSdMaxOctets && mfma_decode::lds_bytes(a.H, a.xr_quant, true, a.Is) <= 160 * 1024;
 }
 
 template <int TR, int PER>
@@ -754,14 +754,11 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
                              runs_down_covers(quant, a.H, a.I, a.k);
   const bool use_mfma_down = use_q2k_down || use_runs_down;
   a.h_mfma = (use_mfma_down || use_multi) ? 1 : 0;
-  // the run down's first tiles, warmed in L2 by the selecting gate/up
-  // launch (INFERNO_DECODE_WARM_DOWN=0: off; =2: also before the Q2_K MFMA
-  // down, where the gate/up launch's longer end ate the gain: c2 49.2
-  // against 48.9 µs)
+  // the down launch's first tiles, warmed in L2 by the selecting gate/up
+  // launch under its last routed tile (INFERNO_DECODE_WARM_DOWN=0: off)
   a.dpf_rows = a.dpf_row_bytes = 0;
-  const char* warm_env = std::getenv("INFERNO_DECODE_WARM_DOWN");
   if (a.T == 1 && !switch_off("INFERNO_DECODE_WARM_DOWN")) {
-    if (use_q2k_down && warm_env && warm_env[0] == '2') {
+    if (use_q2k_down) {
       a.dpf_rows = down_tile_rows(a.H);
       a.dpf_row_bytes = a.I / kKBlock * mfma_decode::kQ2Bytes;
     } else if (use_runs_down) {

@@ -250,7 +250,8 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
   float* sdpart = reinterpret_cast<float*>(tk + 1);  // [wave][8] shared down parts (SEL)
   uint32_t* hsd = reinterpret_cast<uint32_t*>(sdpart + kWaves * 8);  // shared h (SEL)
   // shared down rows (SEL), kWaveLds bytes per wavefront, 16-byte aligned
-  uint32_t* sdl = smem + ((int(hsd - smem) + int(staged_stride(p.Is, false)) + 3) & ~3);
+  const int is_sd = (SEL && p.Is && p.ys) ? p.Is : 0;  // shared down in this launch
+  uint32_t* sdl = smem + ((int(hsd - smem) + int(staged_stride(is_sd, false)) + 3) & ~3);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, q = lane >> 4;
@@ -343,6 +344,33 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
   const bool term0 = q < 2;
   const float* sums = reinterpret_cast<const float*>(xs + H);
   const int* e1s = reinterpret_cast<const int*>(xs + H + H / 16);
+  // SEL: the down launch's workgroup of this index (on the same XCD) starts
+  // with its tile blockIdx.x. Its rows of the k selected experts are copied
+  // by the LDS DMA into the first KB of the shared down area (free once the
+  // shared down is dotted; the data is not used, the copy leaves the rows in
+  // this XCD's L2), issued when the last routed tile is in LDS so that the
+  // copies complete under its compute. Written as asm so that the compiler
+  // does not make the tile's LDS reads wait for them; the in-order vmcnt
+  // only makes its waits for older loads longer, and the kernel waits for
+  // the copies before it ends.
+  bool warmed = false;
+  auto warm_down = [&]() {
+    warmed = true;
+    if (!p.dpf_rows || int(blockIdx.x) >= p.H / p.dpf_rows) return;  // uniform
+    const size_t rbd = size_t(p.dpf_row_bytes);
+    const int cr = int(size_t(p.dpf_rows) * rbd / 16), nc = p.k * cr;
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(
+        uint32_t(size_t((__attribute__((address_space(3))) uint32_t*)sdl)));
+    for (int b = wave * kWave; b < nc; b += kThreads) {
+      const int i = min(b + lane, nc - 1), r = i / cr, w = i - r * cr;
+      const u32x4* src = reinterpret_cast<const u32x4*>(
+          p.down + size_t(slot_e[r]) * p.down_stride + size_t(blockIdx.x) * p.dpf_rows * rbd) + w;
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                   :
+                   : "s"(dst), "v"(src)
+                   : "memory", "m0");
+    }
+  };
   for (; t < ntiles; t += gridDim.x) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
@@ -358,6 +386,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
     if constexpr (SEL) {  // once: the shared down parts (written before this barrier)
       if (sd_rows && tid < sd_rows) SharedDownSlice::store(p, sdpart, tid, sd_row0);
       sd_rows = 0;
+      if (t + int(gridDim.x) >= ntiles) warm_down();
     }
     const int slot = t / tiles_i, tile = t - slot * tiles_i;
     float acc[2] = {0.f, 0.f};
@@ -500,31 +529,14 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
     }
   }
   if constexpr (SEL) {
-    // The down launch's workgroup of this index (on the same XCD) starts
-    // with its tile blockIdx.x: its rows of the k selected experts, known
-    // here, are copied by the LDS DMA into the free x area (the data is not
-    // used; the copy leaves them in this XCD's L2; every wavefront writes
-    // the same first KB, stage_words(H) >= 256 words). Issued after every
-    // load this kernel waits for.
-    auto warm_down = [&]() {
-      if (!p.dpf_rows || int(blockIdx.x) >= p.H / p.dpf_rows) return;  // uniform
-      const size_t rbd = size_t(p.dpf_row_bytes);
-      const int cr = int(size_t(p.dpf_rows) * rbd / 16), nc = p.k * cr;
-      uint8_t* dst = reinterpret_cast<uint8_t*>(xs);  // every wavefront: the x area's first KB
-      for (int b = wave * kWave; b < nc; b += kThreads) {
-        const int i = min(b + lane, nc - 1), r = i / cr, w = i - r * cr;
-        const u32x4* src = reinterpret_cast<const u32x4*>(
-            p.down + size_t(slot_e[r]) * p.down_stride + size_t(blockIdx.x) * p.dpf_rows * rbd) + w;
-        __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) const void*)src,
-                                         (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
-      }
-    };
-    warm_down();
+    if (!warmed) warm_down();
     // a workgroup without routed tiles sums its shared down parts here
     if (sd_rows) {
       __syncthreads();
       if (tid < sd_rows) SharedDownSlice::store(p, sdpart, tid, sd_row0);
     }
+    // the warm-up copies are not tracked by the compiler's wait counts
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
   }
 }
 
@@ -688,13 +700,16 @@ inline bool covers_width(int H) {
   return H % kKBlock == 0 && NB % 4 == 0 && NB >= 4 && NB <= 28;
 }
 
-inline size_t lds_bytes(int H, int quant = INFERNO_Q2_K, int Is_sel = 0) {
+// sel: the selecting launch; Is_sd: the shared expert's width when its down
+// runs in that launch, else 0
+inline size_t lds_bytes(int H, int quant = INFERNO_Q2_K, bool sel = false, int Is_sd = 0) {
   const int rb = H / kKBlock * fp4_block_bytes(quant);
   return size_t(stage_words(H) + 4) * 4 + size_t(2 * 16) * (rb + kRowPad) +
          size_t(kWaves * 2 * 16) * 4 + size_t(3 * kMaxExperts) * 4 + sizeof(Top1Lds) +
          size_t(kWaves * 8) * 4 +
-         size_t(staged_stride(Is_sel, false)) * 4 +
-         (Is_sel ? 12 + size_t(kSdMaxOctets * kSdWpo * SharedDownSlice::kWaveLds) : 0);
+         (sel ? size_t(staged_stride(Is_sd, false)) * 4 + 12 +
+                    (Is_sd ? size_t(kSdMaxOctets * kSdWpo * SharedDownSlice::kWaveLds) : 1024)
+              : 0);
 }
 
 }  // namespace mfma_decode

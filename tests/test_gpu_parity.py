@@ -787,32 +787,36 @@ def test_layer_decode_shared_expert_alone(cuda, switches, sel):
     _layer_parity(cuda, cfg, 1, variants=4, tol=1e-3)
 
 
-@pytest.mark.parametrize("key", ["c2", "c4", "small"])
+@pytest.mark.parametrize("key", ["c2", "c4", "small", "small_noshared"])
 def test_layer_decode_warm_down_has_no_effect_on_results(cuda, switches, key):
     """The selecting gate/up launch warms L2 with the down launch's first
-    tiles through the LDS DMA into its free x area (data unused there): the
-    outputs must be bitwise those of INFERNO_DECODE_WARM_DOWN=0, on c2
-    (Q2_K MFMA down), c4 layer 2 (Q3_K run down) and a 1024-wide layer whose
-    x area is the smallest (4 KB)."""
-    if key == "small":
-        cfg = cf.Config("warm_small_h1024", 27, 1024, 16, 2048, 4, (cf.Q2_K,), cf.SCORE_SIGMOID,
-                        True, 2.5, 0.1, 256, torch.bfloat16, (1,))
+    tiles through the LDS DMA into a KB of LDS nothing reads afterwards (the
+    shared down's area, or a KB of its own without a shared expert), under
+    its last routed tile: the outputs must be bitwise those of
+    INFERNO_DECODE_WARM_DOWN=0, on c2 (Q2_K MFMA down), c4 layer 2 (Q3_K run
+    down) and a 1024-wide layer with and without a shared expert."""
+    if key.startswith("small"):
+        cfg = cf.Config("warm_" + key, 27, 1024, 16, 2048, 4, (cf.Q2_K,), cf.SCORE_SIGMOID,
+                        True, 2.5, 0.1, 0 if key.endswith("noshared") else 256, torch.bfloat16, (1,))
     else:
         cfg = cf.CONFIGS[key]
     lt = cf.build_layer(cfg, 2 if key == "c4" else 0, cuda, max_tokens=1)
     inputs = [(cf.make_input(cfg, 1, variant=v, device=cuda), torch.randn(1, cfg.hidden, device=cuda))
               for v in range(3)]
     got = {}
-    for warm in ("2", "0"):  # 2: the Q2_K MFMA down too
+    for warm in ("1", "0"):
         switches(INFERNO_DECODE_WARM_DOWN=warm)
         outs = []
         for x, residual in inputs:
             outs.append(ph.to_np(lt.layer.forward(x, residual)).copy())
         torch.cuda.synchronize()
         got[warm] = outs
-    for a, b in zip(got["2"], got["0"]):
+    for a, b in zip(got["1"], got["0"]):
         assert np.isfinite(a).all()
         assert np.array_equal(a, b)
+    if key != "c4":  # layer 0's launches; c4's layer 2 is checked by the c4 label tests
+        labels, _ = _labels_of_one_step(cfg, cuda)
+        assert labels[ops.TIMER_GATE_UP].startswith("mfma+select:")
 
 
 def test_kernel_timing_hook_counts_decode_launches(cuda):
