@@ -551,13 +551,21 @@ bool mfma_enabled() {
   return !switch_off("INFERNO_DECODE_MFMA");
 }
 
-// K parts of the shared gate/up on the MFMA path: the largest of 4, 3, 2
-// dividing the super-block columns.
-int shared_parts(int H) {
-  const int cols = H / kKBlock;
-  for (int k = 4; k > 1; --k)
-    if (cols % k == 0) return k;
-  return 1;
+// K parts of the shared gate/up on the MFMA path: the fewest parts (each
+// re-read of the partial sums costs the gate/up prologue) that divide the
+// super-block columns and give the route launch at least two shared
+// workgroups per CU (16-row tiles x parts), else the most that divide them,
+// at most kMaxSharedParts. c2 (Is 2048, 24 columns): 4; c4 (Is 1536, 16
+// columns): 8, measured 2.8 us per 4-layer step faster than 4.
+int shared_parts(int H, int Is) {
+  const int cols = H / kKBlock, tiles = Is / kRows, want = 2 * std::max(device_cus(), 1);
+  int best = 1;
+  for (int k = 2; k <= kMaxSharedParts; ++k) {
+    if (cols % k) continue;
+    best = k;
+    if (tiles * k >= want) return k;
+  }
+  return best;
 }
 
 // The fp8 x fp4 gate/up: one bf16 token, Q2_K (NB a multiple of 4, 4..28)
@@ -687,7 +695,8 @@ int launch_down_mfma(hipStream_t s, const DecodeArgs& a) {
 
 size_t decode_mfma_stage_words(size_t H) { return size_t(mfma_decode::stage_words(int(H))); }
 size_t decode_shared_partial_floats(size_t H, size_t Is) {
-  return size_t(shared_parts(int(H))) * 2 * Is;
+  (void)H;  // room for the most parts any shape takes
+  return size_t(kMaxSharedParts) * 2 * Is;
 }
 
 bool decode_supported(size_t T, size_t k, size_t E, size_t H, size_t I, size_t Is, int x_dtype,
@@ -739,7 +748,7 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   const bool use_mfma = use_fp4 || use_runs || use_runs32;
   // with a matrix-core gate/up the shared expert's gate/up runs in the route
   // launch and stages its own x; otherwise x is staged for the tile kernels
-  a.shared_parts = shared_parts(a.H);
+  a.shared_parts = shared_parts(a.H, a.Is);
   if (use_mfma || use_multi) a.stage_x = nullptr;
   if (!use_fp4) a.stage_xm = nullptr;
   if (!use_runs && !use_runs32 && !use_multi) a.stage_xr = nullptr;

@@ -81,14 +81,15 @@ __device__ __forceinline__ void load_logits1(const DecodeArgs& p, float (&lg)[4]
 // run's maximum, its sum in value order (as stage_run forms it) and the hi
 // pair words 2 (v4 & 3), + 1, which take only this lane's values. Every lane
 // of the wavefront must take part (quad shuffles).
+constexpr int kMaxSharedParts = 8;
 struct SharedHQuad {
-  float4 gv[4], uv[4];
+  float4 gv[kMaxSharedParts], uv[kMaxSharedParts];
   // unconditional loads (part and position clamped; stage() drops the
   // extra parts): a load under a branch makes the join wait for its data
   __device__ __forceinline__ void load(const DecodeArgs& p, int v4, bool live) {
     const int Is = p.Is, v = live ? v4 : 0;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < kMaxSharedParts; ++k) {
       const size_t kk = size_t(min(k, p.shared_parts - 1));
       gv[k] = reinterpret_cast<const float4*>(p.shared_gu + (kk * 2) * Is)[v];
       uv[k] = reinterpret_cast<const float4*>(p.shared_gu + (kk * 2 + 1) * Is)[v];
@@ -99,7 +100,7 @@ struct SharedHQuad {
     const int Is = p.Is, parts = p.shared_parts;
     float4 gs = make_float4(0.f, 0.f, 0.f, 0.f), us = gs;
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < kMaxSharedParts; ++k)
       if (live && k < parts) {
         gs.x += gv[k].x; gs.y += gv[k].y; gs.z += gv[k].z; gs.w += gv[k].w;
         us.x += uv[k].x; us.y += uv[k].y; us.z += uv[k].z; us.w += uv[k].w;
@@ -140,7 +141,8 @@ struct SharedHQuad {
 // multiple of 64.
 template <int NT>
 __device__ __forceinline__ void form_shared_h(const DecodeArgs& p, uint32_t* xss, int tid) {
-  constexpr int kIt = NT >= 1024 ? 1 : 2;  // float4 positions per thread in flight
+  // float4 positions per thread in flight (each holds every part's loads)
+  constexpr int kIt = (NT >= 1024 || kMaxSharedParts > 4) ? 1 : 2;
   const int n4 = p.Is / 4;
   for (int v0 = tid; v0 < n4; v0 += NT * kIt) {
     SharedHQuad hq[kIt];
