@@ -229,11 +229,18 @@ def main():
             other.pop("traffic_file", None)
         traffic = read_traffic(ROOT / "profiles" / tf, kd["label"].split(":")[1].split("(")[0].strip()) \
             if tf and cfg.name.startswith("c2_") else None
-        roofline = {"bound": "hbm", "kernel": kd["label"], "achieved": kd["GBps"],
+        # achieved and frac count the routed expert bytes only (the north
+        # star's roofline is on the selected experts' quantized bytes); the
+        # launch's other bytes (shared expert) are reported beside them
+        routed_gbps = round(kd["routed_bytes_per_launch"] / (kd["launch_us"] * 1e-6) / 1e9, 1)
+        roofline = {"bound": "hbm", "kernel": kd["label"], "achieved": routed_gbps,
                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(kd["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                    "launch_us": kd["launch_us"], "bytes_per_launch": kd["bytes_per_launch"],
-                    "routed_bytes_per_launch": kd["routed_bytes_per_launch"]}
+                    "frac": round(routed_gbps / HBM_PEAK_GBS, 4), "traffic": traffic,
+                    "launch_us": kd["launch_us"],
+                    "routed_bytes_per_launch": kd["routed_bytes_per_launch"],
+                    "shared_bytes_per_launch": int(kd["bytes_per_launch"] - kd["routed_bytes_per_launch"]),
+                    "all_bytes_per_launch": kd["bytes_per_launch"],
+                    "all_bytes_GBps": kd["GBps"]}
         extra["kernels"] = kernels
         if stacked:
             extra["unique_experts_per_layer"] = [round(u, 3) for u in uniq_sub]
@@ -265,8 +272,15 @@ def main():
     # terms times Q2_K fields as e2m1, down on f16 MFMA; prefill: f16 MFMA;
     # packed-f16 tile kernels otherwise), always fp32 accumulation
     gu_label = labels[ops.TIMER_GATE_UP]
+    dn_label = labels[ops.TIMER_DOWN]
+    dn_mfma = dn_label.startswith(("mfma-down", "runs-down", "runs-multi-down"))
+    down_t = "f16 MFMA down" if dn_mfma else "f16-dot2 down"
     if gu_label.startswith("mfma"):
-        dtype = "e4m3x2*e2m1 MFMA gate/up, f16 MFMA down, f32 acc"
+        dtype = f"e4m3x2*e2m1 MFMA gate/up, {down_t}, f32 acc"
+    elif gu_label.startswith("runs32"):
+        dtype = f"f16x2-term MFMA gate/up (fp32 x), {down_t}, f32 acc"
+    elif gu_label.startswith("runs"):
+        dtype = f"f16 MFMA gate/up, {down_t}, f32 acc"
     elif gu_label.startswith("prefill"):
         dtype = "f16 MFMA, f32 acc"
     else:

@@ -556,9 +556,14 @@ bool mfma_enabled() {
 // super-block columns and give the route launch at least two shared
 // workgroups per CU (16-row tiles x parts), else the most that divide them,
 // at most kMaxSharedParts. c2 (Is 2048, 24 columns): 4; c4 (Is 1536, 16
-// columns): 8, measured 2.8 us per 4-layer step faster than 4.
+// columns): 8, measured 2.8 us per 4-layer step faster than 4. The part
+// count sets the order in which the shared partial sums are added, so it
+// depends on the shape only, never on the device: the CU count is MI355X's
+// (256) whatever the device reports, and the same layer gives the same bits
+// on any device.
+constexpr int kPartsCUs = 256;
 int shared_parts(int H, int Is) {
-  const int cols = H / kKBlock, tiles = Is / kRows, want = 2 * std::max(device_cus(), 1);
+  const int cols = H / kKBlock, tiles = Is / kRows, want = 2 * kPartsCUs;
   int best = 1;
   for (int k = 2; k <= kMaxSharedParts; ++k) {
     if (cols % k) continue;

@@ -208,6 +208,45 @@ __host__ __device__ constexpr int chunks_per_thread(int NB, int bytes = kQ2Bytes
   return (2 * NB * bytes + kThreads - 1) / kThreads;
 }
 
+// LDS layout of gate_up_fp4_kernel, in bytes from the start of its dynamic
+// LDS; the kernel takes its region pointers from here and the launcher its
+// allocation (end), so a host-side check of this function is a check of the
+// kernel's layout. Regions, and when they are live:
+//   xs      staged x (stage_words(H) words): prologue copy .. last tile;
+//   zero    16 zero bytes (A operand of inactive lanes): whole kernel;
+//   tl      the routed tile, gate and up, 32 rows of rb + kRowPad bytes: loop;
+//   part    per-wavefront row sums [wave][matrix][16] floats: loop;
+//   slot_e/slot_a/slot_w  per-slot expert, assignment, weight: whole kernel;
+//   tk      Top1Lds of the selection (SEL): prologue;
+//   sdpart  shared-down parts [wave][8] floats (SEL): prologue .. first tile;
+//   hsd     the shared expert's staged h, staged_stride(Is, false) words
+//           (SEL with the shared down): prologue;
+//   sdl     per-wavefront shared-down rows, kSdMaxOctets * kSdWpo areas of
+//           SharedDownSlice::kWaveLds bytes, written by the LDS DMA of their
+//           own wavefront (SEL with the shared down): prologue.
+struct Fp4Lds {
+  int xs, zero, tl, part, slot_e, slot_a, slot_w, tk, sdpart, hsd, sdl, sdl_bytes, end;
+};
+__host__ __device__ constexpr int align_up(int v, int a) { return (v + a - 1) / a * a; }
+__host__ __device__ constexpr Fp4Lds fp4_lds_layout(int H, int quant, bool sel, int Is_sd) {
+  Fp4Lds L{};
+  const int rb = H / kKBlock * fp4_block_bytes(quant);
+  L.xs = 0;
+  L.zero = L.xs + stage_words(H) * 4;
+  L.tl = L.zero + 16;
+  L.part = L.tl + 2 * 16 * (rb + kRowPad);
+  L.slot_e = L.part + kWaves * 2 * 16 * 4;
+  L.slot_a = L.slot_e + kMaxExperts * 4;
+  L.slot_w = L.slot_a + kMaxExperts * 4;
+  L.tk = align_up(L.slot_w + kMaxExperts * 4, 8);  // Top1Lds holds 64-bit keys
+  L.sdpart = L.tk + (sel ? int(sizeof(Top1Lds)) : 0);
+  L.hsd = L.sdpart + (sel ? kWaves * 8 * 4 : 0);
+  L.sdl = align_up(L.hsd + (sel ? staged_stride(Is_sd, false) * 4 : 0), 16);
+  L.sdl_bytes = (sel && Is_sd) ? kSdMaxOctets * kSdWpo * SharedDownSlice::kWaveLds : 0;
+  L.end = L.sdl + L.sdl_bytes;
+  return L;
+}
+
 // NB = H / 256 super-block columns (rows must be whole 16-byte chunks: NB a
 // multiple of 4 for Q2_K, of 8 for Q3_K); compile-time so that the chunk ->
 // (matrix, row, column) split and the LDS addressing use constant divisors
@@ -239,19 +278,22 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
   static_assert(rb % 16 == 0, "rows must be whole 16-byte chunks");
   constexpr int Sm = stage_words(H);
   const int I = p.I;
-  uint32_t* xs = smem;
-  uint32_t* zero = smem + Sm;
-  uint8_t* tl = reinterpret_cast<uint8_t*>(smem + Sm + 4);
-  float* part = reinterpret_cast<float*>(tl + 2 * 16 * RS);  // [wave][matrix][16]
-  uint32_t* slot_e = reinterpret_cast<uint32_t*>(part + kWaves * 2 * 16);  // [max_slots]
-  uint32_t* slot_a = slot_e + kMaxExperts;
-  float* slot_w = reinterpret_cast<float*>(slot_a + kMaxExperts);
-  Top1Lds* tk = reinterpret_cast<Top1Lds*>(slot_w + kMaxExperts);
-  float* sdpart = reinterpret_cast<float*>(tk + 1);  // [wave][8] shared down parts (SEL)
-  uint32_t* hsd = reinterpret_cast<uint32_t*>(sdpart + kWaves * 8);  // shared h (SEL)
-  // shared down rows (SEL), kWaveLds bytes per wavefront, 16-byte aligned
-  const int is_sd = (SEL && p.Is && p.ys) ? p.Is : 0;  // shared down in this launch
-  uint32_t* sdl = smem + ((int(hsd - smem) + int(staged_stride(is_sd, false)) + 3) & ~3);
+  // shared down in this launch (SEL with a shared expert and its ys rows)
+  const int is_sd = (SEL && p.Is && p.ys) ? p.Is : 0;
+  constexpr Fp4Lds L = fp4_lds_layout(H, Q, SEL, 0);  // sdl: the only offset is_sd moves
+  uint8_t* lds = reinterpret_cast<uint8_t*>(smem);
+  uint32_t* xs = reinterpret_cast<uint32_t*>(lds + L.xs);
+  uint32_t* zero = reinterpret_cast<uint32_t*>(lds + L.zero);
+  uint8_t* tl = lds + L.tl;
+  float* part = reinterpret_cast<float*>(lds + L.part);  // [wave][matrix][16]
+  uint32_t* slot_e = reinterpret_cast<uint32_t*>(lds + L.slot_e);  // [max_slots]
+  uint32_t* slot_a = reinterpret_cast<uint32_t*>(lds + L.slot_a);
+  float* slot_w = reinterpret_cast<float*>(lds + L.slot_w);
+  Top1Lds* tk = reinterpret_cast<Top1Lds*>(lds + L.tk);
+  float* sdpart = reinterpret_cast<float*>(lds + L.sdpart);  // [wave][8] shared down parts (SEL)
+  uint32_t* hsd = reinterpret_cast<uint32_t*>(lds + L.hsd);  // shared h (SEL)
+  // shared down rows (SEL)
+  uint32_t* sdl = reinterpret_cast<uint32_t*>(lds + fp4_lds_layout(H, Q, SEL, is_sd).sdl);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, q = lane >> 4;
@@ -345,30 +387,26 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
   const float* sums = reinterpret_cast<const float*>(xs + H);
   const int* e1s = reinterpret_cast<const int*>(xs + H + H / 16);
   // SEL: the down launch's workgroup of this index (on the same XCD) starts
-  // with its tile blockIdx.x. Its rows of the k selected experts are copied
-  // by the LDS DMA into the first KB of the shared down area (free once the
-  // shared down is dotted; the data is not used, the copy leaves the rows in
-  // this XCD's L2), issued when the last routed tile is in LDS so that the
-  // copies complete under its compute. Written as asm so that the compiler
-  // does not make the tile's LDS reads wait for them; the in-order vmcnt
-  // only makes its waits for older loads longer, and the kernel waits for
-  // the copies before it ends.
+  // with its tile blockIdx.x. When this workgroup has no next routed tile to
+  // fetch, its tile registers v (free from then on) load the k selected
+  // experts' rows of that down tile, as far as kWarmPer chunks per thread reach;
+  // the data is not used, the loads leave the rows in this XCD's L2. They
+  // are ordinary loads the compiler counts: nothing waits for them until
+  // the sink after the loop (no LDS is written).
+  // 64 KB per workgroup at most; none for the widest Q3_K rows, whose
+  // registers are all taken by the tile loop (the sink would spill)
+  constexpr int kWarmPer = (Q == INFERNO_Q3_K && NB > 16) ? 0 : PER < 4 ? PER : 4;
   bool warmed = false;
   auto warm_down = [&]() {
     warmed = true;
     if (!p.dpf_rows || int(blockIdx.x) >= p.H / p.dpf_rows) return;  // uniform
     const size_t rbd = size_t(p.dpf_row_bytes);
     const int cr = int(size_t(p.dpf_rows) * rbd / 16), nc = p.k * cr;
-    const uint32_t dst = __builtin_amdgcn_readfirstlane(
-        uint32_t(size_t((__attribute__((address_space(3))) uint32_t*)sdl)));
-    for (int b = wave * kWave; b < nc; b += kThreads) {
-      const int i = min(b + lane, nc - 1), r = i / cr, w = i - r * cr;
-      const u32x4* src = reinterpret_cast<const u32x4*>(
-          p.down + size_t(slot_e[r]) * p.down_stride + size_t(blockIdx.x) * p.dpf_rows * rbd) + w;
-      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                   :
-                   : "s"(dst), "v"(src)
-                   : "memory", "m0");
+#pragma unroll
+    for (int j = 0; j < kWarmPer; ++j) {
+      const int i = min(j * kThreads + tid, nc - 1), r = i / cr, w = i - r * cr;
+      v[j] = reinterpret_cast<const u32x4*>(p.down + size_t(slot_e[r]) * p.down_stride +
+                                            size_t(blockIdx.x) * p.dpf_rows * rbd)[w];
     }
   };
   for (; t < ntiles; t += gridDim.x) {
@@ -386,7 +424,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
     if constexpr (SEL) {  // once: the shared down parts (written before this barrier)
       if (sd_rows && tid < sd_rows) SharedDownSlice::store(p, sdpart, tid, sd_row0);
       sd_rows = 0;
-      if (t + int(gridDim.x) >= ntiles) warm_down();
+      if (kWarmPer && t + int(gridDim.x) >= ntiles) warm_down();
     }
     const int slot = t / tiles_i, tile = t - slot * tiles_i;
     float acc[2] = {0.f, 0.f};
@@ -529,14 +567,15 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
     }
   }
   if constexpr (SEL) {
-    if (!warmed) warm_down();
+    if (kWarmPer && !warmed) warm_down();
     // a workgroup without routed tiles sums its shared down parts here
     if (sd_rows) {
       __syncthreads();
       if (tid < sd_rows) SharedDownSlice::store(p, sdpart, tid, sd_row0);
     }
-    // the warm-up copies are not tracked by the compiler's wait counts
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    // sink of the warm-up loads: they stay, and the kernel ends after them
+#pragma unroll
+    for (int j = 0; j < kWarmPer; ++j) asm volatile("" : : "v"(v[j]));
   }
 }
 
@@ -703,13 +742,7 @@ inline bool covers_width(int H) {
 // sel: the selecting launch; Is_sd: the shared expert's width when its down
 // runs in that launch, else 0
 inline size_t lds_bytes(int H, int quant = INFERNO_Q2_K, bool sel = false, int Is_sd = 0) {
-  const int rb = H / kKBlock * fp4_block_bytes(quant);
-  return size_t(stage_words(H) + 4) * 4 + size_t(2 * 16) * (rb + kRowPad) +
-         size_t(kWaves * 2 * 16) * 4 + size_t(3 * kMaxExperts) * 4 + sizeof(Top1Lds) +
-         size_t(kWaves * 8) * 4 +
-         (sel ? size_t(staged_stride(Is_sd, false)) * 4 + 12 +
-                    (Is_sd ? size_t(kSdMaxOctets * kSdWpo * SharedDownSlice::kWaveLds) : 1024)
-              : 0);
+  return size_t(fp4_lds_layout(H, quant, sel, Is_sd).end);
 }
 
 }  // namespace mfma_decode

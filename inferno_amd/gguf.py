@@ -38,6 +38,7 @@ MAX_METADATA_DEPTH = 8
 # ggml tensor type codes and (values per block, bytes per block)
 GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q2_K, GGML_Q3_K, GGML_Q4_K, GGML_Q6_K, GGML_BF16 = (
     0, 1, 8, 10, 11, 12, 14, 30)
+_BLOCK_NAMES = {10: "Q2_K", 11: "Q3_K", 12: "Q4_K", 14: "Q6_K", 8: "Q8_0"}
 BLOCKS = {
     0: (1, 4), 1: (1, 2), 2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34),
     9: (32, 36), 10: (256, 84), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210),
@@ -73,11 +74,18 @@ class TensorInfo:
         if self.ty not in BLOCKS:
             raise GGUFError(f"GGUF tensor {self.name} has unsupported type {self.ty}")
         per, size = BLOCKS[self.ty]
-        # the reference checks the element count (lib.rs:1890-1900); the
-        # expert kernels check row widths themselves
-        if self.elements % per:
-            raise GGUFError(f"GGUF tensor {self.name} element count {self.elements} is not a "
-                            f"multiple of the {per}-value block")
+        # block_count_for_quant_block (crates/gguf/src/lib.rs:1877-1900): rows
+        # must be whole blocks (first dimension), then the element count
+        if per > 1:
+            if not self.dims:
+                raise GGUFError(f"GGUF tensor {self.name} has no dimensions")
+            kind = _BLOCK_NAMES.get(self.ty, f"type {self.ty}")
+            if self.dims[0] % per:
+                raise GGUFError(f"GGUF tensor {self.name} first dimension {self.dims[0]} is not "
+                                f"divisible by {kind} block size {per}")
+            if self.elements % per:
+                raise GGUFError(f"GGUF tensor {self.name} element count {self.elements} is not "
+                                f"divisible by {kind} block size {per}")
         return self.elements // per * size
 
 

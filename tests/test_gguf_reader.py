@@ -183,3 +183,18 @@ def test_unstored_array_strings_are_skipped_unchecked(tmp_path):
     path.write_bytes(bytes(raw))
     with G.GGUFFile(path) as g:
         assert g.metadata["tok"].length == 1100 and g.metadata["tok"].values is None
+
+
+def test_quant_rows_must_be_whole_blocks(tmp_path):
+    # block_count_for_quant_block (lib.rs:1877-1900) checks the first
+    # dimension before the element count: Q4_K [48, 16] holds 768 values (3
+    # whole blocks) but its 48-value rows are not whole 256-value blocks
+    path = tmp_path / "r.gguf"
+    path.write_bytes(_header(tensors=[("q", (48, 16), G.GGML_Q4_K, 0)]) + b"\0" * 512)
+    with pytest.raises(G.GGUFError, match="first dimension 48 is not divisible by Q4_K block size 256"):
+        with G.GGUFFile(path) as g:
+            g.tensor_bytes("q")
+    # rows of 512 values are whole blocks: 3 rows of 2 blocks
+    path.write_bytes(_header(tensors=[("q", (512, 3), G.GGML_Q4_K, 0)]) + b"\0" * 1024)
+    with G.GGUFFile(path) as g:
+        assert g.tensor_bytes("q").size == 6 * 144
