@@ -209,6 +209,32 @@ int inferno_moe_gather_tokens(void* stream, const float* x, const uint32_t* toke
 int inferno_rms_norm(void* stream, const float* x, const float* w, size_t rows, size_t H,
                      float eps, float* out);
 
+/* Workspace bytes of inferno_rms_norm_router_topk with the top-k (T ticket
+ * words, 256-byte aligned). The workspace must be zero-filled before its
+ * first use; every call leaves it zero again. */
+size_t inferno_rms_norm_router_topk_workspace_bytes(size_t T);
+
+/* RMSNorm -> router logits -> exact top-k of T decode tokens in one launch:
+ *   normed[t] = x[t] / sqrt(mean(x[t]^2) + eps) * norm_weight, rounded to
+ *     act_dtype (F32 or BF16; bit-identical to inferno_rms_norm's values);
+ *   logits_out[t, e] = normed[t] . router[e] (fp32 router [E,H]);
+ *   with expert_ids != NULL, the top-k of inferno_moe_router_topk over those
+ *   logits into expert_ids / expert_weights [T*k] (bias may be NULL).
+ * normed_out may be NULL. H a multiple of 16 up to 8192, E <= 256, k <= 16.
+ * Without the top-k the workspace may be NULL. Calls sharing a workspace
+ * must not overlap (they share its tickets).
+ * Replaces Backend::laguna_xs_rms_norm_router_device (backend.rs:1162;
+ * laguna_xs_rms_norm_router_decode_f32_kernel, laguna_xs_kernels.metal:
+ * 1274-1365) followed by the decode top-k (laguna_xs_router_top8_decode_f32_kernel,
+ * laguna_xs_kernels.metal:1077-1165; Backend::moe_router_topk_resident_device,
+ * backend.rs:2151). */
+int inferno_rms_norm_router_topk(void* stream, const float* x, const float* norm_weight, float eps,
+                                 const float* router, const float* bias, size_t T, size_t H,
+                                 size_t E, size_t k, int score_fn, int norm_topk_prob,
+                                 float routed_scaling_factor, int act_dtype, void* normed_out,
+                                 float* logits_out, uint32_t* expert_ids, float* expert_weights,
+                                 void* workspace, size_t workspace_bytes);
+
 /* --------------------------------------------------------- whole layer */
 
 /* One MoE FFN layer as the reference model calls it

@@ -60,6 +60,9 @@ SIGNATURES = {
     "inferno_moe_weighted_index_add_combine": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "inferno_moe_gather_tokens": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "inferno_rms_norm": (_i, [_vp, _vp, _vp, _sz, _sz, _f, _vp]),
+    "inferno_rms_norm_router_topk_workspace_bytes": (_sz, [_sz]),
+    "inferno_rms_norm_router_topk": (_i, [_vp, _vp, _vp, _f, _vp, _vp, _sz, _sz, _sz, _sz, _i, _i,
+                                          _f, _i, _vp, _vp, _vp, _vp, _vp, _sz]),
     "inferno_moe_layer_workspace_bytes": (_sz, [C.POINTER(LayerDesc), _sz]),
     "inferno_moe_layer_forward": (_i, [_vp, C.POINTER(LayerDesc), _vp, _i, _vp, _sz, _vp, _vp,
                                        _vp, _vp, _sz]),

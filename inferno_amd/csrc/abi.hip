@@ -431,6 +431,44 @@ int inferno_rms_norm(void* stream, const float* x, const float* w, size_t rows, 
   return launch_rms_norm(as_stream(stream), x, w, rows, H, eps, out, INFERNO_F32);
 }
 
+size_t inferno_rms_norm_router_topk_workspace_bytes(size_t T) {
+  return (T * sizeof(uint32_t) + 255) / 256 * 256;
+}
+
+int inferno_rms_norm_router_topk(void* stream, const float* x, const float* norm_weight, float eps,
+                                 const float* router, const float* bias, size_t T, size_t H,
+                                 size_t E, size_t k, int score_fn, int norm_topk_prob,
+                                 float routed_scaling_factor, int act_dtype, void* normed_out,
+                                 float* logits_out, uint32_t* expert_ids, float* expert_weights,
+                                 void* workspace, size_t workspace_bytes) {
+  clear_error();
+  INF_CHECK_ARG(eps >= 0.f, "eps must be >= 0");
+  INF_CHECK_ARG(act_dtype == INFERNO_F32 || act_dtype == INFERNO_BF16,
+                "act dtype must be F32 or BF16");
+  INF_CHECK_ARG(score_fn == INFERNO_SCORE_SIGMOID || score_fn == INFERNO_SCORE_SOFTMAX,
+                "score_fn must be SIGMOID or SOFTMAX");
+  if (T == 0) return INFERNO_OK;
+  INF_CHECK_ARG(x && norm_weight && router && logits_out, "null pointer");
+  const bool topk = expert_ids != nullptr;
+  if (topk) {
+    INF_CHECK_ARG(expert_weights && workspace, "null pointer");
+    if (workspace_bytes < inferno_rms_norm_router_topk_workspace_bytes(T)) {
+      set_error("workspace too small: need " +
+                std::to_string(inferno_rms_norm_router_topk_workspace_bytes(T)) + " bytes");
+      return INFERNO_ERR_SIZE;
+    }
+  }
+  if (!norm_router_supported(T, H, E, topk ? k : 0)) {
+    set_error("fused norm+router needs H a multiple of 16 up to 8192, E <= 256, k <= min(E, 16)");
+    return INFERNO_UNSUPPORTED;
+  }
+  if (int st_ = require_device()) return st_;
+  return launch_norm_router(as_stream(stream), x, norm_weight, eps, router, bias, T, H, E, k,
+                            score_fn, norm_topk_prob, routed_scaling_factor, act_dtype, normed_out,
+                            logits_out, static_cast<uint32_t*>(workspace),
+                            topk ? expert_ids : nullptr, expert_weights);
+}
+
 // ------------------------------------------------------------- layer
 
 namespace {

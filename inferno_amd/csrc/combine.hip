@@ -4,6 +4,7 @@
 #include <type_traits>
 
 #include "kernels.hpp"
+#include "norm_dev.hpp"
 
 namespace inferno {
 namespace {
@@ -51,17 +52,9 @@ __global__ void __launch_bounds__(256)
   out[i] = t < T ? x[size_t(t) * H + h] : 0.f;
 }
 
-// One 1024-thread workgroup per row. Rows of a multiple of 4 values up to
-// 32768 are read as float4s all issued at once (one memory round trip; the
-// row is usually the previous kernel's output, not in this XCD's L2), the
-// squares summed per thread, per wavefront (butterfly) and over the 16
-// wavefronts in order: a fixed order, so every call and every caller of the
-// same row gets the same bits. Other widths take a strided scalar loop.
-// The output is fp32 or bf16 (round to nearest even), the activation type a
+// One 1024-thread workgroup per row (rms_norm_row, norm_dev.hpp). The
+// output is fp32 or bf16 (round to nearest even), the activation type a
 // following layer consumes.
-constexpr int kNormThreads = 1024;
-constexpr int kNormVec = 8;  // float4s per thread held in registers
-
 template <typename OutT>
 __device__ __forceinline__ void store_norm(OutT* out, size_t i, float v) {
   if constexpr (std::is_same<OutT, float>::value)
@@ -74,58 +67,10 @@ template <typename OutT>
 __global__ void __launch_bounds__(kNormThreads)
     rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, size_t H, float eps,
                     OutT* __restrict__ out) {
-  __shared__ float part[kNormThreads / 64];
-  __shared__ float scale_s;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const float* row = x + size_t(blockIdx.x) * H;
+  __shared__ float part[kNormThreads / 64 + 1];
   OutT* orow = out + size_t(blockIdx.x) * H;
-  const bool vec = H % 4 == 0 && H <= size_t(4 * kNormThreads * kNormVec);
-  float4 v[kNormVec];
-  float s = 0.f;
-  if (vec) {
-    const float4* r4 = reinterpret_cast<const float4*>(row);
-#pragma unroll
-    for (int j = 0; j < kNormVec; ++j) {
-      const size_t i = size_t(j) * kNormThreads + tid;
-      v[j] = i < H / 4 ? r4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int j = 0; j < kNormVec; ++j) {
-      s += v[j].x * v[j].x;
-      s += v[j].y * v[j].y;
-      s += v[j].z * v[j].z;
-      s += v[j].w * v[j].w;
-    }
-  } else {
-    for (size_t i = tid; i < H; i += kNormThreads) s += row[i] * row[i];
-  }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) s += __shfl_xor(s, m, 64);
-  if (lane == 0) part[wave] = s;
-  __syncthreads();
-  if (tid == 0) {
-    float t = 0.f;
-    for (int i = 0; i < kNormThreads / 64; ++i) t += part[i];
-    scale_s = sqrtf(t / float(H) + eps);
-  }
-  __syncthreads();
-  const float scale = scale_s;
-  if (vec) {
-    const float4* w4 = reinterpret_cast<const float4*>(w);
-#pragma unroll
-    for (int j = 0; j < kNormVec; ++j) {
-      const size_t i = size_t(j) * kNormThreads + tid;
-      if (i < H / 4) {
-        const float4 g = w4[i];
-        store_norm(orow, 4 * i, v[j].x / scale * g.x);
-        store_norm(orow, 4 * i + 1, v[j].y / scale * g.y);
-        store_norm(orow, 4 * i + 2, v[j].z / scale * g.z);
-        store_norm(orow, 4 * i + 3, v[j].w / scale * g.w);
-      }
-    }
-  } else {
-    for (size_t i = tid; i < H; i += kNormThreads) store_norm(orow, i, row[i] / scale * w[i]);
-  }
+  rms_norm_row(x + size_t(blockIdx.x) * H, w, H, eps, part,
+               [&](size_t i, float v) { store_norm(orow, i, v); });
 }
 
 unsigned blocks_for(size_t n) { return unsigned((n + 255) / 256); }

@@ -64,4 +64,12 @@ int launch_gather(hipStream_t s, const float* x, const uint32_t* token_idx, size
 int launch_rms_norm(hipStream_t s, const float* x, const float* w, size_t rows, size_t H,
                     float eps, void* out, int out_dtype = INFERNO_F32);
 
+// RMSNorm -> router logits (-> top-k when ids is not null) in one launch
+// (norm_router.hip); tickets: T words, zero on entry, left zero.
+bool norm_router_supported(size_t T, size_t H, size_t E, size_t k);
+int launch_norm_router(hipStream_t s, const float* x, const float* norm_w, float eps,
+                       const float* router, const float* bias, size_t T, size_t H, size_t E,
+                       size_t k, int score_fn, int norm, float scale, int act_dtype, void* normed,
+                       float* logits, uint32_t* tickets, uint32_t* ids, float* weights);
+
 }  // namespace inferno

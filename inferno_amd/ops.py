@@ -170,6 +170,34 @@ def rms_norm(x, w, eps):
     return out
 
 
+class NormRouter:
+    """RMSNorm -> router logits (-> top-k) of decode tokens in one launch
+    (inferno_rms_norm_router_topk; Backend::laguna_xs_rms_norm_router_device
+    followed by the decode top-k). Holds the zero-filled ticket workspace the
+    top-k needs; calls through one instance must not overlap."""
+
+    def __init__(self, max_tokens=1, device="cuda"):
+        self._ws = torch.zeros(lib().inferno_rms_norm_router_topk_workspace_bytes(max_tokens),
+                               dtype=torch.uint8, device=device)
+        self.max_tokens = max_tokens
+
+    def __call__(self, x, norm_weight, eps, router, bias=None, k=0, score_fn=0, norm=True,
+                 scale=1.0, act_dtype=torch.float32, topk=True):
+        T, H = x.shape
+        E = router.shape[0]
+        if T > self.max_tokens:
+            self.__init__(T, x.device)
+        normed = torch.empty(T, H, dtype=act_dtype, device=x.device)
+        logits = torch.empty(T, E, dtype=torch.float32, device=x.device)
+        ids = torch.empty(T * k, dtype=torch.int32, device=x.device) if topk else None
+        w = torch.empty(T * k, dtype=torch.float32, device=x.device) if topk else None
+        check(lib().inferno_rms_norm_router_topk(
+            _s(), _p(_dev(x)), _p(norm_weight), float(eps), _p(router), _p(bias), T, H, E, k,
+            score_fn, int(norm), float(scale), _DT[act_dtype], _p(normed), _p(logits), _p(ids),
+            _p(w), _p(self._ws), self._ws.numel()))
+        return normed, logits, ids, w
+
+
 TIMER_GATE_UP, TIMER_DOWN, TIMER_ROUTE, TIMER_SELECT = 0, 1, 2, 3
 
 

@@ -95,3 +95,27 @@ def test_synth_quantized_host_is_quantised_normal():
     x = ops.synth_normal_host(9, 0.02, 4 * 512).numpy()
     back = orc.dequantize(Q4_K, q)
     assert np.linalg.norm(back - x) / np.linalg.norm(x) < 0.12
+
+
+def test_norm_router_argument_errors_without_gpu():
+    # the fused RMSNorm -> router -> top-k entry point validates before any
+    # device work: unsupported widths are Ok(None)-style (1), a missing
+    # workspace with the top-k an error, a valid call without a device 1
+    import ctypes as C
+    L = lib()
+    x = C.c_void_p(16)
+    ids = C.c_void_p(32)
+    st = L.inferno_rms_norm_router_topk(None, x, x, 1e-6, x, None, 1, 24, 64, 8, 0, 1, 1.0, 0,
+                                        None, x, None, None, None, 0)
+    assert st == 1 and b"multiple of 16" in L.inferno_last_error()
+    st = L.inferno_rms_norm_router_topk(None, x, x, 1e-6, x, None, 1, 2048, 64, 8, 0, 1, 1.0, 0,
+                                        None, x, ids, ids, x, 0)
+    assert st == -2 and b"workspace too small" in L.inferno_last_error()
+    st = L.inferno_rms_norm_router_topk(None, x, x, 1e-6, x, None, 1, 2048, 64, 8, 7, 1, 1.0, 0,
+                                        None, x, None, None, None, 0)
+    assert st == -1
+    assert L.inferno_rms_norm_router_topk_workspace_bytes(3) == 256
+    if not torch.cuda.is_available():
+        st = L.inferno_rms_norm_router_topk(None, x, x, 1e-6, x, None, 1, 2048, 64, 8, 0, 1, 1.0,
+                                            0, None, x, None, None, None, 0)
+        assert st == 1 and b"no HIP device" in L.inferno_last_error()
