@@ -220,7 +220,7 @@ size_t inferno_rms_norm_router_topk_workspace_bytes(size_t T);
  *   logits_out[t, e] = normed[t] . router[e] (fp32 router [E,H]);
  *   with expert_ids != NULL, the top-k of inferno_moe_router_topk over those
  *   logits into expert_ids / expert_weights [T*k] (bias may be NULL).
- * normed_out may be NULL. H a multiple of 16 up to 8192, E <= 256, k <= 16.
+ * normed_out may be NULL. H a multiple of 64 up to 8192, E <= 256, k <= 16.
  * Without the top-k the workspace may be NULL. Calls sharing a workspace
  * must not overlap (they share its tickets).
  * Replaces Backend::laguna_xs_rms_norm_router_device (backend.rs:1162;

@@ -459,7 +459,7 @@ int inferno_rms_norm_router_topk(void* stream, const float* x, const float* norm
     }
   }
   if (!norm_router_supported(T, H, E, topk ? k : 0)) {
-    set_error("fused norm+router needs H a multiple of 16 up to 8192, E <= 256, k <= min(E, 16)");
+    set_error("fused norm+router needs H a multiple of 64 up to 8192, E <= 256, k <= min(E, 16)");
     return INFERNO_UNSUPPORTED;
   }
   if (int st_ = require_device()) return st_;
@@ -516,10 +516,41 @@ size_t inferno_moe_layer_workspace_bytes(const inferno_moe_layer* layer, size_t 
   return c.used;
 }
 
+namespace {
+int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x_dtype,
+                  const float* residual, size_t T, float* out, uint32_t* expert_ids_out,
+                  float* expert_weights_out, void* workspace, size_t workspace_bytes,
+                  const float* logits_ready);
+}  // namespace
+
 int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const void* x,
                               int x_dtype, const float* residual, size_t T, float* out,
                               uint32_t* expert_ids_out, float* expert_weights_out,
                               void* workspace, size_t workspace_bytes) {
+  return layer_forward(stream, L, x, x_dtype, residual, T, out, expert_ids_out,
+                       expert_weights_out, workspace, workspace_bytes, nullptr);
+}
+
+namespace {
+// True when the layer forward takes the fused decode launches for T tokens.
+bool layer_takes_decode(const inferno_moe_layer* L, size_t T, int x_dtype) {
+  const size_t Is = L->shared_intermediate;
+  const int sq = L->shared_quant ? L->shared_quant : INFERNO_Q8_0;
+  const int sdq = L->shared_down_quant ? L->shared_down_quant : INFERNO_Q8_0;
+  const bool shared_q8 = Is == 0 || (sq == INFERNO_Q8_0 && sdq == INFERNO_Q8_0);
+  return decode_supported(T, L->top_k, L->experts, L->hidden, L->intermediate, Is, x_dtype,
+                          L->quant, L->down_quant) &&
+         shared_q8 &&
+         (T == 1 || !use_mfma(L->quant, L->down_quant, T, L->top_k, L->experts, L->hidden,
+                              L->intermediate));
+}
+
+// logits_ready: the tokens' router logits [T, E], already formed (the
+// stack's fused RMSNorm -> router launch); only the decode path takes them
+int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x_dtype,
+                  const float* residual, size_t T, float* out, uint32_t* expert_ids_out,
+                  float* expert_weights_out, void* workspace, size_t workspace_bytes,
+                  const float* logits_ready) {
   clear_error();
   INF_CHECK_ARG(L != nullptr, "null layer");
   const size_t H = L->hidden, E = L->experts, I = L->intermediate, k = L->top_k;
@@ -566,8 +597,11 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
   // the fused decode path below 256 assignments (and for one token); from
   // there the grouped MFMA GEMM reads each expert's weights once for all its
   // tokens (c4 at T = 32, 2.5 tokens per expert: 2.5 ms against 3.9 ms)
-  const bool decode = decode_supported(T, k, E, H, I, Is, x_dtype, L->quant, L->down_quant) &&
-                      shared_q8 && (T == 1 || !use_mfma(L->quant, L->down_quant, T, k, E, H, I));
+  const bool decode = layer_takes_decode(L, T, x_dtype);
+  if (logits_ready && !decode) {
+    set_error("precomputed logits need the decode path");
+    return INFERNO_ERR_INVALID;
+  }
   if (decode) {
     DecodeArgs d{};
     d.T = int(T); d.H = int(H); d.E = int(E); d.I = int(I); d.k = int(k); d.Is = int(Is);
@@ -589,6 +623,7 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
     d.shared_gu = w.shared_gu;
     d.ys = w.ys;
     d.y = w.moe.y;
+    d.logits_ready = logits_ready;
     return launch_decode_layer(s, d, L->quant);
   }
   const int parts = router_logit_parts(T, H, E, x_dtype);
@@ -638,6 +673,7 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
   }
   return launch_topk_combine(s, nullptr, residual, w.moe.y, nullptr, T, H, k, out);
 }
+}  // namespace
 
 // ------------------------------------------------- layer, no allocation
 
@@ -703,6 +739,7 @@ int inferno_moe_layer_forward_noalloc(void* stream, const inferno_moe_layer* L, 
 namespace {
 struct StackScratch {
   void* normed;      // [T, H] activations of the current layer (fp32 or bf16)
+  float* logits;     // [T, E] router logits of the fused RMSNorm -> router launch
   float* stream[2];  // [T, H] residual stream between layers (ping-pong)
   void* layer_ws;    // the layers' own workspace (the largest one)
   size_t layer_ws_bytes;
@@ -711,6 +748,9 @@ StackScratch carve_stack(Carver& c, const inferno_moe_layer* layers, size_t n, s
   StackScratch s;
   const size_t H = n ? layers[0].hidden : 0;
   s.normed = c.take<float>(T * H);
+  size_t E = 0;
+  for (size_t l = 0; l < n; ++l) E = std::max(E, layers[l].experts);
+  s.logits = c.take<float>(T * E);
   // layer l (but the last) writes stream[l & 1]
   s.stream[0] = c.take<float>(n > 1 ? T * H : 0);
   s.stream[1] = c.take<float>(n > 2 ? T * H : 0);
@@ -759,11 +799,23 @@ int inferno_moe_stack_forward(void* stream, const inferno_moe_layer* layers, siz
   size_t id_off = 0;
   for (size_t l = 0; l < n_layers; ++l) {
     float* next = l + 1 == n_layers ? out : w.stream[l & 1];
-    int st = launch_rms_norm(s, r, norm_weights[l], T, H, eps, w.normed, act_dtype);
+    // INFERNO_STACK_FUSED_ROUTER=1: for decode layers, RMSNorm and the
+    // router logits in one launch (the layer's route launch then only stages
+    // x and runs the shared gate/up). Off by default: measured slower on the
+    // c4 stack (189.9-190.1 against 184.4-185.8 us per step), since every
+    // workgroup of that launch forms the normalised row before its logits
+    const inferno_moe_layer* L = &layers[l];
+    const bool fused = switch_on("INFERNO_STACK_FUSED_ROUTER") &&
+                       layer_takes_decode(L, T, act_dtype) &&
+                       norm_router_supported(T, H, L->experts, 0);
+    int st = fused ? launch_norm_router(s, r, norm_weights[l], eps, L->router, nullptr, T, H,
+                                        L->experts, 0, 0, 0, 1.f, act_dtype, w.normed, w.logits,
+                                        nullptr, nullptr, nullptr)
+                   : launch_rms_norm(s, r, norm_weights[l], T, H, eps, w.normed, act_dtype);
     if (st) return st;
-    st = inferno_moe_layer_forward(stream, &layers[l], w.normed, act_dtype, r, T, next,
-                                   expert_ids_out ? expert_ids_out + id_off : nullptr, nullptr,
-                                   w.layer_ws, w.layer_ws_bytes);
+    st = layer_forward(stream, L, w.normed, act_dtype, r, T, next,
+                       expert_ids_out ? expert_ids_out + id_off : nullptr, nullptr, w.layer_ws,
+                       w.layer_ws_bytes, fused ? w.logits : nullptr);
     if (st) {
       set_error("layer " + std::to_string(l) + ": " + g_last_error);
       return st;

@@ -22,6 +22,13 @@ inline bool switch_off(const char* name) {
   return v && v[0] == '0';
 }
 
+// True when the environment variable `name` starts with '1' (an off-by-
+// default variant switched on).
+inline bool switch_on(const char* name) {
+  const char* v = std::getenv(name);
+  return v && v[0] == '1';
+}
+
 constexpr int kWave = 64;        // CDNA wavefront width
 constexpr int kKBlock = 256;     // K-quant super-block values
 constexpr int kQ8Block = 32;     // Q8_0 block values

@@ -128,6 +128,7 @@ __global__ void __launch_bounds__(256) route_kernel(DecodeArgs p, int gx, int gy
       }
     }
   }
+  if (p.logits_ready) return;  // uniform: the logits come from an earlier launch
   // logits partial of expert e over chunk c for every token
   const int e = bx * 4 + wave;
   const int c = by;
@@ -725,6 +726,11 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   DecodeArgs a = a0;
   a.chunk = decode_chunk(size_t(a.H));
   a.n_chunks = a.H / a.chunk;
+  if (a.logits_ready) {  // one "chunk": the logits themselves
+    a.partials = const_cast<float*>(a.logits_ready);
+    a.chunk = a.H;
+    a.n_chunks = 1;
+  }
   a.max_slots = std::min(a.E, a.T * a.k);
   const bool xsplit = a.x_dtype == INFERNO_F32;
   // gate/up: fp8 x fp4 matrix-core kernel (one Q2_K bf16 token), else the
@@ -789,10 +795,11 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
   // route: grid covers E/4 x chunks workgroups (and enough threads to stage x)
   {
     const int runs = a.T * a.H / 16;
-    const int gx = (a.E + 3) / 4;
     const int need = std::max(std::max((runs + 255) / 256, (a.T * (a.H / kKBlock) + 3) / 4),
                               a.stage_xr ? (a.T * a.H + 255) / 256 : 0);
-    const int gy = std::max(a.n_chunks, (need + gx - 1) / gx);
+    // with the logits ready, only the staging workgroups
+    const int gx = a.logits_ready ? 1 : (a.E + 3) / 4;
+    const int gy = a.logits_ready ? need : std::max(a.n_chunks, (need + gx - 1) / gx);
     const int shared_wgs = use_mfma ? a.Is / kRows * a.shared_parts : 0;
     const unsigned grid = unsigned(gx * gy + shared_wgs);
     const size_t lds = shared_wgs ? gate_up_lds(a.H / a.shared_parts, xsplit) : 0;

@@ -46,6 +46,10 @@ struct DecodeArgs {
   // the down launch's first tile per workgroup index (rows, bytes per row;
   // 0: none): the selecting gate/up launch warms its XCD's L2 with it
   int dpf_rows, dpf_row_bytes;
+  // the tokens' router logits [T, E] when a previous launch already formed
+  // them (the stack's fused RMSNorm -> router launch); the route launch then
+  // only stages x and runs the shared gate/up parts
+  const float* logits_ready;
   // filled by launch_decode_layer
   int chunk, n_chunks, max_slots, routed_tiles;
 };

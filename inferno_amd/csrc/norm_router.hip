@@ -12,9 +12,9 @@
 //
 // Workgroup (g, t), 1024 threads: rms_norm_row (the RMSNorm launch's own
 // code, so the normalised row is bit-identical to it) into LDS, rounded to
-// the activation type the experts take (fp32 or bf16); then experts 4 g ..
-// 4 g + 3, each by four wavefronts over a quarter of H (float4 lanes, wave
-// butterfly, quarters added in order): fixed order, no float atomics. With
+// the activation type the experts take (fp32 or bf16); then expert g, its
+// 16 wavefronts over a sixteenth of H each (float4 lanes, wave butterfly,
+// parts added in order): fixed order, no float atomics. With
 // the top-k: the logits go to the workspace, each workgroup releases them
 // (agent-scope fence) and takes a ticket; the one that draws the last ticket
 // acquires, reads the token's E logits and selects on one wavefront
@@ -27,7 +27,8 @@
 namespace inferno {
 namespace {
 
-constexpr int kNrExperts = 4;  // experts per workgroup
+constexpr int kNrExperts = 1;  // experts per workgroup
+constexpr int kNrParts = 16 / kNrExperts;  // wavefronts (H parts) per expert
 constexpr int kNrMaxH = 8192;  // LDS row of fp32 values (32 KB)
 
 struct NormRouterArgs {
@@ -47,7 +48,7 @@ struct NormRouterArgs {
 __global__ void __launch_bounds__(kNormThreads) norm_router_kernel(NormRouterArgs a) {
   __shared__ float xn[kNrMaxH];
   __shared__ float part[kNormThreads / 64 + 1];
-  __shared__ float lp[4][kNrExperts];
+  __shared__ float lp[kNrParts][kNrExperts];
   __shared__ uint32_t last;
   __shared__ float row[kMaxExperts];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -65,9 +66,9 @@ __global__ void __launch_bounds__(kNormThreads) norm_router_kernel(NormRouterArg
     }
   });
   __syncthreads();
-  // expert e0 + (wave & 3) over quarter (wave >> 2) of H (H a multiple of 16)
-  const int el = wave & 3, qh = wave >> 2, e = int(blockIdx.x) * kNrExperts + el;
-  const int q4 = H / 16;  // float4s per quarter
+  // expert e0 + (wave % kNrExperts) over part (wave / kNrExperts) of H
+  const int el = wave % kNrExperts, qh = wave / kNrExperts, e = int(blockIdx.x) * kNrExperts + el;
+  const int q4 = H / (4 * kNrParts);  // float4s per part
   float acc = 0.f;
   if (e < E) {
     const float4* w4 = reinterpret_cast<const float4*>(a.router + size_t(e) * H) + qh * q4;
@@ -85,7 +86,10 @@ __global__ void __launch_bounds__(kNormThreads) norm_router_kernel(NormRouterArg
   __syncthreads();
   if (tid < kNrExperts) {
     const int ee = int(blockIdx.x) * kNrExperts + tid;
-    if (ee < E) a.logits[size_t(t) * E + ee] = ((lp[0][tid] + lp[1][tid]) + lp[2][tid]) + lp[3][tid];
+    float v = 0.f;
+#pragma unroll
+    for (int j = 0; j < kNrParts; ++j) v += lp[j][tid];
+    if (ee < E) a.logits[size_t(t) * E + ee] = v;
   }
   if (a.ids == nullptr) return;  // uniform
   if (tid == 0) {
@@ -116,7 +120,7 @@ __global__ void __launch_bounds__(kNormThreads) norm_router_kernel(NormRouterArg
 }  // namespace
 
 bool norm_router_supported(size_t T, size_t H, size_t E, size_t k) {
-  return T >= 1 && T <= 65535 && H % 16 == 0 && H >= 16 && H <= size_t(kNrMaxH) && E >= 1 &&
+  return T >= 1 && T <= 65535 && H % (4 * kNrParts) == 0 && H >= 4 * kNrParts && H <= size_t(kNrMaxH) && E >= 1 &&
          E <= size_t(kMaxExperts) && k <= E && k <= size_t(kMaxTopK);
 }
 

@@ -107,7 +107,7 @@ def test_norm_router_argument_errors_without_gpu():
     ids = C.c_void_p(32)
     st = L.inferno_rms_norm_router_topk(None, x, x, 1e-6, x, None, 1, 24, 64, 8, 0, 1, 1.0, 0,
                                         None, x, None, None, None, 0)
-    assert st == 1 and b"multiple of 16" in L.inferno_last_error()
+    assert st == 1 and b"multiple of 64" in L.inferno_last_error()
     st = L.inferno_rms_norm_router_topk(None, x, x, 1e-6, x, None, 1, 2048, 64, 8, 0, 1, 1.0, 0,
                                         None, x, ids, ids, x, 0)
     assert st == -2 and b"workspace too small" in L.inferno_last_error()

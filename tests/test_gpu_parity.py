@@ -632,6 +632,52 @@ def test_stack_c4_laguna_q2k_q3k_rmsnorm_chain(cuda, T):
 
 
 @pytest.mark.parametrize("T", [1, 32])
+def test_stack_c4_fused_norm_router_variant(cuda, monkeypatch, T):
+    """Each c4 layer as a one-layer stack with INFERNO_STACK_FUSED_ROUTER=1
+    (RMSNorm and router logits in one launch before a decode layer) against
+    the default: the normalised rows are bit-identical and the logits are
+    summed in another order, so the same experts except near-ties, and the
+    same output within 1e-5 rel-L2 on tokens whose routing agrees (measured
+    5.9e-6 over 16 tokens: an f16 rounding of h or a bf16 rounding flipped
+    here and there). Along a whole stack the bf16 re-rounding of every RMSNorm
+    amplifies such last-bit differences, as it does between the GPU and the
+    oracle chain, so the layers are compared one at a time. T = 32 takes the
+    prefill path, where the variant does not apply: identical bits."""
+    cfg = cf.CONFIGS["c4"]
+    k = cfg.top_k
+    lts, _ = cf.build_stack(cfg, cuda, max_tokens=T)
+    got, ref, same, total = [], [], 0, 0
+    for l, lt in enumerate(lts):
+        stack = ops.MoEStack([lt.layer], [lt.norm_w], eps=cfg.rms_eps, act_dtype=cfg.x_dtype,
+                             max_tokens=T)
+        for v in range(4 if T == 1 else 1):
+            hidden = cf.make_hidden(cfg, T, variant=10 * l + v, device=cuda)
+            ids0 = torch.empty(T * k, dtype=torch.int32, device=cuda)
+            ids1 = torch.empty_like(ids0)
+            out0 = stack.forward(hidden, ids=ids0)
+            monkeypatch.setenv("INFERNO_STACK_FUSED_ROUTER", "1")
+            out1 = stack.forward(hidden, ids=ids1)
+            out1b = stack.forward(hidden)
+            monkeypatch.delenv("INFERNO_STACK_FUSED_ROUTER")
+            torch.cuda.synchronize()
+            assert torch.equal(out1, out1b), "fused variant not bitwise reproducible"
+            if T > 1:
+                assert torch.equal(out0, out1) and torch.equal(ids0, ids1)
+                continue
+            total += 1
+            if np.array_equal(np.sort(ph.to_np(ids0)), np.sort(ph.to_np(ids1))):
+                same += 1
+                got.append(ph.to_np(out1)[0] - ph.to_np(hidden)[0])
+                ref.append(ph.to_np(out0)[0] - ph.to_np(hidden)[0])
+    if T == 1:
+        assert same >= total - 2
+        err = rn.rel_l2(np.stack(got), np.stack(ref))
+        print(f"c4 fused norm+router, layer by layer: {same}/{total} tokens same routing, "
+              f"rel_l2={err:.2e}")
+        assert err < 1e-5
+
+
+@pytest.mark.parametrize("T", [1, 32])
 def test_stack_c4_each_layer_on_gpu_stream(cuda, T):
     """c4 layer by layer: the GPU stream entering layer l (output of the
     stack's first l layers) is normalised by the library's RMSNorm (the fp32
