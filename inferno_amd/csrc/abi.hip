@@ -80,7 +80,8 @@ MoeScratch carve_moe(Carver& c, size_t T, size_t k, size_t E, size_t H, size_t I
   m.h = c.take<float>(T * k * I);
   m.y = c.take<float>(T * k * H);
   m.stage_x = c.take<uint32_t>(stage_words(T, H));
-  m.stage_h = c.take<uint32_t>(stage_words(T * k, I));
+  // (one row more: the shared expert's h when it runs as assignment k)
+  m.stage_h = c.take<uint32_t>(stage_words(T * k + 1, I));
   m.plan = c.take<uint32_t>(prefill_plan_words(T * k, E));
   return m;
 }
@@ -532,12 +533,25 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const vo
 }
 
 namespace {
+// True when one token's shared expert runs as assignment k of the run
+// decode kernels: a shared expert with the routed formats and width (the
+// Laguna XS layer).
+bool layer_shared_slot(const inferno_moe_layer* L, size_t T, int x_dtype) {
+  const size_t Is = L->shared_intermediate;
+  const int sq = L->shared_quant ? L->shared_quant : INFERNO_Q8_0;
+  const int sdq = L->shared_down_quant ? L->shared_down_quant : INFERNO_Q8_0;
+  return Is != 0 && Is == L->intermediate && sq == L->quant && sdq == L->down_quant &&
+         decode_shared_slot_supported(T, L->top_k, L->experts, L->hidden, L->intermediate,
+                                      x_dtype, L->quant, L->down_quant);
+}
+
 // True when the layer forward takes the fused decode launches for T tokens.
 bool layer_takes_decode(const inferno_moe_layer* L, size_t T, int x_dtype) {
   const size_t Is = L->shared_intermediate;
   const int sq = L->shared_quant ? L->shared_quant : INFERNO_Q8_0;
   const int sdq = L->shared_down_quant ? L->shared_down_quant : INFERNO_Q8_0;
   const bool shared_q8 = Is == 0 || (sq == INFERNO_Q8_0 && sdq == INFERNO_Q8_0);
+  if (layer_shared_slot(L, T, x_dtype)) return true;
   return decode_supported(T, L->top_k, L->experts, L->hidden, L->intermediate, Is, x_dtype,
                           L->quant, L->down_quant) &&
          shared_q8 &&
@@ -624,6 +638,8 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
     d.ys = w.ys;
     d.y = w.moe.y;
     d.logits_ready = logits_ready;
+    d.shared_slot = layer_shared_slot(L, T, x_dtype) ? 1 : 0;
+    d.h_quant = L->down_quant;
     return launch_decode_layer(s, d, L->quant);
   }
   const int parts = router_logit_parts(T, H, E, x_dtype);

@@ -697,7 +697,69 @@ int launch_down_mfma(hipStream_t s, const DecodeArgs& a) {
   return launch_down_mfma_tr<16>(s, a);
 }
 
+// Route launch: router logit partials over E/4 x chunks workgroups (none
+// when the logits are ready), enough of them to stage x for the expert
+// kernels, then shared_wgs workgroups of the shared gate/up in K parts.
+int launch_route(hipStream_t s, const DecodeArgs& a, int shared_wgs) {
+  const bool xsplit = a.x_dtype == INFERNO_F32;
+  const int runs = a.T * a.H / 16;
+  const int need = std::max(std::max((runs + 255) / 256, (a.T * (a.H / kKBlock) + 3) / 4),
+                            a.stage_xr ? (a.T * a.H + 255) / 256 : 0);
+  const int gx = a.logits_ready ? 1 : (a.E + 3) / 4;
+  const int gy = a.logits_ready ? need : std::max(a.n_chunks, (need + gx - 1) / gx);
+  const unsigned grid = unsigned(gx * gy + shared_wgs);
+  const size_t lds = shared_wgs ? gate_up_lds(a.H / a.shared_parts, xsplit) : 0;
+  return timed(s, kTimerRoute,
+               shared_wgs ? "route+shared: route_kernel (router logit partials, Q8_0 "
+                            "shared gate/up in K parts)"
+                          : "route: route_kernel (router logit partials, x staging)",
+               [&] {
+                 if (xsplit)
+                   route_kernel<float><<<grid, 256, lds, s>>>(a, gx, gy);
+                 else
+                   route_kernel<uint16_t><<<grid, 256, lds, s>>>(a, gx, gy);
+                 INF_LAUNCHED();
+                 return INFERNO_OK;
+               });
+}
+
+// One token whose shared expert has the routed formats and width (the
+// Laguna XS layer, crates/backend/src/metal/laguna_xs.rs:1001-1144: the
+// shared expert as a ninth assignment of weight 1 next to the eight routed
+// ones): three launches, route (logits, x as f16 runs), the selecting run
+// gate/up over k + 1 slots, the run down summing k + 1 ranks plus the
+// residual.
+int launch_decode_shared_slot(hipStream_t s, DecodeArgs a, int quant) {
+  a.stage_x = nullptr;
+  a.stage_xm = nullptr;
+  a.xr_quant = quant;
+  a.h_mfma = 1;
+  a.ys = nullptr;
+  a.dpf_rows = a.dpf_row_bytes = 0;
+  a.max_slots = a.k;
+  if (int st = launch_route(s, a, 0)) return st;
+  int st = timed(s, kTimerGateUp,
+                 "runs+shared+select: gate_up_runs_multi_kernel (top-k in every workgroup's "
+                 "prologue; the routed tiles and the shared expert's as assignment k on f16 MFMA)",
+                 [&] { return launch_gate_up_runs_multi(s, a, quant, true); });
+  if (st) return st;
+  return timed(s, kTimerDown,
+               "runs-down+shared: down_runs_kernel (routed and shared down on f16 MFMA + "
+               "residual)",
+               [&] { return launch_down_runs(s, a, a.h_quant); });
+}
+
 }  // namespace
+
+bool decode_shared_slot_supported(size_t T, size_t k, size_t E, size_t H, size_t I, int x_dtype,
+                                  int quant, int down_quant) {
+  return T == 1 && k >= 1 && k <= size_t(kMaxTopK) && E <= size_t(kMaxExperts) &&
+         H % kKBlock == 0 && I % kKBlock == 0 && mfma_enabled() &&
+         !switch_off("INFERNO_DECODE_SHARED_SLOT") &&
+         (quant == INFERNO_Q2_K || quant == INFERNO_Q3_K || quant == INFERNO_Q4_K) &&
+         runs_multi_sel_covers(quant, int(H), x_dtype) &&
+         runs_down_covers(down_quant, int(H), int(I), int(k) + 1);
+}
 
 size_t decode_mfma_stage_words(size_t H) { return size_t(mfma_decode::stage_words(int(H))); }
 size_t decode_shared_partial_floats(size_t H, size_t Is) {
@@ -732,6 +794,8 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
     a.n_chunks = 1;
   }
   a.max_slots = std::min(a.E, a.T * a.k);
+  if (a.shared_slot) return launch_decode_shared_slot(s, a, quant);
+  a.h_quant = quant;
   const bool xsplit = a.x_dtype == INFERNO_F32;
   // gate/up: fp8 x fp4 matrix-core kernel (one Q2_K bf16 token), else the
   // f16-run matrix-core kernel (one token, any routed format, with its down
@@ -792,30 +856,9 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
     set_error("fused decode path does not cover this layer shape");
     return INFERNO_ERR_INVALID;
   }
-  // route: grid covers E/4 x chunks workgroups (and enough threads to stage x)
   {
-    const int runs = a.T * a.H / 16;
-    const int need = std::max(std::max((runs + 255) / 256, (a.T * (a.H / kKBlock) + 3) / 4),
-                              a.stage_xr ? (a.T * a.H + 255) / 256 : 0);
-    // with the logits ready, only the staging workgroups
-    const int gx = a.logits_ready ? 1 : (a.E + 3) / 4;
-    const int gy = a.logits_ready ? need : std::max(a.n_chunks, (need + gx - 1) / gx);
     const int shared_wgs = use_mfma ? a.Is / kRows * a.shared_parts : 0;
-    const unsigned grid = unsigned(gx * gy + shared_wgs);
-    const size_t lds = shared_wgs ? gate_up_lds(a.H / a.shared_parts, xsplit) : 0;
-    const int st = timed(s, kTimerRoute,
-                         shared_wgs ? "route+shared: route_kernel (router logit partials, Q8_0 "
-                                      "shared gate/up in K parts)"
-                                    : "route: route_kernel (router logit partials, x staging)",
-                         [&] {
-                           if (xsplit)
-                             route_kernel<float><<<grid, 256, lds, s>>>(a, gx, gy);
-                           else
-                             route_kernel<uint16_t><<<grid, 256, lds, s>>>(a, gx, gy);
-                           INF_LAUNCHED();
-                           return INFERNO_OK;
-                         });
-    if (st) return st;
+    if (int st = launch_route(s, a, shared_wgs)) return st;
   }
   // one token on the fp8 x fp4 gate/up: the selection and the shared down
   // run in the gate/up launch (no select launch)

@@ -38,6 +38,9 @@ struct DecodeArgs {
   uint32_t* stage_xm;     // [T, decode_mfma_stage_words(H)]: x staged for the MFMA gate/up
   uint32_t* stage_xr;     // [T, decode_runs_stage_words(H)]: x as f16 runs (runs gate/up)
   int xr_quant;           // format whose field offsets the x runs are staged for
+  int h_quant;            // format whose field offsets the h runs are staged for (the down's)
+  int shared_slot;        // 1: the shared expert (Is == I, the routed formats) is the
+                          // token's assignment k, weight 1 (one token, run kernels)
   float* shared_gu;       // [shared_parts][2][Is]: shared gate/up partial sums (MFMA path, T = 1)
   int shared_parts;       // K parts of the shared gate/up in the route launch
   float* ys;              // [T, H]: shared down output (MFMA down path)
@@ -58,6 +61,11 @@ struct DecodeArgs {
 bool decode_supported(size_t T, size_t k, size_t E, size_t H, size_t I, size_t Is, int x_dtype,
                       int quant, int down_quant);
 int decode_chunk(size_t H);
+// True when one token of a layer whose shared expert has the routed formats
+// (gate/up quant, down down_quant) and width I runs the shared expert as
+// assignment k of the run kernels (DecodeArgs::shared_slot).
+bool decode_shared_slot_supported(size_t T, size_t k, size_t E, size_t H, size_t I, int x_dtype,
+                                  int quant, int down_quant);
 // Words per token of the activation staging used by the MFMA gate/up kernel.
 size_t decode_mfma_stage_words(size_t H);
 // Words per token of the f16-run staging of x (fp32 tokens: split layout).

@@ -83,14 +83,14 @@ int down_per(hipStream_t s, const DecodeArgs& a) {
   if (int st = allow_lds(kern, attr)) return st;
   const int ntiles = a.H / TR;
   const unsigned grid = unsigned(std::min(ntiles, cus_now()));
-  kern<<<grid, kThreads, down_runs_lds<Q, NB, TR>(a.k), s>>>(a, ntiles);
+  kern<<<grid, kThreads, down_runs_lds<Q, NB, TR>(a.k + a.shared_slot), s>>>(a, ntiles);
   INF_LAUNCHED();
   return INFERNO_OK;
 }
 
 template <int Q, int NB, int TR>
 int down_tr(hipStream_t s, const DecodeArgs& a) {
-  const int per = down_runs_per<Q, NB, TR>(a.k);
+  const int per = down_runs_per<Q, NB, TR>(a.k + a.shared_slot);
   if (per <= 2) return down_per<Q, NB, TR, 2>(s, a);
   if (per <= 4) return down_per<Q, NB, TR, 4>(s, a);
   if (per <= 6) return down_per<Q, NB, TR, 6>(s, a);
@@ -99,13 +99,14 @@ int down_tr(hipStream_t s, const DecodeArgs& a) {
 
 template <int Q, int NB>
 int down_nb(hipStream_t s, const DecodeArgs& a) {
-  if (down_tr_fits<Q, NB, 16>(a.k)) return down_tr<Q, NB, 16>(s, a);
+  if (down_tr_fits<Q, NB, 16>(a.k + a.shared_slot)) return down_tr<Q, NB, 16>(s, a);
   return down_tr<Q, NB, 8>(s, a);
 }
 
 template <int Q>
 int down_q(hipStream_t s, const DecodeArgs& a) {
   switch (a.I / kKBlock) {
+    case 2: return down_nb<Q, 2>(s, a);
     case 3: return down_nb<Q, 3>(s, a);
     case 4: return down_nb<Q, 4>(s, a);
     case 6: return down_nb<Q, 6>(s, a);
@@ -121,6 +122,7 @@ bool down_nb_fits(int k) {
 template <int Q>
 bool down_fits(int NB, int k) {
   switch (NB) {
+    case 2: return down_nb_fits<Q, 2>(k);
     case 3: return down_nb_fits<Q, 3>(k);
     case 4: return down_nb_fits<Q, 4>(k);
     case 6: return down_nb_fits<Q, 6>(k);
@@ -147,12 +149,14 @@ bool runs_gate_up_covers(int quant, int H, int x_dtype) {
 }
 
 bool runs_down_covers(int quant, int H, int I, int k) {
-  if (I % kKBlock || H % 16 || k < 1 || k > kMaxTopK) return false;
+  // k: ranks summed, up to kMaxTopK routed ones plus the shared expert
+  if (I % kKBlock || H % 16 || k < 1 || k > kMaxTopK + 1) return false;
   const int NB = I / kKBlock;
   switch (quant) {
     case INFERNO_Q2_K: return down_fits<INFERNO_Q2_K>(NB, k);
     case INFERNO_Q3_K: return down_fits<INFERNO_Q3_K>(NB, k);
     case INFERNO_Q4_K: return down_fits<INFERNO_Q4_K>(NB, k);
+    case INFERNO_Q6_K: return down_fits<INFERNO_Q6_K>(NB, k);
     default: return false;
   }
 }
@@ -169,6 +173,7 @@ int runs_down_tile_rows(int quant, int I, int k) {
   auto pick = [&](auto q_c) {
     constexpr int Q = decltype(q_c)::value;
     switch (I / kKBlock) {
+      case 2: return down_tr_fits<Q, 2, 16>(k) ? 16 : 8;
       case 3: return down_tr_fits<Q, 3, 16>(k) ? 16 : 8;
       case 4: return down_tr_fits<Q, 4, 16>(k) ? 16 : 8;
       case 6: return down_tr_fits<Q, 6, 16>(k) ? 16 : 8;
@@ -178,6 +183,7 @@ int runs_down_tile_rows(int quant, int I, int k) {
   switch (quant) {
     case INFERNO_Q2_K: return pick(std::integral_constant<int, INFERNO_Q2_K>{});
     case INFERNO_Q3_K: return pick(std::integral_constant<int, INFERNO_Q3_K>{});
+    case INFERNO_Q6_K: return pick(std::integral_constant<int, INFERNO_Q6_K>{});
     default: return pick(std::integral_constant<int, INFERNO_Q4_K>{});
   }
 }
@@ -187,6 +193,7 @@ int runs_down_row_bytes(int quant, int I) {
   switch (quant) {
     case INFERNO_Q2_K: return NB * RF<INFERNO_Q2_K>::kBytes;
     case INFERNO_Q3_K: return NB * RF<INFERNO_Q3_K>::kBytes;
+    case INFERNO_Q6_K: return NB * RF<INFERNO_Q6_K>::kBytes;
     default: return NB * RF<INFERNO_Q4_K>::kBytes;
   }
 }
@@ -195,6 +202,7 @@ int launch_down_runs(hipStream_t s, const DecodeArgs& a, int quant) {
   switch (quant) {
     case INFERNO_Q2_K: return down_q<INFERNO_Q2_K>(s, a);
     case INFERNO_Q3_K: return down_q<INFERNO_Q3_K>(s, a);
+    case INFERNO_Q6_K: return down_q<INFERNO_Q6_K>(s, a);
     default: return down_q<INFERNO_Q4_K>(s, a);
   }
 }

@@ -45,6 +45,9 @@ typedef uint32_t u32_a2 __attribute__((aligned(2)));
 constexpr int kWaves = 16;
 constexpr int kThreads = 64 * kWaves;
 constexpr float kTwoM24 = 1.0f / 16777216.0f;
+// Expert id of the shared expert when it runs as the token's assignment k
+// (DecodeArgs::shared_slot): its gate/up/down rows come from sgate/sup/sdown.
+constexpr uint32_t kSharedId = 0xffffffffu;
 
 __host__ __device__ constexpr int run_words(int K) { return K / 2 + K / 8; }
 
@@ -245,6 +248,81 @@ struct RF<INFERNO_Q4_K> {
   }
 };
 
+// Q6_K [ql 128 | qh 64 | scales 16 (int8) | d] (crates/gguf/src/lib.rs:
+// 1418-1470): value j = 128 h + 32 u + l (half h, quarter u, l < 32) is
+// q6 = (ql[64 h + 32 (u & 1) + l] >> 4 (u >> 1)) & 15 | ((qh[32 h + l] >> 2 u)
+// & 3) << 4, value = d sc[8 h + 2 u + l / 16] (q6 - 32): run r (16 values) =
+// 8 h + 2 u + s has scale byte r. MFMA (h, u): lane group q = 2 s + hf takes
+// ql bytes 64 h + 32 (u & 1) + 8 q .. + 7 and qh bytes 32 h + 8 q .. + 7, the
+// six bits assembled inside each 16-bit half at bit 4 (u >> 1) (the nibble
+// where it lies, qh's two bits above it): an exact f16 subnormal q6 2^(4 (u
+// >> 1) - 24). Run m is live in lane groups q with q >> 1 == (m & 1), half
+// hf = q & 1 of its values, in MFMA (m >> 3, (m >> 1) & 3).
+template <>
+struct RF<INFERNO_Q6_K> {
+  static constexpr int kBytes = 210;
+  typedef mfma_decode::half2v half2v_t;
+  __host__ __device__ static int run_shift(int r) { return 4 * ((r >> 2) & 1); }
+  template <int NA>
+  __device__ static void dot(const uint8_t* blk, const uint32_t* const (&cols)[NA],
+                             const uint32_t* zero, int n, int q, floatx4 (&C)[NA]) {
+    typedef uint32_t u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
+    const bool act_q = (q >> 1) == (n & 1);
+    const int mh = n >> 3, mu = (n >> 1) & 3;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const u32x2_a2 l0 = *reinterpret_cast<const u32x2_a2*>(blk + 64 * h + 8 * q);
+      const u32x2_a2 l1 = *reinterpret_cast<const u32x2_a2*>(blk + 64 * h + 32 + 8 * q);
+      const u32x2_a2 hq = *reinterpret_cast<const u32x2_a2*>(blk + 128 + 32 * h + 8 * q);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t w0 = (u & 1) ? l1.x : l0.x, w1 = (u & 1) ? l1.y : l0.y;
+        const int nb = 4 * (u >> 1);  // the field's bit offset
+        const uint32_t M = 0x000f000fu << nb, MH = 0x00300030u << nb;
+        // qh bits 2 u, 2 u + 1 of each byte moved to bits nb + 4, nb + 5
+        auto hb = [&](uint32_t x) {
+          const int sh = nb + 4 - 2 * u;
+          return (sh >= 0 ? (x << sh) : (x >> -sh)) & MH;
+        };
+        const uint4 bv = make_uint4((w0 & M) | hb(hq.x), ((w0 >> 8) & M) | hb(hq.x >> 8),
+                                    (w1 & M) | hb(hq.y), ((w1 >> 8) & M) | hb(hq.y >> 8));
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+          const uint32_t* src = (act_q && mh == h && mu == u) ? cols[a] + n * 8 + 4 * (q & 1) : zero;
+          C[a] = mfma(load_a(src), bv, C[a]);
+        }
+      }
+    }
+  }
+  __device__ static float epilogue(const uint8_t* blk, floatx4 C, float4 sums, float4 kk,
+                                   int q) {
+    // runs 4 q + j: int8 scales at bytes 192 + 4 q + j
+    const uint32_t sw = *reinterpret_cast<const u32_a2*>(blk + 192 + 4 * q);
+    const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 208));
+    const float c[4] = {C[0], C[1], C[2], C[3]};
+    const float s[4] = {sums.x, sums.y, sums.z, sums.w};
+    const float f[4] = {kk.x, kk.y, kk.z, kk.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float sc = float(int8_t((sw >> (8 * j)) & 0xffu));
+      acc = fmaf(sc, fmaf(c[j] * f[j], kTwoM24, -32.0f * s[j]), acc);
+    }
+    return d * acc;
+  }
+};
+
+// Bit offset at which format `quant` keeps the fields of run r (r < 16) of a
+// super-block column: the scale the runs of h are staged with for the down
+// kernel of that format.
+__device__ __forceinline__ int run_shift_of(int quant, int r) {
+  switch (quant) {
+    case INFERNO_Q4_K: return RF<INFERNO_Q4_K>::run_shift(r);
+    case INFERNO_Q6_K: return RF<INFERNO_Q6_K>::run_shift(r);
+    default: return RF<INFERNO_Q2_K>::run_shift(r);  // Q2_K, Q3_K
+  }
+}
+
 // ------------------------------------------------------------- staging
 
 // Words per staged x row: one f16 term (bf16 tokens), or two (fp32 tokens:
@@ -422,7 +500,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_kernel(DecodeArgs p, in
       const float h = silu(r) * u * slot_w[slot];
       if (tid < 16)
         stage_run16(h, p.stage_h + size_t(a) * run_words(I), I, tile,
-                           RF<Q>::run_shift(tile & 15));
+                    run_shift_of(p.h_quant, tile & 15));
     }
   }
 }
@@ -443,11 +521,13 @@ struct DownShape {
   static_assert(TR * rb % 16 == 0, "a rank tile must be whole 16-byte chunks");
 };
 
+// k: the ranks the kernel sums (the routed k, plus the shared expert when
+// it runs as rank k)
 template <int Q, int NB, int TR>
 __host__ __device__ constexpr size_t down_runs_lds(int k) {
   using S = DownShape<Q, NB, TR>;
   return size_t(k * S::Sh + 4) * 4 + size_t(k * TR) * S::rb + size_t(kWaves * 16) * 4 +
-         size_t(kMaxTopK) * 4;
+         size_t(kMaxTopK + 1) * 4;
 }
 
 template <int Q, int NB, int TR>
@@ -461,7 +541,7 @@ __global__ void __launch_bounds__(kThreads) down_runs_kernel(DecodeArgs p, int n
   extern __shared__ uint32_t smem[];
   constexpr int K = S::K, rb = S::rb, Sh = S::Sh;
   constexpr int cr = TR * rb / 16;  // 16-byte chunks per rank tile
-  const int k = p.k;
+  const int k = p.k + p.shared_slot;  // ranks summed: rank p.k is the shared expert
   uint32_t* hs = smem;                                     // [k][Sh]
   uint32_t* zero = hs + k * Sh;
   uint8_t* tl = reinterpret_cast<uint8_t*>(zero + 4);     // [k][TR rows of rb], contiguous
@@ -471,7 +551,8 @@ __global__ void __launch_bounds__(kThreads) down_runs_kernel(DecodeArgs p, int n
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, q = lane >> 4;
   const int nr = n < TR ? n : TR - 1;
-  if (tid < k) rank_e[tid] = p.ids[tid];
+  if (tid < p.k) rank_e[tid] = p.ids[tid];
+  if (tid == p.k && p.shared_slot) rank_e[tid] = kSharedId;
   u32x4 v[PER];
   auto fetch = [&](int t) {
     const int nv = k * cr;
@@ -480,8 +561,9 @@ __global__ void __launch_bounds__(kThreads) down_runs_kernel(DecodeArgs p, int n
       int i = j * kThreads + tid;
       i = i < nv ? i : nv - 1;  // clamped; the extra chunks are not stored
       const int r = i / cr, w = i - r * cr;
-      const u32x4* src = reinterpret_cast<const u32x4*>(
-          p.down + size_t(rank_e[r]) * p.down_stride + size_t(t) * TR * rb);
+      const uint32_t e = rank_e[r];
+      const uint8_t* base = e == kSharedId ? p.sdown : p.down + size_t(e) * p.down_stride;
+      const u32x4* src = reinterpret_cast<const u32x4*>(base + size_t(t) * TR * rb);
       v[j] = src[w];
     }
   };
@@ -600,7 +682,7 @@ struct MultiGateUpShape {
 
 // LDS of the selecting variant's additions: topk1_wave's scratch and the
 // slot table (expert, assignment, routing weight per slot)
-constexpr size_t kSelMultiLds = 8 + sizeof(Top1Lds) + size_t(3 * kMaxTopK) * 4;
+constexpr size_t kSelMultiLds = 8 + sizeof(Top1Lds) + size_t(3 * (kMaxTopK + 1)) * 4;
 
 template <int Q, int NB, bool SPLIT, int NT, bool SEL = false>
 __host__ __device__ constexpr size_t gate_up_multi_lds() {
@@ -630,9 +712,10 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
   // SEL: topk1_wave's scratch (8-byte aligned: every region above is a
   // whole number of 8-byte words) and the slot table
   Top1Lds* tk = reinterpret_cast<Top1Lds*>(tok_ab + 2 * NT);
+  // (kMaxTopK + 1 entries: the shared expert as slot k)
   uint32_t* sel_e = reinterpret_cast<uint32_t*>(tk + 1);
-  uint32_t* sel_a = sel_e + kMaxTopK;
-  float* sel_w = reinterpret_cast<float*>(sel_a + kMaxTopK);
+  uint32_t* sel_a = sel_e + kMaxTopK + 1;
+  float* sel_w = reinterpret_cast<float*>(sel_a + kMaxTopK + 1);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, q = lane >> 4;
@@ -650,11 +733,16 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
         sel_a[lane] = rank;
         sel_w[lane] = tk->w[rank];
       }
+      if (lane == 0 && p.shared_slot) {  // the shared expert: assignment k, weight 1
+        sel_e[k] = kSharedId;
+        sel_a[k] = uint32_t(k);
+        sel_w[k] = 1.0f;
+      }
       __builtin_amdgcn_s_setprio(0);
       if (blockIdx.x == 0) select1_write(p, tk);
     }
     __syncthreads();
-    ntiles = k * tiles_i;  // one token: every slot is a distinct expert
+    ntiles = (k + p.shared_slot) * tiles_i;  // one token: every slot is a distinct expert
   } else {
     ntiles = int(p.active[0]) * tiles_i;
   }
@@ -672,12 +760,20 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
   if (t >= ntiles) return;  // uniform per workgroup
   u32x4 v[PER];
   RowPrefetch<NT, Sx / 4> xr;
-  auto row_of = [&](uint32_t a) { return p.stage_xr + size_t(a / uint32_t(k)) * Sx; };
+  // token of assignment a (the shared expert's assignments T k + t follow
+  // the routed ones)
+  const uint32_t Tk = uint32_t(p.T) * uint32_t(k);
+  auto row_of = [&](uint32_t a) {
+    return p.stage_xr + size_t(a < Tk ? a / uint32_t(k) : a - Tk) * Sx;
+  };
   auto fetch = [&](int tt) {
     const uint4 s2 = slot_of(tt / tiles_i);
-    const size_t off = size_t(s2.x) * p.gate_stride + size_t(tt % tiles_i) * 16 * size_t(rb);
-    const u32x4* g4 = reinterpret_cast<const u32x4*>(p.gate + off);
-    const u32x4* u4 = reinterpret_cast<const u32x4*>(p.up + off);
+    const size_t off = size_t(tt % tiles_i) * 16 * size_t(rb);
+    const bool sh = s2.x == kSharedId;
+    const u32x4* g4 =
+        reinterpret_cast<const u32x4*>((sh ? p.sgate : p.gate + size_t(s2.x) * p.gate_stride) + off);
+    const u32x4* u4 =
+        reinterpret_cast<const u32x4*>((sh ? p.sup : p.up + size_t(s2.x) * p.gate_stride) + off);
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       int i = j * kThreads + tid;
@@ -753,7 +849,8 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
         }
         const uint32_t a = tok_a[ti];
         const float h = silu(g) * u * weight_of(slot, a);
-        stage_run16(h, p.stage_h + size_t(a) * run_words(I), I, tile, RF<Q>::run_shift(tile & 15));
+        stage_run16(h, p.stage_h + size_t(a) * run_words(I), I, tile,
+                    run_shift_of(p.h_quant, tile & 15));
       }
       // the next writes of part and xs come after a barrier these lanes reach
     }

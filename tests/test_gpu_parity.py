@@ -502,15 +502,61 @@ def test_layer_runs_multi_decode(cuda, quant, H, E, I, k, T, dt):
 # Q4_K or Q6_K down, shared expert Q4_K gate/up with the routed down format,
 # at c1's shape (H 2048, 64 experts, I 768, top-8 softmax, fp32 tokens),
 # one token (16 seeded inputs), 16 tokens, and 64 tokens (512 assignments:
-# the grouped GEMM path with the shared expert on the GEMV kernels).
+# the grouped GEMM path). Shared width 768 is the XS layer's own (the shared
+# expert as the token's ninth assignment, laguna_xs.rs:1001-1144): one token
+# runs it as assignment k of the run kernels, asserted below; 1024 (another
+# width) keeps the shared expert on its own kernels.
+@pytest.mark.parametrize("Is", [768, 1024])
 @pytest.mark.parametrize("down", [Q4_K, Q6_K])
 @pytest.mark.parametrize("T", [1, 16, 64])
-def test_layer_laguna_xs_q4k_shared(cuda, down, T):
+def test_layer_laguna_xs_q4k_shared(cuda, down, T, Is):
     c1 = cf.CONFIGS["c1"]
-    cfg = cf.Config(f"xs_q4k_down{down}", 60 + down, c1.hidden, c1.experts, c1.intermediate,
-                    c1.top_k, (Q4_K,), c1.score_fn, True, 1.0, 0.0, 1024, torch.float32, (T,),
-                    down_quant=down, shared_quant=Q4_K)
+    cfg = cf.Config(f"xs_q4k_down{down}_s{Is}", 60 + down, c1.hidden, c1.experts,
+                    c1.intermediate, c1.top_k, (Q4_K,), c1.score_fn, True, 1.0, 0.0, Is,
+                    torch.float32, (T,), down_quant=down, shared_quant=Q4_K)
     _layer_parity(cuda, cfg, T, variants=16 if T == 1 else 1)
+    if T != 1:
+        return
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=1)
+    ops.kernel_timing(True)
+    try:
+        lt.layer.forward(cf.make_input(cfg, 1, device=cuda), None)
+        torch.cuda.synchronize()
+        gu = ops.kernel_timing_label(ops.TIMER_GATE_UP)
+        dn = ops.kernel_timing_label(ops.TIMER_DOWN)
+    finally:
+        ops.kernel_timing(False)
+    if Is == c1.intermediate:
+        assert gu.startswith("runs+shared+select:"), gu
+        assert dn.startswith("runs-down+shared:"), dn
+    else:
+        assert gu.startswith("stage:"), gu
+
+
+# The shared expert as assignment k of the one-token run kernels for every
+# routed gate/up format and every down format, bf16 and fp32 tokens, k up to
+# 16 (the slot table's last entry), against the oracle.
+@pytest.mark.parametrize("quant,down,H,E,I,k,dt", [
+    (Q4_K, Q6_K, 2048, 256, 512, 8, torch.bfloat16),
+    (Q2_K, Q2_K, 4096, 128, 1536, 10, torch.bfloat16),
+    (Q3_K, Q6_K, 2048, 64, 1024, 16, torch.float32),
+    (Q4_K, Q4_K, 3072, 32, 2048, 4, torch.float32)])
+def test_layer_decode_shared_slot_shapes(cuda, quant, down, H, E, I, k, dt):
+    cfg = cf.Config(f"shared_slot_q{quant}_d{down}_h{H}_i{I}_k{k}", 80 + quant + down, H, E, I, k,
+                    (quant,), cf.SCORE_SIGMOID, True, 2.5, 0.1, I, dt, (1,), down_quant=down,
+                    shared_quant=quant)
+    _layer_parity(cuda, cfg, 1, variants=4)
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=1)
+    ops.kernel_timing(True)
+    try:
+        lt.layer.forward(cf.make_input(cfg, 1, device=cuda), None)
+        torch.cuda.synchronize()
+        gu = ops.kernel_timing_label(ops.TIMER_GATE_UP)
+        dn = ops.kernel_timing_label(ops.TIMER_DOWN)
+    finally:
+        ops.kernel_timing(False)
+    assert gu.startswith("runs+shared+select:"), gu
+    assert dn.startswith("runs-down+shared:"), dn
 
 
 def test_layer_c3_glm_q3k_prefill_all_tokens(cuda):
