@@ -663,18 +663,23 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
                                   sdq_staged, w.moe.y, k, nullptr, residual, T, Is, H, out);
   };
   if (use_mfma(L->quant, L->down_quant, T, k, E, H, I)) {
-    // a shared expert in another format than Q8_0 runs its gate/up first,
-    // while moe.stage_x still holds its staging (the f16 copy of x reuses it)
-    if (!shared_q8 && (st = shared_gate_up_gemv(false))) return st;
+    // the shared expert on the dense MFMA GEMMs when its formats have them
+    // (Q8_0; the Laguna XS Q4_K gate/up with Q4_K or Q6_K down), else on the
+    // GEMV kernels
+    const bool shared_gemm = Is && prefill_dense_supported(sq, sdq, H, Is);
+    // a shared expert on the GEMVs runs its gate/up first, while moe.stage_x
+    // still holds its staging (the f16 copy of x reuses it)
+    if (Is && !shared_gemm && (st = shared_gate_up_gemv(false))) return st;
     // x in f16 once for the routed and the shared expert GEMMs
     uint16_t* x16 = reinterpret_cast<uint16_t*>(w.moe.stage_x);
     if ((st = launch_to_f16(s, x, x_dtype, T, H, x16))) return st;
     if ((st = run_routed(s, L->quant, L->down_quant, L->gate, L->up, L->down, x, x_dtype, ids,
                          wts, T, k, E, H, I, w.moe, false, x16)))
       return st;
-    if (!shared_q8) return shared_down_gemv();
-    if (Is && (st = launch_prefill_dense(s, L->shared_gate, L->shared_up, L->shared_down, x16, T,
-                                         H, Is, reinterpret_cast<uint16_t*>(w.hs), w.ys)))
+    if (Is && !shared_gemm) return shared_down_gemv();
+    if (shared_gemm &&
+        (st = launch_prefill_dense(s, sq, sdq, L->shared_gate, L->shared_up, L->shared_down, x16,
+                                   T, H, Is, reinterpret_cast<uint16_t*>(w.hs), w.ys)))
       return st;
     return launch_prefill_combine(s, w.moe.y, Is ? w.ys : nullptr, residual, T, k, H, out);
   }

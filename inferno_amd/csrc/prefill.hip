@@ -209,6 +209,44 @@ struct Frag<INFERNO_Q4_K> {
   }
 };
 
+// Q6_K [ql 128 | qh 64 | scales 16 (int8) | d]: value j = 128 h + 32 u + l
+// uses q6 = (ql[64 h + 32 (u & 1) + l] >> 4 (u >> 1)) & 15 | ((qh[32 h + l]
+// >> 2 u) & 3) << 4 and value = d sc[8 h + 2 u + l / 16] (q6 - 32)
+// (crates/gguf/src/lib.rs:1418-1470). Chunk qc = 2 h + (u >> 1): step s has
+// u = 2 (qc & 1) + (s >> 1) and l = 16 (s & 1) + 8 kg + i. The six bits are
+// assembled per byte, then one v_fma_mix per value: q6 * (d sc) - 32 d sc,
+// rounded once as the reference's fp32 (d sc) (q6 - 32) is, then to f16.
+template <>
+struct Frag<INFERNO_Q6_K> {
+  static constexpr int kBytes = 210, kRaw = 14;
+  __device__ static void load(const uint8_t* b, int qc, int kg, uint32_t r[kRaw]) {
+    const int h = qc >> 1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {  // ql bytes 64 h + 32 (s >> 1) + 16 (s & 1) + 8 kg
+      const uint2 v = ld_u2(b + 64 * h + 16 * s + 8 * kg);
+      r[2 * s] = v.x;
+      r[2 * s + 1] = v.y;
+    }
+    const uint2 q0 = ld_u2(b + 128 + 32 * h + 8 * kg);
+    const uint2 q1 = ld_u2(b + 128 + 32 * h + 16 + 8 * kg);
+    r[8] = q0.x; r[9] = q0.y; r[10] = q1.x; r[11] = q1.y;
+    r[12] = ld_u1(b + 192 + 8 * h + 4 * (qc & 1));  // scales 8 h + 2 u + {0, 1}
+    r[13] = *reinterpret_cast<const uint16_t*>(b + 208);  // d
+  }
+  template <int QC>
+  __device__ static half8 get(const uint32_t r[kRaw], int s) {
+    const int u = 2 * (QC & 1) + (s >> 1), nib = QC & 1;
+    auto six = [&](uint32_t w, uint32_t x) {
+      return ((w >> (4 * nib)) & 0x0f0f0f0fu) | (((x >> (2 * u)) & 0x03030303u) << 4);
+    };
+    const uint32_t w0 = six(r[2 * s], r[8 + 2 * (s & 1)]);
+    const uint32_t w1 = six(r[2 * s + 1], r[9 + 2 * (s & 1)]);
+    const float d = f16_bits_to_f32_fast(uint16_t(r[13]));
+    const float dsc = d * float(int8_t(byte_of(r[12], 2 * (s >> 1) + (s & 1))));
+    return dequant8(w0, w1, 0x003f003fu, __builtin_amdgcn_ldexpf(dsc, 24), -32.0f * dsc);
+  }
+};
+
 // Q8_0: a K unit is eight 34-byte blocks [d | int8 x32]; value = d * q
 // (crates/gguf/src/lib.rs:1472-1499). Codes enter as q ^ 0x80 = q + 128.
 template <>
@@ -920,6 +958,9 @@ int launch_gemm_q(hipStream_t s, int quant, const GemmArgs& a, unsigned grid_y) 
     case INFERNO_Q3_K: return launch_gemm<INFERNO_Q3_K, NMAT, TM>(s, a, grid_y);
     case INFERNO_Q4_K: return launch_gemm<INFERNO_Q4_K, NMAT, TM>(s, a, grid_y);
     case INFERNO_Q8_0: return launch_gemm<INFERNO_Q8_0, NMAT, TM>(s, a, grid_y);
+    case INFERNO_Q6_K:  // a down format only
+      if constexpr (NMAT == 1) return launch_gemm<INFERNO_Q6_K, 1, TM>(s, a, grid_y);
+      break;
   }
   set_error("quant kind has no MFMA prefill GEMM");
   return INFERNO_ERR_INVALID;
@@ -1000,7 +1041,14 @@ bool prefill_routed_supported(int quant, int down_quant, size_t H, size_t I, siz
   auto routed = [](int q) {
     return q == INFERNO_Q2_K || q == INFERNO_Q3_K || q == INFERNO_Q4_K;
   };
-  return routed(quant) && routed(down_quant) && H % kUnit == 0 && I % kUnit == 0 && E <= 256;
+  return routed(quant) && (routed(down_quant) || down_quant == INFERNO_Q6_K) &&
+         H % kUnit == 0 && I % kUnit == 0 && E <= 256;
+}
+
+bool prefill_dense_supported(int quant, int down_quant, size_t H, size_t Is) {
+  return prefill_supported(quant) && quant != INFERNO_Q6_K &&
+         (prefill_supported(down_quant) || down_quant == INFERNO_Q6_K) && H % kUnit == 0 &&
+         Is % kUnit == 0 && H % kTileN == 0 && Is % kTileN == 0;
 }
 
 size_t prefill_plan_words(size_t A, size_t E) {
@@ -1062,9 +1110,9 @@ int launch_prefill_down(hipStream_t s, const PrefillRouted& p) {
   return launch_tiled<1>(s, p.down_quant, d, v);
 }
 
-int launch_prefill_dense(hipStream_t s, const void* gate, const void* up, const void* down,
-                         const uint16_t* x16, size_t T, size_t H, size_t Is, uint16_t* h16,
-                         float* ys) {
+int launch_prefill_dense(hipStream_t s, int quant, int down_quant, const void* gate,
+                         const void* up, const void* down, const uint16_t* x16, size_t T,
+                         size_t H, size_t Is, uint16_t* h16, float* ys) {
   if (T == 0) return INFERNO_OK;
   if (H % kUnit || Is % kUnit) {
     set_error("MFMA prefill path needs 256-multiple dimensions");
@@ -1080,7 +1128,7 @@ int launch_prefill_dense(hipStream_t s, const void* gate, const void* up, const 
   g.K = int(H);
   g.h_out = h16;
   int st;
-  if ((st = launch_dense<2>(s, INFERNO_Q8_0, g, T))) return st;
+  if ((st = launch_dense<2>(s, quant, g, T))) return st;
   GemmArgs d{};
   d.w0 = static_cast<const uint8_t*>(down);
   d.xin = h16;
@@ -1089,7 +1137,7 @@ int launch_prefill_dense(hipStream_t s, const void* gate, const void* up, const 
   d.N = int(H);
   d.K = int(Is);
   d.y_out = ys;
-  return launch_dense<1>(s, INFERNO_Q8_0, d, T);
+  return launch_dense<1>(s, down_quant, d, T);
 }
 
 int launch_prefill_combine(hipStream_t s, const float* y, const float* ys, const float* residual,

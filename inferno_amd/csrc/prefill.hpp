@@ -37,10 +37,14 @@ int launch_prefill_gate_up(hipStream_t s, const PrefillRouted& p);
 // Routed down over the same tiles (after launch_prefill_gate_up): writes y.
 int launch_prefill_down(hipStream_t s, const PrefillRouted& p);
 
-// Dense Q8_0 expert over all T rows: h16 = silu(x G^T) * (x U^T); ys = h16 D^T.
-int launch_prefill_dense(hipStream_t s, const void* gate, const void* up, const void* down,
-                         const uint16_t* x16, size_t T, size_t H, size_t Is, uint16_t* h16,
-                         float* ys);
+// True when a dense (shared) expert of these formats and widths has the
+// MFMA GEMMs (gate/up Q2_K/Q3_K/Q4_K/Q8_0, down also Q6_K).
+bool prefill_dense_supported(int quant, int down_quant, size_t H, size_t Is);
+// Dense expert over all T rows (gate/up format quant, down down_quant):
+// h16 = silu(x G^T) * (x U^T); ys = h16 D^T.
+int launch_prefill_dense(hipStream_t s, int quant, int down_quant, const void* gate,
+                         const void* up, const void* down, const uint16_t* x16, size_t T,
+                         size_t H, size_t Is, uint16_t* h16, float* ys);
 
 // out = (residual + ys) + sum over ranks of y[t*k + r] (rank order); residual,
 // ys may be null.

@@ -175,10 +175,10 @@ def _skewed_ids(T, E, k, hot=(0, 1), share=(1.0, 0.8)):
     return np.array(rows, np.uint32).reshape(-1)
 
 
-@pytest.mark.parametrize("quant", [Q2_K, Q3_K, Q4_K])
+@pytest.mark.parametrize("quant,down", [(Q2_K, Q2_K), (Q3_K, Q3_K), (Q4_K, Q4_K), (Q4_K, Q6_K)])
 @pytest.mark.parametrize("T,H,I,E,k,bf16,skew", [(64, 512, 256, 16, 4, True, False),
                                                  (96, 768, 512, 8, 4, False, True)])
-def test_gguf_moe_mfma_prefill(cuda, quant, T, H, I, E, k, bf16, skew):
+def test_gguf_moe_mfma_prefill(cuda, quant, down, T, H, I, E, k, bf16, skew):
     # T * k >= 256 assignments: the MFMA grouped GEMM (f16 operands, fp32
     # accumulation). The skewed case gives two experts >= 64 rows (128-row
     # tiles) next to small experts (32-row tiles).
@@ -188,22 +188,29 @@ def test_gguf_moe_mfma_prefill(cuda, quant, T, H, I, E, k, bf16, skew):
     seed = 77 + quant
     gate = ph.to_np(ops.synth_quantized(quant, seed, 0.02, E * I, H, cuda))
     up = ph.to_np(ops.synth_quantized(quant, seed + 1, 0.02, E * I, H, cuda))
-    dn = ph.to_np(ops.synth_quantized(quant, seed + 2, 0.02, E * H, I, cuda))
+    dn = ph.to_np(ops.synth_quantized(down, seed + 2, 0.02, E * H, I, cuda))
     x = torch.randn(T, H, device=cuda)
     if bf16:
         x = x.bfloat16()
     ids = (_skewed_ids(T, E, k) if skew else
            np.stack([rng.permutation(E)[:k] for _ in range(T)]).reshape(-1).astype(np.uint32))
     w = rng.random(T * k).astype(np.float32)
-    args = (quant, quant, dev(gate, cuda), dev(up, cuda), dev(dn, cuda), x,
+    args = (quant, down, dev(gate, cuda), dev(up, cuda), dev(dn, cuda), x,
             dev(ids.view(np.int32), cuda), dev(w, cuda), k, E, I)
     out = ops.gguf_moe(*args)
     out2 = ops.gguf_moe(*args)
     torch.cuda.synchronize()
     assert torch.equal(out, out2), "MFMA prefill output is not bitwise reproducible"
-    ref = orc.moe_routed(quant, quant, gate, up, dn, ph.x_f32(x), ids, w, E, k, I)
+    ref = orc.moe_routed(quant, down, gate, up, dn, ph.x_f32(x), ids, w, E, k, I)
     err = rn.rel_l2(ph.to_np(out), ref)
     print(f"rel_l2={err:.3e}")
+    ops.kernel_timing(True)
+    try:
+        ops.gguf_moe(*args)
+        torch.cuda.synchronize()
+        assert ops.kernel_timing_label(ops.TIMER_DOWN).startswith("prefill:")
+    finally:
+        ops.kernel_timing(False)
     assert err < ph.TOL_REL_L2
 
 
@@ -515,6 +522,16 @@ def test_layer_laguna_xs_q4k_shared(cuda, down, T, Is):
                     c1.intermediate, c1.top_k, (Q4_K,), c1.score_fn, True, 1.0, 0.0, Is,
                     torch.float32, (T,), down_quant=down, shared_quant=Q4_K)
     _layer_parity(cuda, cfg, T, variants=16 if T == 1 else 1)
+    if T == 64:  # the grouped GEMMs, Q6_K down included, and the dense shared GEMMs
+        lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
+        ops.kernel_timing(True)
+        try:
+            lt.layer.forward(cf.make_input(cfg, T, device=cuda), None)
+            torch.cuda.synchronize()
+            assert ops.kernel_timing_label(ops.TIMER_GATE_UP).startswith("prefill:")
+            assert ops.kernel_timing_label(ops.TIMER_DOWN).startswith("prefill:")
+        finally:
+            ops.kernel_timing(False)
     if T != 1:
         return
     lt = cf.build_layer(cfg, 0, cuda, max_tokens=1)
