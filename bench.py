@@ -137,7 +137,14 @@ def main():
     # assignments (routed only).
     quants = list(cfg.quants)
     gu_per_expert = [2 * I * (H // 256) * ops.block_bytes(q) for q in quants]
-    dn_per_expert = [H * (I // 256) * ops.block_bytes(q) for q in quants]
+    dn_per_expert = [H * (I // 256) * ops.block_bytes(cfg.down_quant or q) for q in quants]
+    # shared expert bytes per layer: gate + up, down (Q8_0, or the Laguna XS
+    # formats: the shared gate/up format and the routed down format)
+    Is = cfg.shared_intermediate
+    sq = cfg.shared_quant
+    sdq = cfg.shared_down_quant or (sq if sq == cf.Q8_0 else (cfg.down_quant or quants[0]))
+    shared_gu = 2 * Is * H // ops.block_values(sq) * ops.block_bytes(sq) if Is else 0
+    shared_dn = H * Is // ops.block_values(sdq) * ops.block_bytes(sdq) if Is else 0
     reps = max(args.steps, 64) if not prefill else max(args.steps, 10)
     timers = [ops.TIMER_GATE_UP, ops.TIMER_DOWN, ops.TIMER_ROUTE, ops.TIMER_SELECT]
     uniq = [0] * n_sub
@@ -179,12 +186,10 @@ def main():
     gu_routed = sum(g * u for g, u in zip(gu_per_expert, uniq_sub)) / n_sub  # per launch
     dn_routed = sum(d * u for d, u in zip(dn_per_expert, uniq_sub)) / n_sub
     layer_routed_bytes = (gu_routed + dn_routed) * n_sub
-    shared_bytes = n_sub * 3 * cfg.shared_intermediate * (H // 32) * 34 if cfg.shared_intermediate else 0
+    shared_bytes = n_sub * (shared_gu + shared_dn)
     router_bytes = n_sub * E * H * 4
     extra = {}
     if not prefill:
-        shared_gu = 2 * cfg.shared_intermediate * (H // 32) * 34
-        shared_dn = cfg.shared_intermediate * (H // 32) * 34
         kinds = {tm: labels[tm].split(":")[0] for tm in timers}
         # a stack mixes formats: the label is the last layer's, so the shared
         # bytes follow the kind of each layer's launch, read per layer below
@@ -195,14 +200,16 @@ def main():
             "route": {"label": labels[ops.TIMER_ROUTE], "launch_us": us[ops.TIMER_ROUTE],
                       "bytes_per_launch": E * H * 4 + (shared_gu if rt_kind == "route+shared" else 0)},
             "gate_up": {"label": labels[ops.TIMER_GATE_UP], "launch_us": gu_us,
-                        "bytes_per_launch": gu_routed + (shared_gu if gu_kind in ("tiles", "ring") else 0)
+                        "bytes_per_launch": gu_routed
+                        + (shared_gu if gu_kind in ("tiles", "ring", "runs+shared+select") else 0)
                         + (shared_dn if gu_kind == "mfma+select" else 0),
                         "routed_bytes_per_launch": gu_routed,
                         "traffic_file": {"mfma": "gate_up_fp4_q2k_c2_decode_traffic.txt",
                                          "mfma+select": "gate_up_sel_fp4_q2k_c2_decode_traffic.txt",
                                          "tiles": "gate_up_q2k_c2_decode_traffic.txt"}.get(gu_kind)},
             "down": {"label": labels[ops.TIMER_DOWN], "launch_us": dn_us,
-                     "bytes_per_launch": dn_routed + (shared_dn if dn_kind == "down8" else 0),
+                     "bytes_per_launch": dn_routed
+                     + (shared_dn if dn_kind in ("down8", "runs-down+shared") else 0),
                      "routed_bytes_per_launch": dn_routed,
                      "traffic_file": {"down8": "down8_q2k_c2_decode_traffic.txt",
                                       "mfma-down": "down_mfma_q2k_c2_decode_traffic.txt"}.get(dn_kind)},
@@ -273,11 +280,11 @@ def main():
     # packed-f16 tile kernels otherwise), always fp32 accumulation
     gu_label = labels[ops.TIMER_GATE_UP]
     dn_label = labels[ops.TIMER_DOWN]
-    dn_mfma = dn_label.startswith(("mfma-down", "runs-down", "runs-multi-down"))
+    dn_mfma = dn_label.startswith(("mfma-down", "runs-down", "runs-multi-down", "prefill"))
     down_t = "f16 MFMA down" if dn_mfma else "f16-dot2 down"
     if gu_label.startswith("mfma"):
         dtype = f"e4m3x2*e2m1 MFMA gate/up, {down_t}, f32 acc"
-    elif gu_label.startswith("runs32"):
+    elif gu_label.startswith("runs") and cfg.x_dtype == torch.float32:
         dtype = f"f16x2-term MFMA gate/up (fp32 x), {down_t}, f32 acc"
     elif gu_label.startswith("runs"):
         dtype = f"f16 MFMA gate/up, {down_t}, f32 acc"
@@ -397,10 +404,11 @@ def cpu_baseline(cfg, units, xs, residual, T, seconds):
             ids_c = np.array([remap[int(e)] for e in ids], np.uint32)
             shared = [s.cpu().numpy() for s in lt.shared] if lt.shared else None
             t0 = time.perf_counter()
-            routed = orc.moe_routed(lt.quant, lt.quant, g, u, d, x, ids_c, w, len(experts), k,
-                                    cfg.intermediate)
+            routed = orc.moe_routed(lt.quant, lt.down_quant or lt.quant, g, u, d, x, ids_c, w,
+                                    len(experts), k, cfg.intermediate)
             if shared:
-                r = orc.shared_q8_0(*shared, x, cfg.shared_intermediate, routed=routed, residual=r)
+                r = orc.shared_ffn(lt.shared_quant, lt.shared_down_quant, *shared, x,
+                                   cfg.shared_intermediate, routed=routed, residual=r)
             else:
                 r = routed + r
             busy += time.perf_counter() - t0

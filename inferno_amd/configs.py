@@ -9,7 +9,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
-from ._lib import BF16, F32, Q2_K, Q3_K, Q4_K, Q8_0, SCORE_SIGMOID, SCORE_SOFTMAX
+from ._lib import BF16, F32, Q2_K, Q3_K, Q4_K, Q6_K, Q8_0, SCORE_SIGMOID, SCORE_SOFTMAX
 from . import ops
 
 
@@ -61,6 +61,12 @@ CONFIGS = {
                  (1, 32)),
     "c5": Config("c5_glm_q2k_prefill_t4096_zipf", 4, 6144, 256, 2048, 8, (Q2_K,), SCORE_SIGMOID,
                  True, 2.5, 0.1, 2048, torch.bfloat16, (4096,), zipf=1.1, zipf_empty=40),
+    # not a BASELINE workload: the Laguna XS layer formats (routed Q4_K gate/up
+    # with Q6_K down, a Q4_K/Q6_K shared expert of the routed width) at c1's
+    # shape, one token and 64 tokens
+    "xs": Config("xs_c1shape_q4k_q6kdown_q4k_shared", 5, 2048, 64, 768, 8, (Q4_K,),
+                 SCORE_SOFTMAX, True, 1.0, 0.0, 768, torch.float32, (1, 64), down_quant=Q6_K,
+                 shared_quant=Q4_K),
 }
 
 # sub-stream ids

@@ -846,7 +846,7 @@ int launch_decode_layer(hipStream_t s, const DecodeArgs& a0, int quant) {
       a.dpf_rows = down_tile_rows(a.H);
       a.dpf_row_bytes = a.I / kKBlock * mfma_decode::kQ2Bytes;
     } else if (use_runs_down) {
-      a.dpf_rows = runs_down_tile_rows(quant, a.I, a.k);
+      a.dpf_rows = runs_down_tile_rows(quant, a.H, a.I, a.k);
       a.dpf_row_bytes = runs_down_row_bytes(quant, a.I);
     }
   }

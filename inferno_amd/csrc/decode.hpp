@@ -81,7 +81,7 @@ bool runs_down_covers(int quant, int H, int I, int k);
 int launch_gate_up_runs(hipStream_t s, const DecodeArgs& a, int quant);
 int launch_down_runs(hipStream_t s, const DecodeArgs& a, int quant);
 // Rows per tile and bytes per row of the run down kernel for this layer.
-int runs_down_tile_rows(int quant, int I, int k);
+int runs_down_tile_rows(int quant, int H, int I, int k);
 int runs_down_row_bytes(int quant, int I);
 // The same kernels for T > 1 tokens (no shared expert): gate/up per expert
 // tile for all of the expert's tokens, down rows per assignment into a.y.

@@ -97,9 +97,19 @@ int down_tr(hipStream_t s, const DecodeArgs& a) {
   return down_per<Q, NB, TR, 8>(s, a);
 }
 
+// 16-row tiles when they fit and give every CU a tile (H / 16 >= CUs),
+// else 8-row tiles (H = 2048: 128 tiles of 16 rows would leave half of a
+// 256-CU part idle)
+template <int Q, int NB>
+int pick_tr(int k, int H) {
+  const bool fits16 = down_tr_fits<Q, NB, 16>(k), fits8 = down_tr_fits<Q, NB, 8>(k);
+  if (fits16 && (!fits8 || H / 16 >= cus_now())) return 16;
+  return 8;
+}
+
 template <int Q, int NB>
 int down_nb(hipStream_t s, const DecodeArgs& a) {
-  if (down_tr_fits<Q, NB, 16>(a.k + a.shared_slot)) return down_tr<Q, NB, 16>(s, a);
+  if (pick_tr<Q, NB>(a.k + a.shared_slot, a.H) == 16) return down_tr<Q, NB, 16>(s, a);
   return down_tr<Q, NB, 8>(s, a);
 }
 
@@ -169,15 +179,15 @@ int launch_gate_up_runs(hipStream_t s, const DecodeArgs& a, int quant) {
   }
 }
 
-int runs_down_tile_rows(int quant, int I, int k) {
+int runs_down_tile_rows(int quant, int H, int I, int k) {
   auto pick = [&](auto q_c) {
     constexpr int Q = decltype(q_c)::value;
     switch (I / kKBlock) {
-      case 2: return down_tr_fits<Q, 2, 16>(k) ? 16 : 8;
-      case 3: return down_tr_fits<Q, 3, 16>(k) ? 16 : 8;
-      case 4: return down_tr_fits<Q, 4, 16>(k) ? 16 : 8;
-      case 6: return down_tr_fits<Q, 6, 16>(k) ? 16 : 8;
-      default: return down_tr_fits<Q, 8, 16>(k) ? 16 : 8;
+      case 2: return pick_tr<Q, 2>(k, H);
+      case 3: return pick_tr<Q, 3>(k, H);
+      case 4: return pick_tr<Q, 4>(k, H);
+      case 6: return pick_tr<Q, 6>(k, H);
+      default: return pick_tr<Q, 8>(k, H);
     }
   };
   switch (quant) {
