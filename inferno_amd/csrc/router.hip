@@ -160,7 +160,11 @@ __global__ void __launch_bounds__(256)
   for (int b = 0; b < NTB; ++b)
 #pragma unroll
     for (int h = 0; h < 2; ++h) acc[b][h] = float4v{0.f, 0.f, 0.f, 0.f};
-  for (int k0 = 0; k0 < H; k0 += 32) {
+  // blockIdx.z: K chunk of H / gridDim.z (whole 32-deep blocks), partial
+  // logits to logits + z T E (summed in chunk order by the top-k kernel)
+  const int kc = H / int(gridDim.z), kbeg = int(blockIdx.z) * kc;
+  logits += size_t(blockIdx.z) * size_t(T) * E;
+  for (int k0 = kbeg; k0 < kbeg + kc; k0 += 32) {
     float a[8];
     load8<float>(wrow + k0, ev, a);
 #pragma unroll
@@ -355,7 +359,8 @@ static bool bf16x3_enabled() {
   return !switch_off("INFERNO_ROUTER_BF16X3");
 }
 
-// K chunks for the bf16 x router logits of a T-token batch: 1 when the
+// K chunks for the router logits of a T-token batch (bf16 tokens on the
+// bf16x3 kernel, fp32 tokens on the fp32 MFMA kernel): 1 when the
 // batch alone gives the kernel enough workgroups; else the most (a power of
 // two, up to kMaxRouterParts) that keeps at most kRouterSplitGroups
 // workgroups of the one-group kernel and a whole number of 32-deep block
@@ -370,7 +375,7 @@ int router_logit_parts_max(size_t T, size_t H, size_t E) {
   return z;
 }
 int router_logit_parts(size_t T, size_t H, size_t E, int x_dtype) {
-  if (x_dtype != INFERNO_BF16 || !bf16x3_enabled()) return 1;
+  if (x_dtype == INFERNO_BF16 && !bf16x3_enabled()) return 1;
   return router_logit_parts_max(T, H, E);
 }
 
@@ -379,8 +384,12 @@ int launch_router_logit_parts(hipStream_t s, const void* x, int x_dtype, const f
   if (parts <= 1) return launch_router_logits(s, x, x_dtype, w, T, H, E, parts_out);
   if (T == 0 || E == 0) return INFERNO_OK;
   const dim3 grid(unsigned((E + 63) / 64), unsigned((T + 15) / 16), unsigned(parts));
-  logits_bf16x3_kernel<1, 1><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x), w, int(T),
-                                                  int(H), int(E), parts_out);
+  if (x_dtype == INFERNO_BF16)
+    logits_bf16x3_kernel<1, 1><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x), w, int(T),
+                                                    int(H), int(E), parts_out);
+  else  // fp32 tokens on the fp32 matrix cores, K split the same way
+    logits_mfma_kernel<float, 1><<<grid, 256, 0, s>>>(static_cast<const float*>(x), w, int(T),
+                                                      int(H), int(E), parts_out);
   INF_LAUNCHED();
   return INFERNO_OK;
 }
