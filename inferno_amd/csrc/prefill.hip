@@ -508,6 +508,68 @@ struct Stage<INFERNO_Q3_K> {
     r[10] = row[27] & 0xffffu;
   }
 };
+// Q4_K: 144 bytes per row, fetched as nine 16-byte chunks (seven rows per
+// wavefront load instruction) and stored as dwords at an odd pitch of 37
+// words; Frag<Q4_K>'s words read back from LDS.
+template <>
+struct Stage<INFERNO_Q4_K> {
+  static constexpr int kWords = 9, kPitch = 37;
+  using Chunk = uint4;
+  __device__ static int offset(int j, int& shift) {
+    shift = 0;
+    return 16 * j;
+  }
+  __device__ static Chunk load(const uint8_t* b, int) { return ld_u4(b); }
+  __device__ static void put(uint32_t* row, int j, Chunk v) {
+    row[4 * j] = v.x; row[4 * j + 1] = v.y; row[4 * j + 2] = v.z; row[4 * j + 3] = v.w;
+  }
+  __device__ static void frag(const uint32_t* row, int qc, int kg, uint32_t r[8]) {
+    const uint32_t* a = row + 4 + 8 * qc + 2 * kg;  // qs bytes 16 + 32 qc + 8 kg
+    r[0] = a[0]; r[1] = a[1]; r[2] = a[4]; r[3] = a[5];
+    r[4] = row[1]; r[5] = row[2]; r[6] = row[3];  // scales
+    r[7] = row[0];                                // d | dmin
+  }
+};
+
+// Q6_K: 210 bytes per row, fetched as thirteen 16-byte chunks (bytes
+// 0..207) and a fourteenth holding only the dword at byte 206 shifted down
+// 16 (d), so no load passes the super-block; stored as 53 dwords per row
+// (an odd pitch); Frag<Q6_K>'s words read back from LDS.
+template <>
+struct Stage<INFERNO_Q6_K> {
+  static constexpr int kWords = 14, kPitch = 53;
+  using Chunk = uint4;
+  __device__ static int offset(int j, int& shift) {
+    shift = j == 13 ? 16 : 0;
+    return j == 13 ? 206 : 16 * j;
+  }
+  __device__ static Chunk load(const uint8_t* b, int shift) {
+    if (shift) return make_uint4(ld_u1(b) >> shift, 0u, 0u, 0u);
+    return ld_u4(b);
+  }
+  __device__ static void put(uint32_t* row, int j, Chunk v) {
+    if (j == 13) {
+      row[52] = v.x;
+      return;
+    }
+    row[4 * j] = v.x; row[4 * j + 1] = v.y; row[4 * j + 2] = v.z; row[4 * j + 3] = v.w;
+  }
+  __device__ static void frag(const uint32_t* row, int qc, int kg, uint32_t r[14]) {
+    const int h = qc >> 1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {  // ql bytes 64 h + 16 s + 8 kg
+      r[2 * s] = row[16 * h + 4 * s + 2 * kg];
+      r[2 * s + 1] = row[16 * h + 4 * s + 2 * kg + 1];
+    }
+    r[8] = row[32 + 8 * h + 2 * kg];  // qh bytes 128 + 32 h + 8 kg
+    r[9] = row[33 + 8 * h + 2 * kg];
+    r[10] = row[36 + 8 * h + 2 * kg];  // qh bytes 144 + 32 h + 8 kg
+    r[11] = row[37 + 8 * h + 2 * kg];
+    r[12] = row[48 + 2 * h + (qc & 1)];  // scales 8 h + 4 (qc & 1) ..
+    r[13] = row[52] & 0xffffu;           // d
+  }
+};
+
 // Q8_0: a K unit is 272 bytes (eight 34-byte blocks), fetched as 17
 // 16-byte chunks per row (three rows per wavefront load instruction) and
 // stored as dwords at an odd pitch of 69 words. The int8 codes of the even
@@ -907,9 +969,12 @@ int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
   constexpr bool kStaged =
       ((Q == INFERNO_Q2_K || Q == INFERNO_Q3_K) &&
        (TM <= 64 || (NMAT == 1 && Q == INFERNO_Q3_K) || (NMAT == 2 && Q == INFERNO_Q2_K))) ||
-      (Q == INFERNO_Q8_0 && (TM == 32 || TM == 128));
+      (Q == INFERNO_Q8_0 && (TM == 32 || TM == 128)) ||
+      (Q == INFERNO_Q4_K && TM == 32) || (Q == INFERNO_Q6_K && NMAT == 1 && TM == 32);
   if constexpr (kStaged) {
-    if (a.N % 128 == 0 && gemm2_enabled()) {
+    // INFERNO_PREFILL_Q4_STAGED=0: Q4_K and Q6_K on the fragment-load kernel
+    if (a.N % 128 == 0 && gemm2_enabled() &&
+        ((Q != INFERNO_Q4_K && Q != INFERNO_Q6_K) || !switch_off("INFERNO_PREFILL_Q4_STAGED"))) {
       const dim3 grid(unsigned(a.N / 128), grid_y);
       if constexpr (Q == INFERNO_Q8_0 && TM == 128) {
         // Q8_0 (272-byte K units): one weight buffer; gate/up with one
