@@ -608,9 +608,12 @@ struct Stage<INFERNO_Q8_0> {
   }
 };
 
-template <int Q, int NMAT, int TM, int WR, int SB = 0>
+constexpr int kUnitPitch = 264;  // halfs per LDS token row of a whole K unit (256 + 8 pad)
+
+template <int Q, int NMAT, int TM, int WR, int SB = 0, int XU = 0>
 constexpr size_t gemm2_lds_bytes() {
-  return size_t(2) * TM * kLdsPitch * 2 + size_t(SB ? 1 : 2) * 32 * WR * NMAT * Stage<Q>::kPitch * 4;
+  return size_t(2) * TM * (XU ? kUnitPitch : kLdsPitch) * 2 +
+         size_t(SB ? 1 : 2) * 32 * WR * NMAT * Stage<Q>::kPitch * 4;
 }
 
 // WR x WT wavefronts: wavefront (wr, wt) computes weight rows 32 wr .. + 32
@@ -625,14 +628,23 @@ constexpr size_t gemm2_lds_bytes() {
 // 0..WR-1 gate, WR..2WR-1 up), halving its fragment and accumulator
 // registers; after the K loop the up wavefronts pass their sums to the gate
 // wavefronts through the (then free) LDS for the SwiGLU.
-template <int Q, int NMAT, int TM, int PF, int WR, int WT, int OCC, int SB = 0, int SPL = 0>
+// XU = 1 (with SB = 1): the token tile of a whole K unit (TM x 256 f16) is
+// double buffered instead of each 64-deep step's, loaded into registers at
+// the unit's first step and stored with the next unit's weights at its end,
+// so a K unit takes two barriers instead of five and the wavefronts drift
+// apart within it (one's dequantisation beside another's MFMA).
+template <int Q, int NMAT, int TM, int PF, int WR, int WT, int OCC, int SB = 0, int SPL = 0,
+          int XU = 0>
 __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
     __attribute__((amdgpu_waves_per_eu(OCC, OCC))) gemm2_kernel(GemmArgs p) {
   using F = Frag<Q>;
   using S = Stage<Q>;
   static_assert(!SPL || (NMAT == 2 && WT == 1), "matrix split: gate/up, no token split");
-  static_assert(!SPL || size_t(WR) * (TM / 32) * 16 * 64 * 4 <= gemm2_lds_bytes<Q, NMAT, TM, WR, SB>(),
+  static_assert(!SPL || size_t(WR) * (TM / 32) * 16 * 64 * 4 <= gemm2_lds_bytes<Q, NMAT, TM, WR, SB, XU>(),
                 "the up sums passed through LDS fit in the workgroup's LDS");
+  static_assert(!XU || SB, "unit token buffers come with the single weight buffer");
+  constexpr int XPitch = XU ? kUnitPitch : kLdsPitch;
+  constexpr int XPR = XU ? 32 : 8;  // 16-byte token pieces per row of a buffer
   constexpr int WAVES = SPL ? 2 * WR : WR * WT;
   constexpr int NB = TM / 32;
   static_assert(NB % WT == 0, "token blocks split evenly over WT");
@@ -644,11 +656,11 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
   constexpr int RW = R / WAVES;         // rows staged by one wavefront
   constexpr int RPI = 64 / S::kWords;   // rows per load instruction
   constexpr int NI = (RW + RPI - 1) / RPI;
-  constexpr int XP = (TM * 8 + NT - 1) / NT;  // 16-byte token pieces per thread
+  constexpr int XP = (TM * XPR + NT - 1) / NT;  // 16-byte token pieces per thread
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   uint16_t* xs_base = smem;
-  uint32_t* ws_base = reinterpret_cast<uint32_t*>(smem + 2 * TM * kLdsPitch);
-  auto xs = [&](int buf, int row) { return xs_base + (size_t(buf) * TM + row) * kLdsPitch; };
+  uint32_t* ws_base = reinterpret_cast<uint32_t*>(smem + 2 * TM * XPitch);
+  auto xs = [&](int buf, int row) { return xs_base + (size_t(buf) * TM + row) * XPitch; };
   auto wsr = [&](int buf, int rr) { return ws_base + (size_t(SB ? 0 : buf) * R + rr) * S::kPitch; };
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -703,31 +715,40 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
     }
   };
 
-  // token staging: piece c = tid + NT q -> row c / 8, 8 halfs at 8 (c % 8)
+  // token staging: piece c = tid + NT q -> row c / XPR, 8 halfs at 8 (c % XPR)
   const uint16_t* src[XP];
 #pragma unroll
   for (int q = 0; q < XP; ++q) {
-    const int c = tid + NT * q, row = c >> 3;
+    const int c = tid + NT * q, row = c / XPR;
     const uint32_t cc = c0 + uint32_t(row);
     src[q] = nullptr;
     if (row < TM && cc < c1) {
       const uint32_t a = p.sorted ? p.sorted[cc] : cc;
-      src[q] = p.xin + size_t(a / p.in_div) * K + 8 * (c & 7);
+      src[q] = p.xin + size_t(a / p.in_div) * K + 8 * (c % XPR);
     }
   }
-  // token pieces of step t sit in register slot t % PF until stored
-  uint4 xv[PF][XP];
-  auto load_x = [&](int st, int slot) {
+  // token pieces of step t (XU: of unit t) sit in register slot t % PF
+  // until stored. XU: a unit's pieces go in XH parts (part h: loaded at the
+  // unit's step 2 h, stored at step 2 h + 1), XP / XH registers
+  constexpr int XS = XU ? 1 : PF;
+  constexpr int XH = (XU && XP % 2 == 0 && XP > 2) ? 2 : 1;
+  constexpr int XPP = XP / XH;
+  uint4 xv[XS][XPP];
+  auto load_x = [&](int st, int slot, int part = 0) {
 #pragma unroll
-    for (int q = 0; q < XP; ++q)
-      xv[slot][q] = src[q] ? *reinterpret_cast<const uint4*>(src[q] + 64 * st) : make_uint4(0, 0, 0, 0);
+    for (int u = 0; u < XPP; ++u) {
+      const int q = part * XPP + u;
+      xv[slot][u] = src[q] ? *reinterpret_cast<const uint4*>(src[q] + 64 * XPR / 8 * st)
+                           : make_uint4(0, 0, 0, 0);
+    }
   };
-  auto store_x = [&](int buf, int slot) {
+  auto store_x = [&](int buf, int slot, int part = 0) {
 #pragma unroll
-    for (int q = 0; q < XP; ++q) {
+    for (int u = 0; u < XPP; ++u) {
+      const int q = part * XPP + u;
       const int c = tid + NT * q;
-      if (XP * NT == TM * 8 || c < TM * 8)
-        *reinterpret_cast<uint4*>(xs(buf, c >> 3) + 8 * (c & 7)) = xv[slot][q];
+      if (XP * NT == TM * XPR || c < TM * XPR)
+        *reinterpret_cast<uint4*>(xs(buf, c / XPR) + 8 * (c % XPR)) = xv[slot][u];
     }
   };
 
@@ -747,18 +768,26 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
     gload_w(0, part, 0);
     store_w(0, part, 0);
   }
-  load_x(0, 0);
-  store_x(0, 0);
-  if (PF == 2 && 1 < nch) load_x(1, 1 % PF);
+#pragma unroll
+  for (int h = 0; h < XH; ++h) {
+    load_x(0, 0, h);
+    store_x(0, 0, h);
+  }
+  if (!XU && PF == 2 && 1 < nch) load_x(1, 1 % PF);
   __syncthreads();
 
   auto step = [&](auto qc_c, int kb) __attribute__((always_inline)) {
     constexpr int QC = decltype(qc_c)::value;
-    constexpr int buf = QC & 1;
+    const int buf = XU ? (kb & 1) : (QC & 1);
     const int st = 4 * kb + QC;
     const bool more = st + 1 < nch;
-    // x of step st + PF into slot (st + PF) % PF; weights of unit kb + 1
-    if (st + PF < nch) load_x(st + PF, QC % PF);
+    // x of step st + PF into slot (st + PF) % PF (XU: of unit kb + 1 at the
+    // unit's first step); weights of unit kb + 1
+    if constexpr (XU) {
+      if (QC % 2 == 0 && QC / 2 < XH && kb + 1 < nkb) load_x(kb + 1, 0, QC / 2);
+    } else if (st + PF < nch) {
+      load_x(st + PF, QC % PF);
+    }
     if (kb + 1 < nkb) {
       if constexpr (SB) gload_w(kb + 1, QC, QC);
       else if constexpr (PF == 1) gload_w(kb + 1, QC, 0);
@@ -778,12 +807,25 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
       if constexpr (NMAT == 2 && !SPL) a1 = F::template get<QC>(rb, s);
 #pragma unroll
       for (int tb = 0; tb < NBW; ++tb) {
-        const half8 b =
-            *reinterpret_cast<const half8*>(xs(buf, (wt * NBW + tb) * 32 + i) + 16 * s + 8 * kg);
+        const half8 b = *reinterpret_cast<const half8*>(xs(buf, (wt * NBW + tb) * 32 + i) +
+                                                        (XU ? 64 * QC : 0) + 16 * s + 8 * kg);
         acc0[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc0[tb], 0, 0, 0);
         if constexpr (NMAT == 2 && !SPL)
           acc1[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc1[tb], 0, 0, 0);
       }
+    }
+    if constexpr (XU) {
+      // the next unit's tokens into the other buffer (free since the last
+      // unit's end); one barrier pair per unit: every wavefront is done with
+      // this unit's weights
+      if (QC % 2 == 1 && QC / 2 < XH && kb + 1 < nkb) store_x(buf ^ 1, 0, QC / 2);
+      if (QC == 3 && kb + 1 < nkb) {
+        __syncthreads();
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) store_w(0, qq, qq);
+        __syncthreads();
+      }
+      return;
     }
     if (more) store_x(buf ^ 1, (QC + 1) % PF);
     if constexpr (SB) {
@@ -959,6 +1001,10 @@ bool gemm2_enabled() {
   return !switch_off("INFERNO_PREFILL_GEMM2");
 }
 
+// Token tiles of whole K units in the 32-token staged GEMMs
+// (INFERNO_PREFILL_XU=0: per 64-deep step).
+bool unit_tokens() { return !switch_off("INFERNO_PREFILL_XU"); }
+
 template <int Q, int NMAT, int TM>
 int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
   if (grid_y == 0) return INFERNO_OK;
@@ -988,13 +1034,21 @@ int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
       } else if constexpr (NMAT == 1 && TM == 32) {
         // down over few tokens: one weight buffer, four waves per SIMD (at
         // 64 tokens the 128-register budget spills)
+        // (token tiles per K unit as in the gate/up below measured slower
+        // here: c3 down 0.69 against 0.60 ms)
         gemm2_kernel<Q, 1, TM, 2, 4, 1, 4, 1>
             <<<grid, 256, gemm2_lds_bytes<Q, 1, TM, 4, 1>(), s>>>(a);
       } else if constexpr (NMAT == 2 && TM == 32) {
         // gate/up over few tokens: one matrix per wavefront (eight), one
-        // weight buffer, four waves per SIMD
-        gemm2_kernel<Q, 2, TM, 1, 4, 1, 4, 1, 1>
-            <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 1>(), s>>>(a);
+        // weight buffer, four waves per SIMD; token tiles per K unit
+        // (INFERNO_PREFILL_XU=0: per 64-deep step; Q8_0 keeps them per step,
+        // its unit tiles would spill)
+        if (Q != INFERNO_Q8_0 && unit_tokens())
+          gemm2_kernel<Q, 2, TM, 1, 4, 1, 4, 1, 1, Q != INFERNO_Q8_0>
+              <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 1, Q != INFERNO_Q8_0>(), s>>>(a);
+        else
+          gemm2_kernel<Q, 2, TM, 1, 4, 1, 4, 1, 1>
+              <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 1>(), s>>>(a);
       } else if constexpr (NMAT == 2 && TM == 128) {
         // Q2_K gate/up over 128 tokens: one matrix per wavefront (64
         // accumulators each), compiled for three waves per SIMD (lab, dense
