@@ -608,11 +608,12 @@ struct Stage<INFERNO_Q8_0> {
   }
 };
 
-constexpr int kUnitPitch = 264;  // halfs per LDS token row of a whole K unit (256 + 8 pad)
+// Halfs per LDS token row of a buffer of XG 64-deep steps (+ 8 pad).
+constexpr int x_pitch(int XG) { return 64 * (XG > 1 ? XG : 1) + 8; }
 
 template <int Q, int NMAT, int TM, int WR, int SB = 0, int XU = 0>
 constexpr size_t gemm2_lds_bytes() {
-  return size_t(2) * TM * (XU ? kUnitPitch : kLdsPitch) * 2 +
+  return size_t(2) * TM * x_pitch(XU) * 2 +
          size_t(SB ? 1 : 2) * 32 * WR * NMAT * Stage<Q>::kPitch * 4;
 }
 
@@ -628,11 +629,12 @@ constexpr size_t gemm2_lds_bytes() {
 // 0..WR-1 gate, WR..2WR-1 up), halving its fragment and accumulator
 // registers; after the K loop the up wavefronts pass their sums to the gate
 // wavefronts through the (then free) LDS for the SwiGLU.
-// XU = 1 (with SB = 1): the token tile of a whole K unit (TM x 256 f16) is
-// double buffered instead of each 64-deep step's, loaded into registers at
-// the unit's first step and stored with the next unit's weights at its end,
-// so a K unit takes two barriers instead of five and the wavefronts drift
-// apart within it (one's dequantisation beside another's MFMA).
+// XU = XG in {2, 4}: the token tile of XG 64-deep steps (TM x 64 XG f16) is
+// double buffered instead of each step's, loaded into registers at the
+// group's first step and stored into the other buffer at its last, so a K
+// unit takes 4 / XG barriers (XG = 4 with SB = 1: two, around the next
+// unit's weight stores) instead of four or five, and the wavefronts drift
+// apart between them (one's dequantisation beside another's MFMA).
 template <int Q, int NMAT, int TM, int PF, int WR, int WT, int OCC, int SB = 0, int SPL = 0,
           int XU = 0>
 __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
@@ -642,9 +644,11 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
   static_assert(!SPL || (NMAT == 2 && WT == 1), "matrix split: gate/up, no token split");
   static_assert(!SPL || size_t(WR) * (TM / 32) * 16 * 64 * 4 <= gemm2_lds_bytes<Q, NMAT, TM, WR, SB, XU>(),
                 "the up sums passed through LDS fit in the workgroup's LDS");
-  static_assert(!XU || SB, "unit token buffers come with the single weight buffer");
-  constexpr int XPitch = XU ? kUnitPitch : kLdsPitch;
-  constexpr int XPR = XU ? 32 : 8;  // 16-byte token pieces per row of a buffer
+  static_assert(XU == 0 || XU == 2 || XU == 4, "token buffers of 1, 2 or 4 steps");
+  static_assert(!(SB && XU == 2), "the single weight buffer takes whole-unit token buffers");
+  constexpr int XG = XU ? XU : 1;   // 64-deep steps per token buffer
+  constexpr int XPitch = x_pitch(XU);
+  constexpr int XPR = 8 * XG;  // 16-byte token pieces per row of a buffer
   constexpr int WAVES = SPL ? 2 * WR : WR * WT;
   constexpr int NB = TM / 32;
   static_assert(NB % WT == 0, "token blocks split evenly over WT");
@@ -727,28 +731,22 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
       src[q] = p.xin + size_t(a / p.in_div) * K + 8 * (c % XPR);
     }
   }
-  // token pieces of step t (XU: of unit t) sit in register slot t % PF
-  // until stored. XU: a unit's pieces go in XH parts (part h: loaded at the
-  // unit's step 2 h, stored at step 2 h + 1), XP / XH registers
+  // token pieces of step t (XU: of step group t) sit in register slot
+  // t % PF (XU: slot 0) until stored
   constexpr int XS = XU ? 1 : PF;
-  constexpr int XH = (XU && XP % 2 == 0 && XP > 2) ? 2 : 1;
-  constexpr int XPP = XP / XH;
-  uint4 xv[XS][XPP];
-  auto load_x = [&](int st, int slot, int part = 0) {
+  uint4 xv[XS][XP];
+  auto load_x = [&](int st, int slot) {
 #pragma unroll
-    for (int u = 0; u < XPP; ++u) {
-      const int q = part * XPP + u;
-      xv[slot][u] = src[q] ? *reinterpret_cast<const uint4*>(src[q] + 64 * XPR / 8 * st)
+    for (int q = 0; q < XP; ++q)
+      xv[slot][q] = src[q] ? *reinterpret_cast<const uint4*>(src[q] + 64 * XG * st)
                            : make_uint4(0, 0, 0, 0);
-    }
   };
-  auto store_x = [&](int buf, int slot, int part = 0) {
+  auto store_x = [&](int buf, int slot) {
 #pragma unroll
-    for (int u = 0; u < XPP; ++u) {
-      const int q = part * XPP + u;
+    for (int q = 0; q < XP; ++q) {
       const int c = tid + NT * q;
       if (XP * NT == TM * XPR || c < TM * XPR)
-        *reinterpret_cast<uint4*>(xs(buf, c / XPR) + 8 * (c % XPR)) = xv[slot][u];
+        *reinterpret_cast<uint4*>(xs(buf, c / XPR) + 8 * (c % XPR)) = xv[slot][q];
     }
   };
 
@@ -768,23 +766,21 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
     gload_w(0, part, 0);
     store_w(0, part, 0);
   }
-#pragma unroll
-  for (int h = 0; h < XH; ++h) {
-    load_x(0, 0, h);
-    store_x(0, 0, h);
-  }
+  load_x(0, 0);
+  store_x(0, 0);
   if (!XU && PF == 2 && 1 < nch) load_x(1, 1 % PF);
   __syncthreads();
 
   auto step = [&](auto qc_c, int kb) __attribute__((always_inline)) {
     constexpr int QC = decltype(qc_c)::value;
-    const int buf = XU ? (kb & 1) : (QC & 1);
     const int st = 4 * kb + QC;
+    const int grp = st / XG;  // token group (XU) of this step
+    const int buf = grp & 1;
     const bool more = st + 1 < nch;
-    // x of step st + PF into slot (st + PF) % PF (XU: of unit kb + 1 at the
-    // unit's first step); weights of unit kb + 1
+    // x of step st + PF into slot (st + PF) % PF (XU: of the next step group
+    // at this group's first step); weights of unit kb + 1
     if constexpr (XU) {
-      if (QC % 2 == 0 && QC / 2 < XH && kb + 1 < nkb) load_x(kb + 1, 0, QC / 2);
+      if (QC % XG == 0 && (grp + 1) * XG < nch) load_x(grp + 1, 0);
     } else if (st + PF < nch) {
       load_x(st + PF, QC % PF);
     }
@@ -808,22 +804,33 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
 #pragma unroll
       for (int tb = 0; tb < NBW; ++tb) {
         const half8 b = *reinterpret_cast<const half8*>(xs(buf, (wt * NBW + tb) * 32 + i) +
-                                                        (XU ? 64 * QC : 0) + 16 * s + 8 * kg);
+                                                        64 * (QC % XG) + 16 * s + 8 * kg);
         acc0[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc0[tb], 0, 0, 0);
         if constexpr (NMAT == 2 && !SPL)
           acc1[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc1[tb], 0, 0, 0);
       }
     }
     if constexpr (XU) {
-      // the next unit's tokens into the other buffer (free since the last
-      // unit's end); one barrier pair per unit: every wavefront is done with
-      // this unit's weights
-      if (QC % 2 == 1 && QC / 2 < XH && kb + 1 < nkb) store_x(buf ^ 1, 0, QC / 2);
-      if (QC == 3 && kb + 1 < nkb) {
-        __syncthreads();
+      // the next group's tokens into the other buffer (free since the last
+      // group's end barrier); SB: one barrier pair per unit around the next
+      // unit's weights (every wavefront done with this unit's); else the
+      // next unit's weights go, a quarter per step, into the other weight
+      // buffer (read by no one during this unit) and a barrier ends each
+      // token group
+      if (QC % XG == XG - 1 && (grp + 1) * XG < nch) store_x(buf ^ 1, 0);
+      if constexpr (SB) {
+        if (QC == 3 && kb + 1 < nkb) {
+          __syncthreads();
 #pragma unroll
-        for (int qq = 0; qq < 4; ++qq) store_w(0, qq, qq);
-        __syncthreads();
+          for (int qq = 0; qq < 4; ++qq) store_w(0, qq, qq);
+          __syncthreads();
+        }
+      } else {
+        if (kb + 1 < nkb) {
+          if constexpr (PF == 1) store_w((kb + 1) & 1, QC, 0);
+          else if constexpr (QC >= 2) store_w((kb + 1) & 1, QC - 2, QC - 2);
+        }
+        if (QC % XG == XG - 1) __syncthreads();
       }
       return;
     }
@@ -1044,8 +1051,8 @@ int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
         // (INFERNO_PREFILL_XU=0: per 64-deep step; Q8_0 keeps them per step,
         // its unit tiles would spill)
         if (Q != INFERNO_Q8_0 && unit_tokens())
-          gemm2_kernel<Q, 2, TM, 1, 4, 1, 4, 1, 1, Q != INFERNO_Q8_0>
-              <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 1, Q != INFERNO_Q8_0>(), s>>>(a);
+          gemm2_kernel<Q, 2, TM, 1, 4, 1, 4, 1, 1, Q != INFERNO_Q8_0 ? 4 : 0>
+              <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 1, Q != INFERNO_Q8_0 ? 4 : 0>(), s>>>(a);
         else
           gemm2_kernel<Q, 2, TM, 1, 4, 1, 4, 1, 1>
               <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 1>(), s>>>(a);
@@ -1054,8 +1061,15 @@ int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
         // accumulators each), compiled for three waves per SIMD (lab, dense
         // tiles: 1.81 vs 2.13 ms for the fragment-load kernel; c5 layer:
         // 5.21 vs 5.29 ms)
-        gemm2_kernel<Q, 2, TM, 1, 4, 1, 3, 0, 1>
-            <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 0>(), s>>>(a);
+        // INFERNO_PREFILL_XU2=1: token tiles of two steps, one barrier per
+        // two steps, compiled for two waves per SIMD (one 8-wave workgroup
+        // per CU either way)
+        if (switch_on("INFERNO_PREFILL_XU2"))
+          gemm2_kernel<Q, 2, TM, 1, 4, 1, 2, 0, 1, 2>
+              <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 0, 2>(), s>>>(a);
+        else
+          gemm2_kernel<Q, 2, TM, 1, 4, 1, 3, 0, 1>
+              <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 0>(), s>>>(a);
       } else {
         constexpr int PF = Q == INFERNO_Q3_K ? 2 : 1;
         gemm2_kernel<Q, NMAT, TM, PF, 4, 1, 2><<<grid, 256, gemm2_lds_bytes<Q, NMAT, TM, 4>(), s>>>(a);
