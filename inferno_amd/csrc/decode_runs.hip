@@ -1,5 +1,7 @@
 // Launchers of the f16-run matrix-core decode kernels (decode_runs.hpp):
 // instances per format, super-block columns and register batch.
+#include <cstdlib>
+
 #include "decode.hpp"
 #include "decode_runs.hpp"
 
@@ -243,10 +245,32 @@ constexpr int kDownNT = 8;
 template <int Q, int NB, bool SPLIT, bool SEL>
 int gate_up_multi_nb(hipStream_t s, const DecodeArgs& a) {
   constexpr int NT = SEL ? 1 : multi_nt<Q, NB, SPLIT>();
+  // upper bound: active slots <= max_slots (plus the shared slot)
+  const int ntiles = (a.max_slots + a.shared_slot) * (a.I / kRows);
+  if constexpr (SEL) {
+    // one token: workgroups of WV wavefronts, several per CU (all of a
+    // layer's tiles in flight at once); INFERNO_DECODE_SEL_WAVES = 16, 8
+    // (default) or 4
+    const char* wv = std::getenv("INFERNO_DECODE_SEL_WAVES");
+    const int waves = wv ? std::atoi(wv) : 8;
+    auto launch_wv = [&](auto wv_c) -> int {
+      constexpr int WV = decltype(wv_c)::value;
+      static bool attr_wv = false;
+      auto* kw = gate_up_runs_multi_kernel<Q, NB, SPLIT, NT, SEL, WV>;
+      if (int st = allow_lds(kw, attr_wv)) return st;
+      constexpr size_t lds = gate_up_multi_lds<Q, NB, SPLIT, NT, SEL, WV>();
+      const int per_cu = std::min(int(16 / WV), int(kLdsMax / lds));
+      const unsigned grid = unsigned(std::min(ntiles, per_cu * cus_now()));
+      kw<<<grid, 64 * WV, lds, s>>>(a);
+      INF_LAUNCHED();
+      return INFERNO_OK;
+    };
+    if (waves == 8) return launch_wv(std::integral_constant<int, 8>{});
+    if (waves == 4) return launch_wv(std::integral_constant<int, 4>{});
+  }
   static bool attr = false;
   auto* kern = gate_up_runs_multi_kernel<Q, NB, SPLIT, NT, SEL>;
   if (int st = allow_lds(kern, attr)) return st;
-  const int ntiles = a.max_slots * (a.I / kRows);  // upper bound: active slots <= max_slots
   const unsigned grid = unsigned(std::min(ntiles, cus_now()));
   kern<<<grid, kThreads, gate_up_multi_lds<Q, NB, SPLIT, NT, SEL>(), s>>>(a);
   INF_LAUNCHED();

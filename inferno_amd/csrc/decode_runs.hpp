@@ -582,6 +582,13 @@ __global__ void __launch_bounds__(kThreads) down_runs_kernel(DecodeArgs p, int n
     }
     __syncthreads();
     if (t + int(gridDim.x) < ntiles) fetch(t + gridDim.x);
+    // the output rows' residual and shared down, fetched now so that the
+    // epilogue below does not wait for them
+    float base = 0.f;
+    if (tid < TR) {
+      const size_t o = size_t(t) * TR + tid;
+      base = (p.residual ? p.residual[o] : 0.f) + (p.ys ? p.ys[o] : 0.f);
+    }
     float acc = 0.f;
     for (int b = wave; b < nblk; b += kWaves) {
       const int r = b / NB, c = b - r * NB;
@@ -603,9 +610,7 @@ __global__ void __launch_bounds__(kThreads) down_runs_kernel(DecodeArgs p, int n
       float y = 0.f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) y += part[w * 16 + tid];
-      const size_t o = size_t(t) * TR + tid;
-      const float base = (p.residual ? p.residual[o] : 0.f) + (p.ys ? p.ys[o] : 0.f);
-      p.out[o] = base + y;
+      p.out[size_t(t) * TR + tid] = base + y;
     }
   }
 }
@@ -630,20 +635,20 @@ __device__ __forceinline__ uint32_t slot_assignment(const DecodeArgs& p, const u
 
 // Copies the staged rows (words each) of nt entries into LDS rows of the
 // same width; `src(i)` gives entry i's row.
-template <typename Src>
+template <int WV = kWaves, typename Src>
 __device__ __forceinline__ void load_rows(uint32_t* dst, int words, int nt, Src src) {
   const int w4 = words / 4;
-  for (int i = threadIdx.x; i < nt * w4; i += kThreads) {
+  for (int i = threadIdx.x; i < nt * w4; i += (64 * WV)) {
     const int e = i / w4, o = i - e * w4;
     reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src(e))[o];
   }
 }
 
 // Register prefetch of the first NT entries' staged rows (W4 16-byte words
-// each) of a slot: entry e = i / W4 of flat index i = x kThreads + tid.
-template <int NT, int W4>
+// each) of a slot: entry e = i / W4 of flat index i = x (64 * WV) + tid.
+template <int NT, int W4, int WV = kWaves>
 struct RowPrefetch {
-  static constexpr int XP = (NT * W4 + kThreads - 1) / kThreads;
+  static constexpr int XP = (NT * W4 + (64 * WV) - 1) / (64 * WV);
   u32x4 v[XP];
   uint32_t a[XP];  // the entry's assignment (kept where i % W4 == 0)
   // `row(a)` is assignment a's staged row
@@ -651,7 +656,7 @@ struct RowPrefetch {
   __device__ __forceinline__ void load(const DecodeArgs& p, const uint4& sl, int nt, Row row) {
 #pragma unroll
     for (int x = 0; x < XP; ++x) {
-      const int i = x * kThreads + int(threadIdx.x);
+      const int i = x * (64 * WV) + int(threadIdx.x);
       if (i < nt * W4) {
         const int e = i / W4;
         a[x] = slot_assignment(p, sl, sl.y + uint32_t(e));
@@ -662,7 +667,7 @@ struct RowPrefetch {
   __device__ __forceinline__ void store(uint32_t* dst, uint32_t* tok_a, int nt) const {
 #pragma unroll
     for (int x = 0; x < XP; ++x) {
-      const int i = x * kThreads + int(threadIdx.x);
+      const int i = x * (64 * WV) + int(threadIdx.x);
       if (i < nt * W4) {
         reinterpret_cast<u32x4*>(dst)[i] = v[x];
         if (i % W4 == 0) tok_a[i / W4] = a[x];
@@ -671,24 +676,24 @@ struct RowPrefetch {
   }
 };
 
-template <int Q, int NB, bool SPLIT, int NT>
+template <int Q, int NB, bool SPLIT, int NT, int WV = kWaves>
 struct MultiGateUpShape {
   static constexpr int H = NB * kKBlock;
   static constexpr int rb = NB * RF<Q>::kBytes;
   static constexpr int Sx = xrun_words(H, SPLIT);
   static constexpr int chunks = 2 * 16 * rb / 16;
-  static constexpr int PER = (chunks + kThreads - 1) / kThreads;
+  static constexpr int PER = (chunks + (64 * WV) - 1) / (64 * WV);
 };
 
 // LDS of the selecting variant's additions: topk1_wave's scratch and the
 // slot table (expert, assignment, routing weight per slot)
 constexpr size_t kSelMultiLds = 8 + sizeof(Top1Lds) + size_t(3 * (kMaxTopK + 1)) * 4;
 
-template <int Q, int NB, bool SPLIT, int NT, bool SEL = false>
+template <int Q, int NB, bool SPLIT, int NT, bool SEL = false, int WV = kWaves>
 __host__ __device__ constexpr size_t gate_up_multi_lds() {
-  using S = MultiGateUpShape<Q, NB, SPLIT, NT>;
+  using S = MultiGateUpShape<Q, NB, SPLIT, NT, WV>;
   return size_t(NT) * S::Sx * 4 + 16 + size_t(2 * 16) * row_pitch(S::rb) +
-         size_t(kWaves * NT * 16) * 4 + size_t(2 * NT) * 4 + (SEL ? kSelMultiLds : 0);
+         size_t(WV * NT * 16) * 4 + size_t(2 * NT) * 4 + (SEL ? kSelMultiLds : 0);
 }
 
 // SEL (one token, no shared expert in this launch's epilogue): the kernel
@@ -697,9 +702,9 @@ __host__ __device__ constexpr size_t gate_up_multi_lds() {
 // LDS slot table (slot j = the j-th smallest selected id, its one
 // assignment = its rank, its routing weight), and workgroup 0 writes the
 // ids, weights and dispatch for the down launch: no select launch.
-template <int Q, int NB, bool SPLIT, int NT, bool SEL = false>
-__global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs p) {
-  using S = MultiGateUpShape<Q, NB, SPLIT, NT>;
+template <int Q, int NB, bool SPLIT, int NT, bool SEL = false, int WV = kWaves>
+__global__ void __launch_bounds__(64 * WV) gate_up_runs_multi_kernel(DecodeArgs p) {
+  using S = MultiGateUpShape<Q, NB, SPLIT, NT, WV>;
   constexpr int NA = SPLIT ? 2 : 1;
   extern __shared__ uint32_t smem[];
   constexpr int rb = S::rb, PER = S::PER, Sx = S::Sx, H = S::H, RS = row_pitch(rb);
@@ -708,7 +713,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
   uint32_t* zero = xs + NT * Sx;
   uint8_t* tl = reinterpret_cast<uint8_t*>(zero + 4);               // [2][16 rows at pitch RS]
   float* part = reinterpret_cast<float*>(tl + 2 * 16 * RS);         // [wave][NT][16]
-  uint32_t* tok_ab = reinterpret_cast<uint32_t*>(part + kWaves * NT * 16);  // [2][NT]
+  uint32_t* tok_ab = reinterpret_cast<uint32_t*>(part + WV * NT * 16);  // [2][NT]
   // SEL: topk1_wave's scratch (8-byte aligned: every region above is a
   // whole number of 8-byte words) and the slot table
   Top1Lds* tk = reinterpret_cast<Top1Lds*>(tok_ab + 2 * NT);
@@ -722,7 +727,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
   const int tiles_i = I / kRows;
   int ntiles;
   if constexpr (SEL) {
-    if (wave == kWaves - 1) {
+    if (wave == WV - 1) {
       __builtin_amdgcn_s_setprio(3);
       float lg[4], bs[4];
       load_logits1(p, lg, bs);
@@ -759,7 +764,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
   int t = blockIdx.x;
   if (t >= ntiles) return;  // uniform per workgroup
   u32x4 v[PER];
-  RowPrefetch<NT, Sx / 4> xr;
+  RowPrefetch<NT, Sx / 4, WV> xr;
   // token of assignment a (the shared expert's assignments T k + t follow
   // the routed ones)
   const uint32_t Tk = uint32_t(p.T) * uint32_t(k);
@@ -776,7 +781,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
         reinterpret_cast<const u32x4*>((sh ? p.sup : p.up + size_t(s2.x) * p.gate_stride) + off);
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      int i = j * kThreads + tid;
+      int i = j * (64 * WV) + tid;
       i = i < S::chunks ? i : S::chunks - 1;  // clamped; the extra chunks are not stored
       v[j] = i < S::chunks / 2 ? g4[i] : u4[i - S::chunks / 2];
     }
@@ -793,7 +798,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
     uint32_t* tok_a = tok_ab + (it & 1) * NT;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      const int i = j * kThreads + tid;
+      const int i = j * (64 * WV) + tid;
       if (i < S::chunks) store_tile_chunk(tl, rb, i, v[j]);
     }
     xr.store(xs, tok_a, min(NT, int(sl.z - sl.y)));
@@ -805,7 +810,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
         __syncthreads();      // the previous chunk's readers of tok_a / part / xs are done
         if (tid < nt) tok_a[tid] = slot_assignment(p, sl, uint32_t(c0 + tid));
         __syncthreads();
-        load_rows(xs, Sx, nt, [&](int e) { return row_of(tok_a[e]); });
+        load_rows<WV>(xs, Sx, nt, [&](int e) { return row_of(tok_a[e]); });
         __syncthreads();
       }
       // one token at a time (the tile's blocks are read from LDS again per
@@ -814,7 +819,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
         const uint32_t* row = xs + ti * Sx;
         const float* sums = reinterpret_cast<const float*>(row + H / 2);
         float acc = 0.f;
-        for (int c = wave >> 1; c < NB; c += kWaves / 2) {
+        for (int c = wave >> 1; c < NB; c += WV / 2) {
           const uint8_t* blk = tl + (mat * 16 + n) * RS + c * RF<Q>::kBytes;
           const float4 xsum = *reinterpret_cast<const float4*>(sums + c * 16 + 4 * q);
           const float4 kk = *reinterpret_cast<const float4*>(sums + H / 16 + c * 16 + 4 * q);
@@ -843,7 +848,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_multi_kernel(DecodeArgs
         const int ti = tid >> 4, row = tid & 15;
         float g = 0.f, u = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; w += 2) {
+        for (int w = 0; w < WV; w += 2) {
           g += part[(w * NT + ti) * 16 + row];
           u += part[((w + 1) * NT + ti) * 16 + row];
         }
