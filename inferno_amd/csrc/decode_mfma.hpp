@@ -654,13 +654,6 @@ __global__ void __launch_bounds__(kThreads) down_q2k_kernel(DecodeArgs p, int nt
     }
     __syncthreads();
     if (t + int(gridDim.x) < ntiles) fetch_down_tile<NB, TR, PER>(v, p, k, rank_e, t + gridDim.x);
-    // the output rows' residual and shared down, fetched now so that the
-    // epilogue below does not wait for them
-    float base = 0.f;
-    if (tid < TR) {
-      const size_t o = size_t(t) * TR + tid;
-      base = (p.residual ? p.residual[o] : 0.f) + (p.ys ? p.ys[o] : 0.f);
-    }
     float acc = 0.f;
     for (int b = wave; b < nblk; b += kWaves) {
       const int r = b / NB, c = b - r * NB;
@@ -719,7 +712,9 @@ __global__ void __launch_bounds__(kThreads) down_q2k_kernel(DecodeArgs p, int nt
       float y = 0.f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) y += part[w * 16 + tid];
-      p.out[size_t(t) * TR + tid] = base + y;
+      const size_t o = size_t(t) * TR + tid;
+      const float base = (p.residual ? p.residual[o] : 0.f) + (p.ys ? p.ys[o] : 0.f);
+      p.out[o] = base + y;
     }
   }
 }
