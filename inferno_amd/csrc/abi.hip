@@ -114,7 +114,8 @@ int validate_moe(int quant, int down_quant, size_t gate_bytes, size_t up_bytes,
 // down. Leaves per-assignment down rows (already routing-weighted) in m.y.
 // Many assignments take the MFMA grouped GEMM; few take the packed-f16 GEMV.
 bool use_mfma(int quant, int down_quant, size_t T, size_t k, size_t E, size_t H, size_t I) {
-  return T * k >= kPrefillMinAssignments && prefill_routed_supported(quant, down_quant, H, I, E);
+  return T * k >= env_size("INFERNO_PREFILL_MIN_ASSIGNMENTS", kPrefillMinAssignments) &&
+         prefill_routed_supported(quant, down_quant, H, I, E);
 }
 
 // `x16`: x already converted to f16 (MFMA path), or null.
@@ -608,9 +609,10 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
   hipStream_t s = as_stream(stream);
   uint32_t* ids = expert_ids_out ? expert_ids_out : w.ids;
   float* wts = expert_weights_out ? expert_weights_out : w.weights;
-  // the fused decode path below 256 assignments (and for one token); from
-  // there the grouped MFMA GEMM reads each expert's weights once for all its
-  // tokens (c4 at T = 32, 2.5 tokens per expert: 2.5 ms against 3.9 ms)
+  // the fused decode path below kPrefillMinAssignments assignments (and for
+  // one token); from there the grouped MFMA GEMM reads each expert's weights
+  // once for all its tokens (c2 at T = 16: 0.55 ms against 0.62 ms; c4 at
+  // T = 32: 2.0 ms against 3.9 ms)
   const bool decode = layer_takes_decode(L, T, x_dtype);
   if (logits_ready && !decode) {
     set_error("precomputed logits need the decode path");

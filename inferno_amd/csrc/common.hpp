@@ -29,6 +29,14 @@ inline bool switch_on(const char* name) {
   return v && v[0] == '1';
 }
 
+// The environment variable `name` as a non-negative integer, or `dflt` when
+// it is unset or not a number (a tuning threshold; read on every call).
+inline size_t env_size(const char* name, size_t dflt) {
+  const char* v = std::getenv(name);
+  if (!v || *v < '0' || *v > '9') return dflt;
+  return size_t(std::strtoull(v, nullptr, 10));
+}
+
 constexpr int kWave = 64;        // CDNA wavefront width
 constexpr int kKBlock = 256;     // K-quant super-block values
 constexpr int kQ8Block = 32;     // Q8_0 block values

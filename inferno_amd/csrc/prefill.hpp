@@ -8,8 +8,10 @@ namespace inferno {
 bool prefill_supported(int quant);
 // True when the routed layer (gate/up kind, down kind, shapes) has the MFMA path.
 bool prefill_routed_supported(int quant, int down_quant, size_t H, size_t I, size_t E);
-// Assignments from which the routed layer takes the MFMA path.
-constexpr size_t kPrefillMinAssignments = 256;
+// Assignments from which the routed layer takes the MFMA path (measured
+// crossover against the several-token decode kernels: 96 to 128 assignments
+// for the c1, c2 and c4 layers; INFERNO_PREFILL_MIN_ASSIGNMENTS overrides).
+constexpr size_t kPrefillMinAssignments = 96;
 
 // 32-bit words of the routed planner's scratch (tile lists and counts).
 size_t prefill_plan_words(size_t A, size_t E);

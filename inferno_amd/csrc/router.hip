@@ -27,8 +27,9 @@ __device__ __forceinline__ float load_x<uint16_t>(const uint16_t* p, size_t i) {
 }
 
 
-// Few tokens: one wavefront per expert row; the row is read once with
-// 16-byte loads and dotted with every token (T <= 16).
+// Few tokens, H not a multiple of 32 (else the matrix-core kernels): one
+// wavefront per expert row; the row is read once with 16-byte loads and
+// dotted with every token (T <= 16).
 template <typename XT>
 __global__ void __launch_bounds__(256)
     logits_small_kernel(const XT* __restrict__ x, const float* __restrict__ w, int T, int H,
@@ -367,7 +368,7 @@ static bool bf16x3_enabled() {
 // pairs per chunk.
 constexpr size_t kRouterSplitGroups = 256;
 int router_logit_parts_max(size_t T, size_t H, size_t E) {
-  if (T <= 16 || H % 256) return 1;
+  if (H % 256) return 1;
   const size_t base = ((E + 63) / 64) * ((T + 15) / 16);
   if (base * 2 > kRouterSplitGroups) return 1;
   int z = 1;
@@ -397,7 +398,7 @@ int launch_router_logit_parts(hipStream_t s, const void* x, int x_dtype, const f
 int launch_router_logits(hipStream_t s, const void* x, int x_dtype, const float* w, size_t T,
                          size_t H, size_t E, float* logits) {
   if (T == 0 || E == 0) return INFERNO_OK;
-  if (T <= 16) {
+  if (T <= 16 && H % 32) {
     dim3 grid(unsigned((E + 3) / 4));
     if (x_dtype == INFERNO_BF16)
       logits_small_kernel<uint16_t><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x), w,
