@@ -118,11 +118,14 @@ bool use_mfma(int quant, int down_quant, size_t T, size_t k, size_t E, size_t H,
          prefill_routed_supported(quant, down_quant, H, I, E);
 }
 
-// `x16`: x already converted to f16 (MFMA path), or null.
+// `x16`: x already converted to f16 (MFMA path), or null. `distinct_ids`:
+// every token's k ids are distinct (the layer's own top-k), so one expert
+// takes at most T rows (caller ids may repeat an expert within a token).
 int run_routed(hipStream_t s, int quant, int down_quant, const void* gate, const void* up,
                const void* down, const void* x, int x_dtype, const uint32_t* ids,
                const float* w, size_t T, size_t k, size_t E, size_t H, size_t I,
-               const MoeScratch& m, bool x_staged, const uint16_t* x16 = nullptr) {
+               const MoeScratch& m, bool x_staged, const uint16_t* x16 = nullptr,
+               bool distinct_ids = false) {
   int st;
   if ((st = launch_dispatch(s, ids, T, k, E, m.offsets, m.sorted, m.active))) return st;
   if (use_mfma(quant, down_quant, T, k, E, H, I)) {
@@ -132,7 +135,8 @@ int run_routed(hipStream_t s, int quant, int down_quant, const void* gate, const
       x16 = conv;
     }
     PrefillRouted p{quant, down_quant, gate, up, down, x16, m.offsets, m.sorted, m.active, w,
-                    T, k, E, H, I, reinterpret_cast<uint16_t*>(m.h), m.y, m.plan};
+                    T, k, E, H, I, reinterpret_cast<uint16_t*>(m.h), m.y, m.plan,
+                    distinct_ids ? T : 0};
     if ((st = timed(s, kTimerGateUp, "prefill: grouped gate/up GEMMs (gemm_kernel / gemm2_kernel, MFMA)",
                     [&] { return launch_prefill_gate_up(s, p); })))
       return st;
@@ -676,7 +680,7 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
     uint16_t* x16 = reinterpret_cast<uint16_t*>(w.moe.stage_x);
     if ((st = launch_to_f16(s, x, x_dtype, T, H, x16))) return st;
     if ((st = run_routed(s, L->quant, L->down_quant, L->gate, L->up, L->down, x, x_dtype, ids,
-                         wts, T, k, E, H, I, w.moe, false, x16)))
+                         wts, T, k, E, H, I, w.moe, false, x16, true)))
       return st;
     if (Is && !shared_gemm) return shared_down_gemv();
     if (shared_gemm &&

@@ -43,6 +43,7 @@ typedef uint32_t u32x2a __attribute__((ext_vector_type(2), aligned(8)));
 constexpr int kUnit = 256;       // values per K unit (super-block / eight Q8_0 blocks)
 constexpr int kTileN = 128;      // weight rows per workgroup
 constexpr int kLdsPitch = 72;    // halfs per LDS token row (64 + 8 pad: conflict-free reads)
+constexpr size_t kGemmCUs = 256;  // MI355X CUs (fixed, so a shape takes the same kernel on any device)
 
 __device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
 __device__ __forceinline__ uint32_t as_u32(half2v v) { return __builtin_bit_cast(uint32_t, v); }
@@ -1049,8 +1050,16 @@ int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
         // gate/up over few tokens: one matrix per wavefront (eight), one
         // weight buffer, four waves per SIMD; token tiles per K unit
         // (INFERNO_PREFILL_XU=0: per 64-deep step; Q8_0 keeps them per step,
-        // its unit tiles would spill)
-        if (Q != INFERNO_Q8_0 && unit_tokens())
+        // its unit tiles would spill). Fewer than two workgroups per CU of
+        // 128-row tiles (few experts, narrow I: c1, the XS layer): 64-row
+        // tiles on four wavefronts, twice the workgroups, so that more of
+        // the weights are in flight per CU
+        if (Q != INFERNO_Q8_0 && unit_tokens() && size_t(a.N / 128) * grid_y < 2 * kGemmCUs &&
+            !switch_off("INFERNO_PREFILL_NARROW32")) {
+          const dim3 g2(unsigned(a.N / 64), grid_y);
+          gemm2_kernel<Q, 2, TM, 1, 2, 1, 4, 1, 1, 4>
+              <<<g2, 256, gemm2_lds_bytes<Q, 2, TM, 2, 1, 4>(), s>>>(a);
+        } else if (Q != INFERNO_Q8_0 && unit_tokens())
           gemm2_kernel<Q, 2, TM, 1, 4, 1, 4, 1, 1, Q != INFERNO_Q8_0 ? 4 : 0>
               <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 1, Q != INFERNO_Q8_0 ? 4 : 0>(), s>>>(a);
         else
@@ -1120,15 +1129,18 @@ PlanView plan_view(uint32_t* plan, size_t A, size_t E) {
 }
 
 // The three tile-list launches of one GEMM.
+// A list no expert can fill (max_rows rows at most: no 128-row tile below
+// 65 rows, no 64-row tile below 33) is not launched; its grid of workgroups
+// that find no tile would still take a few microseconds.
 template <int NMAT>
-int launch_tiled(hipStream_t s, int quant, GemmArgs a, const PlanView& v) {
+int launch_tiled(hipStream_t s, int quant, GemmArgs a, const PlanView& v, size_t max_rows) {
   int st;
   a.tiles = v.l128;
   a.n_tiles = v.counts;
-  if ((st = launch_gemm_q<NMAT, 128>(s, quant, a, unsigned(v.n128)))) return st;
+  if (max_rows > 64 && (st = launch_gemm_q<NMAT, 128>(s, quant, a, unsigned(v.n128)))) return st;
   a.tiles = v.l64;
   a.n_tiles = v.counts + 1;
-  if ((st = launch_gemm_q<NMAT, 64>(s, quant, a, unsigned(v.n64)))) return st;
+  if (max_rows > 32 && (st = launch_gemm_q<NMAT, 64>(s, quant, a, unsigned(v.n64)))) return st;
   a.tiles = v.l32;
   a.n_tiles = v.counts + 2;
   return launch_gemm_q<NMAT, 32>(s, quant, a, unsigned(v.n32));
@@ -1224,7 +1236,7 @@ int launch_prefill_gate_up(hipStream_t s, const PrefillRouted& p) {
   g.N = int(p.I);
   g.K = int(p.H);
   g.h_out = p.h16;
-  return launch_tiled<2>(s, p.quant, g, v);
+  return launch_tiled<2>(s, p.quant, g, v, p.max_rows ? p.max_rows : A);
 }
 
 int launch_prefill_down(hipStream_t s, const PrefillRouted& p) {
@@ -1240,7 +1252,7 @@ int launch_prefill_down(hipStream_t s, const PrefillRouted& p) {
   d.N = int(p.H);
   d.K = int(p.I);
   d.y_out = p.y;
-  return launch_tiled<1>(s, p.down_quant, d, v);
+  return launch_tiled<1>(s, p.down_quant, d, v, p.max_rows ? p.max_rows : A);
 }
 
 int launch_prefill_dense(hipStream_t s, int quant, int down_quant, const void* gate,

@@ -31,6 +31,9 @@ struct PrefillRouted {
   uint16_t* h16;                 // [A, I] SwiGLU intermediate, f16
   float* y;                      // [A, H] per-assignment down rows
   uint32_t* plan;                // prefill_plan_words(A, E)
+  // most rows one expert can take: T when every token's ids are distinct
+  // (the layer's own top-k), 0 when unknown (caller ids: up to A)
+  size_t max_rows;
 };
 
 // Routed gate/up (+SwiGLU, routing weight) over the dispatch groups: plans
