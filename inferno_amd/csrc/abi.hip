@@ -127,8 +127,12 @@ int run_routed(hipStream_t s, int quant, int down_quant, const void* gate, const
                const MoeScratch& m, bool x_staged, const uint16_t* x16 = nullptr,
                bool distinct_ids = false) {
   int st;
-  if ((st = launch_dispatch(s, ids, T, k, E, m.offsets, m.sorted, m.active))) return st;
-  if (use_mfma(quant, down_quant, T, k, E, H, I)) {
+  const bool mfma = use_mfma(quant, down_quant, T, k, E, H, I);
+  // on the MFMA path the dispatch also writes the GEMM's tile lists
+  const PlanOut plan = mfma ? prefill_plan_out(m.plan, T * k, E) : PlanOut{};
+  if ((st = launch_dispatch(s, ids, T, k, E, m.offsets, m.sorted, m.active, mfma ? &plan : nullptr)))
+    return st;
+  if (mfma) {
     if (!x16) {
       uint16_t* conv = reinterpret_cast<uint16_t*>(m.stage_x);
       if ((st = launch_to_f16(s, x, x_dtype, T, H, conv))) return st;

@@ -37,6 +37,16 @@ inline size_t env_size(const char* name, size_t dflt) {
   return size_t(std::strtoull(v, nullptr, 10));
 }
 
+// The grouped GEMM's tile lists, written by the dispatch launch when `l128`
+// is set (the prefill path): per-expert tiles {expert, first row, end row,
+// 0} in expert order, split by row count, and the three list lengths.
+struct PlanOut {
+  uint4* l128;
+  uint4* l64;
+  uint4* l32;
+  uint32_t* counts;  // [3]: lengths of l128, l64, l32
+};
+
 constexpr int kWave = 64;        // CDNA wavefront width
 constexpr int kKBlock = 256;     // K-quant super-block values
 constexpr int kQ8Block = 32;     // Q8_0 block values

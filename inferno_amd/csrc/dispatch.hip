@@ -18,8 +18,8 @@ namespace {
 
 __global__ void __launch_bounds__(kDispatchThreads)
     dispatch_kernel(const uint32_t* __restrict__ ids, int A, int E, uint32_t* __restrict__ offsets,
-                    uint32_t* __restrict__ sorted, uint32_t* __restrict__ active) {
-  dispatch_block(ids, A, E, offsets, sorted, active);
+                    uint32_t* __restrict__ sorted, uint32_t* __restrict__ active, PlanOut plan) {
+  dispatch_block(ids, A, E, offsets, sorted, active, plan);
 }
 
 // Many assignments: workgroup b scatters chunk [b kChunk, (b + 1) kChunk).
@@ -34,7 +34,7 @@ constexpr int kChunk = 2 * kDispatchThreads;
 __global__ void __launch_bounds__(kDispatchThreads)
     dispatch_chunks_kernel(const uint32_t* __restrict__ ids, int A, int E,
                            uint32_t* __restrict__ offsets, uint32_t* __restrict__ sorted,
-                           uint32_t* __restrict__ active) {
+                           uint32_t* __restrict__ active, PlanOut plan) {
   __shared__ uint32_t total[kMaxExperts], before[kMaxExperts], cursor[kMaxExperts];
   // per-wavefront counts (rows of wcount: totals, of wbefore: before the
   // chunk): a match group's leader is the only writer of its expert's slot
@@ -81,7 +81,7 @@ __global__ void __launch_bounds__(kDispatchThreads)
     before[e] = b;
   }
   __syncthreads();
-  if (wave == 0) dispatch_scan(total, E, cursor, blockIdx.x == 0, offsets, active);
+  if (wave == 0) dispatch_scan(total, E, cursor, blockIdx.x == 0, offsets, active, plan);
   __syncthreads();
   for (int e = tid; e < E; e += kDispatchThreads) cursor[e] += before[e];
   __syncthreads();
@@ -91,13 +91,15 @@ __global__ void __launch_bounds__(kDispatchThreads)
 }  // namespace
 
 int launch_dispatch(hipStream_t s, const uint32_t* ids, size_t T, size_t k, size_t E,
-                    uint32_t* offsets, uint32_t* sorted, uint32_t* active) {
+                    uint32_t* offsets, uint32_t* sorted, uint32_t* active, const PlanOut* plan) {
   const size_t A = T * k;
+  const PlanOut po = plan ? *plan : PlanOut{};
   if (A > size_t(2 * kChunk))
     dispatch_chunks_kernel<<<unsigned((A + kChunk - 1) / kChunk), kDispatchThreads, 0, s>>>(
-        ids, int(A), int(E), offsets, sorted, active);
+        ids, int(A), int(E), offsets, sorted, active, po);
   else
-    dispatch_kernel<<<1, kDispatchThreads, 0, s>>>(ids, int(A), int(E), offsets, sorted, active);
+    dispatch_kernel<<<1, kDispatchThreads, 0, s>>>(ids, int(A), int(E), offsets, sorted, active,
+                                                   po);
   INF_LAUNCHED();
   return INFERNO_OK;
 }

@@ -26,8 +26,10 @@ int router_logit_parts_max(size_t T, size_t H, size_t E);
 int launch_router_logit_parts(hipStream_t s, const void* x, int x_dtype, const float* w, size_t T,
                               size_t H, size_t E, float* parts_out, int parts);
 
+// plan: also write the grouped GEMM's tile lists (routing_dev.hpp PlanOut)
 int launch_dispatch(hipStream_t s, const uint32_t* ids, size_t T, size_t k, size_t E,
-                    uint32_t* offsets, uint32_t* sorted, uint32_t* active);
+                    uint32_t* offsets, uint32_t* sorted, uint32_t* active,
+                    const PlanOut* plan = nullptr);
 
 // GEMV stages. Packed-f16 formats (Q2_K, Q3_K, Q4_K, Q8_0) stage their
 // activation rows into `stage` (gemv_stage_bytes bytes) first; with

@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "gemv_common.hpp"
+#include "routing_dev.hpp"
 
 namespace inferno {
 namespace {
@@ -904,62 +905,8 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
 
 // ------------------------------------------------------------- planning
 
-// Tiles of one expert with n rows: full 128-row tiles, then the remainder r
-// as one 128-row (r > 64), 64-row (r > 32) or 32-row tile. The
-// dequantisation cost of a tile does not depend on its row count, the MFMA
-// cost does: small remainders take the cheaper narrow tiles.
-struct TileCounts {
-  uint32_t t128, t64, t32;
-};
-__device__ __forceinline__ TileCounts tile_counts(uint32_t n) {
-  const uint32_t r = n % 128;
-  TileCounts t{n / 128, 0, 0};
-  if (r > 64) t.t128 += 1;
-  else if (r > 32) t.t64 = 1;
-  else if (r > 0) t.t32 = 1;
-  return t;
-}
-
-// One workgroup: the three tile lists of all active experts, expert order.
-__global__ void __launch_bounds__(256)
-    plan_kernel(const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ active,
-                uint4* __restrict__ l128, uint4* __restrict__ l64, uint4* __restrict__ l32,
-                uint32_t* __restrict__ counts) {
-  __shared__ uint32_t sc[3][256];
-  const int j = threadIdx.x;
-  const uint32_t n_act = active[0];
-  uint32_t e = 0, lo = 0, hi = 0;
-  TileCounts t{0, 0, 0};
-  if (uint32_t(j) < n_act) {
-    e = active[1 + j];
-    lo = offsets[e];
-    hi = offsets[e + 1];
-    t = tile_counts(hi - lo);
-  }
-  sc[0][j] = t.t128;
-  sc[1][j] = t.t64;
-  sc[2][j] = t.t32;
-  __syncthreads();
-  for (int o = 1; o < 256; o <<= 1) {
-    uint32_t v[3];
-#pragma unroll
-    for (int l = 0; l < 3; ++l) v[l] = j >= o ? sc[l][j - o] : 0u;
-    __syncthreads();
-#pragma unroll
-    for (int l = 0; l < 3; ++l) sc[l][j] += v[l];
-    __syncthreads();
-  }
-  const uint32_t o128 = sc[0][j] - t.t128, o64 = sc[1][j] - t.t64, o32 = sc[2][j] - t.t32;
-  for (uint32_t q = 0; q < t.t128; ++q)
-    l128[o128 + q] = make_uint4(e, lo + 128 * q, min(hi, lo + 128 * (q + 1)), 0);
-  if (t.t64) l64[o64] = make_uint4(e, lo + 128 * t.t128, hi, 0);
-  if (t.t32) l32[o32] = make_uint4(e, lo + 128 * t.t128, hi, 0);
-  if (j == 255) {
-    counts[0] = sc[0][255];
-    counts[1] = sc[1][255];
-    counts[2] = sc[2][255];
-  }
-}
+// The tile lists themselves are written by the dispatch launch
+// (dispatch_scan with a PlanOut, routing_dev.hpp).
 
 // Upper bounds of the tile lists (grid heights): a 128-row tile covers at
 // least 65 rows, the 64- and 32-row lists hold at most one tile per expert.
@@ -1196,6 +1143,11 @@ bool prefill_dense_supported(int quant, int down_quant, size_t H, size_t Is) {
          Is % kUnit == 0 && H % kTileN == 0 && Is % kTileN == 0;
 }
 
+PlanOut prefill_plan_out(uint32_t* plan, size_t A, size_t E) {
+  const PlanView v = plan_view(plan, A, E);
+  return PlanOut{v.l128, v.l64, v.l32, v.counts};
+}
+
 size_t prefill_plan_words(size_t A, size_t E) {
   return 4 * (bound128(A, E) + 2 * bound_small(A, E)) + 4;
 }
@@ -1223,8 +1175,6 @@ int launch_prefill_gate_up(hipStream_t s, const PrefillRouted& p) {
     return INFERNO_ERR_INVALID;
   }
   const PlanView v = plan_view(p.plan, A, p.E);
-  plan_kernel<<<1, 256, 0, s>>>(p.offsets, p.active, v.l128, v.l64, v.l32, v.counts);
-  INF_LAUNCHED();
   GemmArgs g{};
   g.w0 = static_cast<const uint8_t*>(p.gate);
   g.w1 = static_cast<const uint8_t*>(p.up);

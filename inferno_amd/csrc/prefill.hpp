@@ -15,6 +15,9 @@ constexpr size_t kPrefillMinAssignments = 96;
 
 // 32-bit words of the routed planner's scratch (tile lists and counts).
 size_t prefill_plan_words(size_t A, size_t E);
+// The tile lists inside that scratch, for the dispatch launch to fill
+// (launch_dispatch with a plan) before launch_prefill_gate_up reads them.
+PlanOut prefill_plan_out(uint32_t* plan, size_t A, size_t E);
 
 // x [rows, K] (bf16 or fp32) -> f16 [rows, K], round to nearest even.
 int launch_to_f16(hipStream_t s, const void* x, int x_dtype, size_t rows, size_t K, uint16_t* out);

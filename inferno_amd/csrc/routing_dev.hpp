@@ -329,13 +329,31 @@ __device__ __forceinline__ int expert_bits(int E) {
   return nbits;
 }
 
+// Tiles of one expert with n rows: full 128-row tiles, then the remainder r
+// as one 128-row (r > 64), 64-row (r > 32) or 32-row tile. The
+// dequantisation cost of a tile does not depend on its row count, the MFMA
+// cost does: small remainders take the cheaper narrow tiles.
+struct TileCounts {
+  uint32_t t128, t64, t32;
+};
+__device__ __forceinline__ TileCounts tile_counts(uint32_t n) {
+  const uint32_t r = n % 128;
+  TileCounts t{n / 128, 0, 0};
+  if (r > 64) t.t128 += 1;
+  else if (r > 32) t.t64 = 1;
+  else if (r > 0) t.t32 = 1;
+  return t;
+}
+
 // Exclusive scan of count[0..E) on wavefront 0 (each lane owns four
 // consecutive experts, E <= 256) into cursor[]; when `write`, also the
 // expert offsets (offsets[E] = total) and the compacted active list
-// (active[0] = number of experts with assignments).
+// (active[0] = number of experts with assignments), and with plan.l128 set
+// the tile lists (experts in id order, tile counts scanned the same way).
 __device__ __forceinline__ void dispatch_scan(const uint32_t* count, int E, uint32_t* cursor,
                                               bool write, uint32_t* __restrict__ offsets,
-                                              uint32_t* __restrict__ active) {
+                                              uint32_t* __restrict__ active,
+                                              PlanOut plan = PlanOut{}) {
   const int lane = threadIdx.x & 63;
   uint32_t c4[4], f4[4], cs = 0, fs = 0;
 #pragma unroll
@@ -356,6 +374,7 @@ __device__ __forceinline__ void dispatch_scan(const uint32_t* count, int E, uint
     }
   }
   uint32_t cex = ci - cs, fex = fi - fs;
+  const uint32_t c_first = cex;  // offset of this lane's first expert
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int e = 4 * lane + j;
@@ -372,6 +391,45 @@ __device__ __forceinline__ void dispatch_scan(const uint32_t* count, int E, uint
   if (write && lane == 63) {
     offsets[E] = ci;
     active[0] = fi;
+  }
+  if (!write || plan.l128 == nullptr) return;  // uniform
+  TileCounts t4[4];
+  uint32_t s128 = 0, s64 = 0, s32 = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    t4[j] = tile_counts(c4[j]);  // zero for e >= E (c4 is zero there)
+    s128 += t4[j].t128;
+    s64 += t4[j].t64;
+    s32 += t4[j].t32;
+  }
+  uint32_t i128 = s128, i64 = s64, i32 = s32;  // inclusive wave scans
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t a = __shfl_up(i128, o, kWave), b = __shfl_up(i64, o, kWave),
+                   c = __shfl_up(i32, o, kWave);
+    if (lane >= o) {
+      i128 += a;
+      i64 += b;
+      i32 += c;
+    }
+  }
+  uint32_t o128 = i128 - s128, o64 = i64 - s64, o32 = i32 - s32, lo = c_first;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t e = uint32_t(4 * lane + j), hi = lo + c4[j];
+    for (uint32_t q = 0; q < t4[j].t128; ++q)
+      plan.l128[o128 + q] = make_uint4(e, lo + 128 * q, min(hi, lo + 128 * (q + 1)), 0);
+    if (t4[j].t64) plan.l64[o64] = make_uint4(e, lo + 128 * t4[j].t128, hi, 0);
+    if (t4[j].t32) plan.l32[o32] = make_uint4(e, lo + 128 * t4[j].t128, hi, 0);
+    o128 += t4[j].t128;
+    o64 += t4[j].t64;
+    o32 += t4[j].t32;
+    lo = hi;
+  }
+  if (lane == 63) {
+    plan.counts[0] = i128;
+    plan.counts[1] = i64;
+    plan.counts[2] = i32;
   }
 }
 
@@ -419,7 +477,8 @@ __device__ __forceinline__ void dispatch_scatter(const uint32_t* ids, int a_begi
 __device__ __forceinline__ void dispatch_block(const uint32_t* ids, int A, int E,
                                                uint32_t* __restrict__ offsets,
                                                uint32_t* __restrict__ sorted,
-                                               uint32_t* __restrict__ active) {
+                                               uint32_t* __restrict__ active,
+                                               PlanOut plan = PlanOut{}) {
   __shared__ uint32_t count[kMaxExperts];
   __shared__ uint32_t cursor[kMaxExperts];
   __shared__ uint32_t wcount[kDispatchWaves * kMaxExperts];  // [wave][expert], row stride E
@@ -431,7 +490,7 @@ __device__ __forceinline__ void dispatch_block(const uint32_t* ids, int A, int E
     if (e < uint32_t(E)) atomicAdd(&count[e], 1u);
   }
   __syncthreads();
-  if (wave == 0) dispatch_scan(count, E, cursor, true, offsets, active);
+  if (wave == 0) dispatch_scan(count, E, cursor, true, offsets, active, plan);
   __syncthreads();
   dispatch_scatter(ids, 0, A, E, cursor, wcount, sorted);
 }
