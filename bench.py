@@ -256,12 +256,26 @@ def main():
         gu_flops = 4.0 * H * I * A
         gu_tfs = gu_flops / (gu_us * 1e-6) / 1e12
         dn_tfs = 2.0 * H * I * A / (dn_us * 1e-6) / 1e12
-        roofline = {"bound": "mfma", "kernel": labels[ops.TIMER_GATE_UP],
-                    "achieved": round(gu_tfs, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(gu_tfs / MFMA_BF16_PEAK_TFLOPS, 4),
-                    "traffic": None, "launch_us": round(gu_us, 3),
-                    "flops_per_launch": gu_flops,
-                    "routed_bytes_per_launch": int(gu_routed)}
+        # the gate/up launch's bound by its arithmetic intensity (flops per
+        # algorithmic byte, the expert weights each read once) against the
+        # ridge point of the two peaks: c5 (~900 flop/B) is MFMA-bound; c3
+        # (~75), c4 at T = 32 and c1 at T = 16 stream their weights (HBM)
+        gu_gbps = gu_routed / (gu_us * 1e-6) / 1e9
+        intensity = gu_flops / max(gu_routed, 1.0)
+        ridge = MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+        mfma_frac = round(gu_tfs / MFMA_BF16_PEAK_TFLOPS, 4)
+        hbm_frac = round(gu_gbps / HBM_PEAK_GBS, 4)
+        if intensity >= ridge:
+            roofline = {"bound": "mfma", "achieved": round(gu_tfs, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                        "unit": "TFLOP/s", "frac": mfma_frac}
+        else:
+            roofline = {"bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": hbm_frac}
+        roofline.update({"kernel": labels[ops.TIMER_GATE_UP], "traffic": None,
+                         "launch_us": round(gu_us, 3), "flops_per_launch": gu_flops,
+                         "routed_bytes_per_launch": int(gu_routed),
+                         "flops_per_byte": round(intensity, 1), "ridge_flops_per_byte": round(ridge, 1),
+                         "mfma_frac": mfma_frac, "hbm_frac": hbm_frac})
         extra["down_launch"] = {"launch_us": round(dn_us, 3), "TFLOPs": round(dn_tfs, 2)}
         extra["layer_mfma_frac"] = round(6.0 * H * I * A * n_sub / (layer_us * 1e-6) / 1e12
                                          / MFMA_BF16_PEAK_TFLOPS, 4)
