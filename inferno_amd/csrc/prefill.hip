@@ -1001,12 +1001,18 @@ int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
         // 128-row tiles (few experts, narrow I: c1, the XS layer): 64-row
         // tiles on four wavefronts, twice the workgroups, so that more of
         // the weights are in flight per CU
-        if (Q != INFERNO_Q8_0 && unit_tokens() && size_t(a.N / 128) * grid_y < 2 * kGemmCUs &&
-            !switch_off("INFERNO_PREFILL_NARROW32")) {
-          const dim3 g2(unsigned(a.N / 64), grid_y);
-          gemm2_kernel<Q, 2, TM, 1, 2, 1, 4, 1, 1, 4>
-              <<<g2, 256, gemm2_lds_bytes<Q, 2, TM, 2, 1, 4>(), s>>>(a);
-        } else if (Q != INFERNO_Q8_0 && unit_tokens())
+        // (not Q3_K: its 64-row instance spills 18 registers)
+        if constexpr (Q == INFERNO_Q2_K || Q == INFERNO_Q4_K) {
+          if (unit_tokens() && size_t(a.N / 128) * grid_y < 2 * kGemmCUs &&
+              !switch_off("INFERNO_PREFILL_NARROW32")) {
+            const dim3 g2(unsigned(a.N / 64), grid_y);
+            gemm2_kernel<Q, 2, TM, 1, 2, 1, 4, 1, 1, 4>
+                <<<g2, 256, gemm2_lds_bytes<Q, 2, TM, 2, 1, 4>(), s>>>(a);
+            INF_LAUNCHED();
+            return INFERNO_OK;
+          }
+        }
+        if (Q != INFERNO_Q8_0 && unit_tokens())
           gemm2_kernel<Q, 2, TM, 1, 4, 1, 4, 1, 1, Q != INFERNO_Q8_0 ? 4 : 0>
               <<<grid, 512, gemm2_lds_bytes<Q, 2, TM, 4, 1, Q != INFERNO_Q8_0 ? 4 : 0>(), s>>>(a);
         else
