@@ -135,6 +135,38 @@ __global__ void __launch_bounds__(256) route_kernel(DecodeArgs p, int gx, int gy
   if (e >= E || c >= p.n_chunks) return;
   const int h0 = c * p.chunk;
   const float* wrow = p.router + size_t(e) * H + h0;
+  if (T == 1 && int(gridDim.x) == gx * gy) {
+    // one token, no shared workgroups (c1: the router is the whole launch):
+    // the lane's router values of the chunk (NF float4: chunks are 256, 512
+    // or 768 wide) and its x values, all loads issued before the first
+    // product (the loop below waits for each 256-value step's loads in
+    // turn); same summation order. With shared workgroups in the launch
+    // (c2, c4) they bound it, and the loop measured as fast.
+    auto one = [&](auto nf_c) {
+      constexpr int NF = decltype(nf_c)::value;
+      float4 wv[NF];
+      float xv[NF][4];
+#pragma unroll
+      for (int j = 0; j < NF; ++j) {
+        const int i = lane * 4 + 256 * j;
+        wv[j] = *reinterpret_cast<const float4*>(wrow + i);
+        const XT* xr = static_cast<const XT*>(p.x) + h0 + i;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xv[j][q] = to_f32(xr[q]);
+      }
+      float a1 = 0.f;
+#pragma unroll
+      for (int j = 0; j < NF; ++j)
+        a1 += wv[j].x * xv[j][0] + wv[j].y * xv[j][1] + wv[j].z * xv[j][2] + wv[j].w * xv[j][3];
+      const float s1 = wave_sum(a1);
+      if (lane == 0) p.partials[size_t(c) * E + e] = s1;
+    };
+    const int nf = p.chunk / 256;  // uniform; decode_chunk gives 768, 512 or 256
+    if (nf == 3) one(std::integral_constant<int, 3>{});
+    else if (nf == 2) one(std::integral_constant<int, 2>{});
+    else one(std::integral_constant<int, 1>{});
+    return;
+  }
   float acc[16];
   for (int t0 = 0; t0 < T; t0 += 16) {
 #pragma unroll
