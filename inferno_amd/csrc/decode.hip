@@ -205,7 +205,9 @@ __device__ __forceinline__ void sum_partials(const DecodeArgs& p, int t, float* 
       float v[8];
 #pragma unroll
       for (int c = 0; c < 8; ++c)
-        v[c] = c0 + c < p.n_chunks ? p.partials[(size_t(c0 + c) * T + t) * E + e] : 0.f;
+        v[c] = c0 + c < p.n_chunks  // clamped address: the eight loads go out together
+                   ? p.partials[(size_t(min(c0 + c, p.n_chunks - 1)) * T + t) * E + e]
+                   : 0.f;
 #pragma unroll
       for (int c = 0; c < 8; ++c) s += v[c];
     }

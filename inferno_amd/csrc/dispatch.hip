@@ -55,7 +55,8 @@ __global__ void __launch_bounds__(kDispatchThreads)
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int a = base + u * kDispatchThreads + tid;
-      ev[u] = a < A ? ids[a] : 0xffffffffu;
+      const uint32_t id = ids[min(a, A - 1)];  // clamped: the U loads go out together
+      ev[u] = a < A ? id : 0xffffffffu;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {

@@ -340,7 +340,8 @@ __global__ void __launch_bounds__(256)
     const size_t stride = size_t(T) * E;
     float v[kMaxRouterParts];
 #pragma unroll
-    for (int z = 0; z < kMaxRouterParts; ++z) v[z] = z < parts ? src[size_t(z) * stride] : 0.f;
+    for (int z = 0; z < kMaxRouterParts; ++z)  // clamped: all loads go out together
+      v[z] = src[size_t(min(z, parts - 1)) * stride];
     float sum = 0.f;
 #pragma unroll
     for (int z = 0; z < kMaxRouterParts; ++z)

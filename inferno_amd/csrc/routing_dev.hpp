@@ -79,7 +79,8 @@ __device__ __forceinline__ void topk_row_wave(const float* row, const float* __r
       sel = lg[j];
     }
     score[j] = s;
-    const float corrected = sel + ((bias != nullptr && e < E) ? bias[e] : 0.0f);
+    const float bv = bias != nullptr ? bias[min(e, E - 1)] : 0.0f;  // clamped, unconditional
+    const float corrected = sel + (e < E ? bv : 0.0f);
     key[j] = total_order_key(corrected);
     live[j] = e < E;
   }
