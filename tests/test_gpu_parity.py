@@ -181,11 +181,16 @@ def _skewed_ids(T, E, k, hot=(0, 1), share=(1.0, 0.8)):
 
 @pytest.mark.parametrize("quant,down", [(Q2_K, Q2_K), (Q3_K, Q3_K), (Q4_K, Q4_K), (Q4_K, Q6_K)])
 @pytest.mark.parametrize("T,H,I,E,k,bf16,skew", [(64, 512, 256, 16, 4, True, False),
-                                                 (96, 768, 512, 8, 4, False, True)])
+                                                 (96, 768, 512, 8, 4, False, True),
+                                                 (40, 512, 256, 8, 4, True, "dup")])
 def test_gguf_moe_mfma_prefill(cuda, quant, down, T, H, I, E, k, bf16, skew):
-    # T * k >= 256 assignments: the MFMA grouped GEMM (f16 operands, fp32
+    # T * k >= 96 assignments: the MFMA grouped GEMM (f16 operands, fp32
     # accumulation). The skewed case gives two experts >= 64 rows (128-row
-    # tiles) next to small experts (32-row tiles).
+    # tiles) next to small experts (32-row tiles). "dup": caller ids that
+    # name expert 0 twice in every token (the entry point takes any ids),
+    # so one expert holds 2 T = 80 rows although T = 40: the 128-row tile
+    # launch must run (the layer's own top-k never repeats an id, and there
+    # T <= 64 skips it).
     # weights of realistic size (N(0, 0.02) quantised): the f16 operands and
     # the f16 intermediate, as in the reference's prefill kernels
     # (gguf_moe_prefill_kernels.metal:50-59, :263), cover |h| < 65504 only
@@ -196,8 +201,12 @@ def test_gguf_moe_mfma_prefill(cuda, quant, down, T, H, I, E, k, bf16, skew):
     x = torch.randn(T, H, device=cuda)
     if bf16:
         x = x.bfloat16()
-    ids = (_skewed_ids(T, E, k) if skew else
-           np.stack([rng.permutation(E)[:k] for _ in range(T)]).reshape(-1).astype(np.uint32))
+    if skew == "dup":
+        ids = np.stack([np.concatenate([[0, 0], 1 + rng.permutation(E - 1)[:k - 2]])
+                        for _ in range(T)]).reshape(-1).astype(np.uint32)
+    else:
+        ids = (_skewed_ids(T, E, k) if skew else
+               np.stack([rng.permutation(E)[:k] for _ in range(T)]).reshape(-1).astype(np.uint32))
     w = rng.random(T * k).astype(np.float32)
     args = (quant, down, dev(gate, cuda), dev(up, cuda), dev(dn, cuda), x,
             dev(ids.view(np.int32), cuda), dev(w, cuda), k, E, I)
