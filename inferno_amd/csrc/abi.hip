@@ -653,7 +653,20 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
     return launch_decode_layer(s, d, L->quant);
   }
   const int parts = router_logit_parts(T, H, E, x_dtype);
-  if ((st = launch_router_logit_parts(s, x, x_dtype, L->router, T, H, E, w.logits, parts)))
+  const bool mfma_path = use_mfma(L->quant, L->down_quant, T, k, E, H, I);
+  // the shared expert on the dense MFMA GEMMs when its formats have them
+  // (Q8_0; the Laguna XS Q4_K gate/up with Q4_K or Q6_K down), else on the
+  // GEMV kernels
+  const bool shared_gemm = Is && prefill_dense_supported(sq, sdq, H, Is);
+  // x in f16 for the grouped GEMMs (moe.stage_x, which a shared expert on
+  // the GEMVs stages into first); fp32 tokens over K chunks get it from the
+  // logits launch (INFERNO_ROUTER_X16=0: its own launch)
+  uint16_t* x16 = reinterpret_cast<uint16_t*>(w.moe.stage_x);
+  const bool x16_by_router = mfma_path && !(Is && !shared_gemm) &&
+                             router_writes_x16(T, H, E, x_dtype, parts) &&
+                             !switch_off("INFERNO_ROUTER_X16");
+  if ((st = launch_router_logit_parts(s, x, x_dtype, L->router, T, H, E, w.logits, parts,
+                                      x16_by_router ? x16 : nullptr)))
     return st;
   if ((st = launch_router_topk(s, w.logits, L->router_bias, T, E, k, L->score_fn,
                                L->norm_topk_prob, L->routed_scaling_factor, ids, wts, nullptr,
@@ -672,17 +685,12 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
     return launch_gemv_down_dense(s, sdq, L->shared_down, w.hs, sdq_staged ? w.stage_hs : nullptr,
                                   sdq_staged, w.moe.y, k, nullptr, residual, T, Is, H, out);
   };
-  if (use_mfma(L->quant, L->down_quant, T, k, E, H, I)) {
-    // the shared expert on the dense MFMA GEMMs when its formats have them
-    // (Q8_0; the Laguna XS Q4_K gate/up with Q4_K or Q6_K down), else on the
-    // GEMV kernels
-    const bool shared_gemm = Is && prefill_dense_supported(sq, sdq, H, Is);
+  if (mfma_path) {
     // a shared expert on the GEMVs runs its gate/up first, while moe.stage_x
     // still holds its staging (the f16 copy of x reuses it)
     if (Is && !shared_gemm && (st = shared_gate_up_gemv(false))) return st;
     // x in f16 once for the routed and the shared expert GEMMs
-    uint16_t* x16 = reinterpret_cast<uint16_t*>(w.moe.stage_x);
-    if ((st = launch_to_f16(s, x, x_dtype, T, H, x16))) return st;
+    if (!x16_by_router && (st = launch_to_f16(s, x, x_dtype, T, H, x16))) return st;
     if ((st = run_routed(s, L->quant, L->down_quant, L->gate, L->up, L->down, x, x_dtype, ids,
                          wts, T, k, E, H, I, w.moe, false, x16, true)))
       return st;

@@ -23,8 +23,12 @@ int launch_router_topk(hipStream_t s, const float* logits, const float* bias, si
 // any token type and switch setting (workspace sizing).
 int router_logit_parts(size_t T, size_t H, size_t E, int x_dtype);
 int router_logit_parts_max(size_t T, size_t H, size_t E);
+// True when the K-chunk logits launch of fp32 tokens (parts > 1) can also
+// write x in f16 (the grouped GEMMs' copy, as launch_to_f16 writes it).
+bool router_writes_x16(size_t T, size_t H, size_t E, int x_dtype, int parts);
 int launch_router_logit_parts(hipStream_t s, const void* x, int x_dtype, const float* w, size_t T,
-                              size_t H, size_t E, float* parts_out, int parts);
+                              size_t H, size_t E, float* parts_out, int parts,
+                              uint16_t* x16 = nullptr);
 
 // plan: also write the grouped GEMM's tile lists (routing_dev.hpp PlanOut)
 int launch_dispatch(hipStream_t s, const uint32_t* ids, size_t T, size_t k, size_t E,

@@ -142,7 +142,7 @@ __device__ __forceinline__ void load8<uint16_t>(const uint16_t* p, bool ok, floa
 template <typename XT, int NTB>
 __global__ void __launch_bounds__(256)
     logits_mfma_kernel(const XT* __restrict__ x, const float* __restrict__ w, int T, int H, int E,
-                       float* __restrict__ logits) {
+                       float* __restrict__ logits, uint16_t* __restrict__ x16 = nullptr) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int e0 = blockIdx.x * 64 + wave * 16, t0 = blockIdx.y * (16 * NTB);
@@ -175,6 +175,17 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         acc[b][j & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], v[j], acc[b][j & 1], 0, 0, 0);
+      // x16: the f16 copy of x for the grouped GEMMs (to_f16_kernel's k
+      // order 0 2 1 3 4 6 5 7), written by the first expert group's first
+      // wavefront, which reads every token row of the tile over its chunk
+      if (x16 != nullptr && blockIdx.x == 0 && wave == 0 && tv[b]) {
+        auto pair = [](float lo, float hi) {
+          return uint32_t(__builtin_bit_cast(uint16_t, (_Float16)lo)) |
+                 (uint32_t(__builtin_bit_cast(uint16_t, (_Float16)hi)) << 16);
+        };
+        *reinterpret_cast<uint4*>(x16 + size_t(t0 + 16 * b + r) * H + k0 + 8 * g) =
+            make_uint4(pair(v[0], v[2]), pair(v[1], v[3]), pair(v[4], v[6]), pair(v[5], v[7]));
+      }
     }
   }
   // lane holds C[4 g + q][r]: expert e0 + 4 g + q, token t0 + 16 b + r
@@ -376,13 +387,22 @@ int router_logit_parts_max(size_t T, size_t H, size_t E) {
   while (z < kMaxRouterParts && base * size_t(2 * z) <= kRouterSplitGroups && (H / 32) % size_t(4 * z) == 0) z *= 2;
   return z;
 }
+bool router_writes_x16(size_t T, size_t H, size_t E, int x_dtype, int parts) {
+  (void)T; (void)E;
+  return x_dtype == INFERNO_F32 && parts > 1 && H % 32 == 0;
+}
+
 int router_logit_parts(size_t T, size_t H, size_t E, int x_dtype) {
   if (x_dtype == INFERNO_BF16 && !bf16x3_enabled()) return 1;
   return router_logit_parts_max(T, H, E);
 }
 
 int launch_router_logit_parts(hipStream_t s, const void* x, int x_dtype, const float* w, size_t T,
-                              size_t H, size_t E, float* parts_out, int parts) {
+                              size_t H, size_t E, float* parts_out, int parts, uint16_t* x16) {
+  if (x16 != nullptr && !router_writes_x16(T, H, E, x_dtype, parts)) {
+    set_error("router logits: this launch does not write the f16 copy of x");
+    return INFERNO_ERR_INVALID;
+  }
   if (parts <= 1) return launch_router_logits(s, x, x_dtype, w, T, H, E, parts_out);
   if (T == 0 || E == 0) return INFERNO_OK;
   const dim3 grid(unsigned((E + 63) / 64), unsigned((T + 15) / 16), unsigned(parts));
@@ -391,7 +411,7 @@ int launch_router_logit_parts(hipStream_t s, const void* x, int x_dtype, const f
                                                     int(H), int(E), parts_out);
   else  // fp32 tokens on the fp32 matrix cores, K split the same way
     logits_mfma_kernel<float, 1><<<grid, 256, 0, s>>>(static_cast<const float*>(x), w, int(T),
-                                                      int(H), int(E), parts_out);
+                                                      int(H), int(E), parts_out, x16);
   INF_LAUNCHED();
   return INFERNO_OK;
 }

@@ -847,6 +847,26 @@ def _labels_of_one_step(cfg, cuda, T=1):
     return labels, counts
 
 
+@pytest.mark.parametrize("key,T", [("c1", 16), ("xs", 64), ("c1", 300)])
+def test_layer_prefill_router_x16_variant(cuda, switches, key, T):
+    """fp32 tokens on the grouped GEMMs with the router logits over K chunks:
+    the logits launch also writes x in f16 for the GEMMs (no conversion
+    launch); INFERNO_ROUTER_X16=0 keeps the conversion launch. Same f16
+    rounding of the same values: outputs bit-identical; the default agrees
+    with the oracle."""
+    cfg = cf.CONFIGS[key]
+    _layer_parity(cuda, cfg, T, tokens=None if T <= 64 else np.arange(0, T, 7))
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
+    x = cf.make_input(cfg, T, variant=2, device=cuda)
+    residual = torch.randn(T, cfg.hidden, device=cuda)
+    outs = []
+    for flag in ("1", "0"):
+        switches(INFERNO_ROUTER_X16=flag)
+        outs.append(lt.layer.forward(x, residual))
+        torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("runs", [True, False])
 def test_layer_c1_fp32_token_kernels(cuda, switches, runs):
     """One fp32 token (c1): the f16 run kernels with two f16 terms per run
