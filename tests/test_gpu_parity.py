@@ -847,14 +847,18 @@ def _labels_of_one_step(cfg, cuda, T=1):
     return labels, counts
 
 
-@pytest.mark.parametrize("key,T", [("c1", 16), ("xs", 64), ("c1", 300)])
+_E128_FP32 = cf.Config("q4k_h2048_e128_fp32_q8shared", 91, 2048, 128, 768, 8, (Q4_K,),
+                       cf.SCORE_SIGMOID, True, 2.5, 0.1, 1024, torch.float32, (24,))
+
+
+@pytest.mark.parametrize("key,T", [("c1", 16), ("xs", 64), ("c1", 300), (_E128_FP32, 24)])
 def test_layer_prefill_router_x16_variant(cuda, switches, key, T):
     """fp32 tokens on the grouped GEMMs with the router logits over K chunks:
     the logits launch also writes x in f16 for the GEMMs (no conversion
     launch); INFERNO_ROUTER_X16=0 keeps the conversion launch. Same f16
     rounding of the same values: outputs bit-identical; the default agrees
     with the oracle."""
-    cfg = cf.CONFIGS[key]
+    cfg = cf.CONFIGS[key] if isinstance(key, str) else key  # E 128: two expert groups
     _layer_parity(cuda, cfg, T, tokens=None if T <= 64 else np.arange(0, T, 7))
     lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
     x = cf.make_input(cfg, T, variant=2, device=cuda)
