@@ -871,6 +871,19 @@ def test_layer_prefill_router_x16_variant(cuda, switches, key, T):
     assert torch.equal(outs[0], outs[1])
 
 
+# The router caps (256 experts, top-16, the reference's limits,
+# metal/moe.rs:618-623, moe_kernels.metal:131) on a small layer: one token,
+# a few tokens (the decode launches) and 64 tokens (1024 assignments: the
+# grouped GEMM, ~4 rows per expert), Q2_K with a Q8_0 shared expert, bf16
+# and fp32 tokens, against the oracle.
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T", [1, 5, 64])
+def test_layer_router_caps(cuda, T, dt):
+    cfg = cf.Config(f"caps_e256_k16_t{T}", 95, 512, 256, 256, 16, (Q2_K,), cf.SCORE_SIGMOID, True,
+                    2.5, 0.1, 256, dt, (T,))
+    _layer_parity(cuda, cfg, T, variants=2)
+
+
 @pytest.mark.parametrize("runs", [True, False])
 def test_layer_c1_fp32_token_kernels(cuda, switches, runs):
     """One fp32 token (c1): the f16 run kernels with two f16 terms per run
