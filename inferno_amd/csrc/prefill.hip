@@ -963,6 +963,27 @@ bool unit_tokens() { return !switch_off("INFERNO_PREFILL_XU"); }
 template <int Q, int NMAT, int TM>
 int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
   if (grid_y == 0) return INFERNO_OK;
+  // Q2_K (c5) on more, smaller workgroups with one LDS weight buffer, so
+  // that three or four waves share each SIMD: the 128-token down on staged
+  // weights (four wavefronts, 48 KB of LDS, three workgroups per CU; the
+  // fragment-load kernel runs two waves per SIMD): 1125 -> 1066 us; the
+  // 64-token gate/up as one matrix per wavefront on 64-row tiles (four
+  // wavefronts, four workgroups per CU): 468 -> 438 us; c5 layer 5.28 ->
+  // 5.22 ms (three A/B pairs). INFERNO_PREFILL_Q2_SMALL_WG=0: the kernels
+  // below.
+  if constexpr (Q == INFERNO_Q2_K && ((NMAT == 1 && TM == 128) || (NMAT == 2 && TM == 64))) {
+    if (a.N % 128 == 0 && gemm2_enabled() && !switch_off("INFERNO_PREFILL_Q2_SMALL_WG")) {
+      if constexpr (NMAT == 1) {
+        const dim3 g2(unsigned(a.N / 128), grid_y);
+        gemm2_kernel<Q, 1, TM, 1, 4, 1, 3, 1, 0><<<g2, 256, gemm2_lds_bytes<Q, 1, TM, 4, 1>(), s>>>(a);
+      } else {
+        const dim3 g2(unsigned(a.N / 64), grid_y);
+        gemm2_kernel<Q, 2, TM, 1, 2, 1, 4, 1, 1><<<g2, 256, gemm2_lds_bytes<Q, 2, TM, 2, 1>(), s>>>(a);
+      }
+      INF_LAUNCHED();
+      return INFERNO_OK;
+    }
+  }
   // staged weights where measured faster: 32- and 64-token tiles, the Q3_K
   // down, the Q2_K gate/up over 128 tokens and the Q8_0 shared expert (the
   // Q3_K 128-token gate/up and the Q2_K 128-token down stay on the fragment

@@ -625,10 +625,15 @@ def c5_check_tokens(ids, T, k, E):
     return np.array(sorted(rows)), load, sorted(classes)
 
 
-def test_layer_c5_glm_q2k_prefill_zipf(cuda):
+@pytest.mark.parametrize("variant", ["default", "wide"])
+def test_layer_c5_glm_q2k_prefill_zipf(cuda, switches, variant):
     # full-size skewed prefill: router bias fitted so the load follows
     # Zipf(1.1) over 216 experts (hottest capped at one slot per token,
-    # 12.5%), 40 experts without a token
+    # 12.5%), 40 experts without a token. "wide": the Q2_K GEMMs on their
+    # larger-workgroup kernels (INFERNO_PREFILL_Q2_SMALL_WG=0,
+    # INFERNO_PREFILL_G128_WIDE=1), against the same oracle bound
+    if variant == "wide":
+        switches(INFERNO_PREFILL_Q2_SMALL_WG="0", INFERNO_PREFILL_G128_WIDE="1")
     cfg = cf.CONFIGS["c5"]
     T, k, E = 4096, cfg.top_k, cfg.experts
     lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
