@@ -969,13 +969,17 @@ int launch_gemm(hipStream_t s, const GemmArgs& a, unsigned grid_y) {
   // fragment-load kernel runs two waves per SIMD): 1125 -> 1066 us; the
   // 64-token gate/up as one matrix per wavefront on 64-row tiles (four
   // wavefronts, four workgroups per CU): 468 -> 438 us; c5 layer 5.28 ->
-  // 5.22 ms (three A/B pairs). INFERNO_PREFILL_Q2_SMALL_WG=0: the kernels
-  // below.
-  if constexpr (Q == INFERNO_Q2_K && ((NMAT == 1 && TM == 128) || (NMAT == 2 && TM == 64))) {
+  // 5.22 ms (three A/B pairs); the 64-token down with one LDS weight buffer
+  // at four waves per SIMD: 300 -> 221 us, layer 4.93 -> 4.84 ms.
+  // INFERNO_PREFILL_Q2_SMALL_WG=0: the kernels below.
+  if constexpr (Q == INFERNO_Q2_K && (TM == 128 || TM == 64) && (NMAT == 1 || TM == 64)) {
     if (a.N % 128 == 0 && gemm2_enabled() && !switch_off("INFERNO_PREFILL_Q2_SMALL_WG")) {
-      if constexpr (NMAT == 1) {
+      if constexpr (NMAT == 1 && TM == 128) {
         const dim3 g2(unsigned(a.N / 128), grid_y);
         gemm2_kernel<Q, 1, TM, 1, 4, 1, 3, 1, 0><<<g2, 256, gemm2_lds_bytes<Q, 1, TM, 4, 1>(), s>>>(a);
+      } else if constexpr (NMAT == 1) {
+        const dim3 g2(unsigned(a.N / 128), grid_y);
+        gemm2_kernel<Q, 1, TM, 1, 4, 1, 4, 1, 0><<<g2, 256, gemm2_lds_bytes<Q, 1, TM, 4, 1>(), s>>>(a);
       } else {
         const dim3 g2(unsigned(a.N / 64), grid_y);
         gemm2_kernel<Q, 2, TM, 1, 2, 1, 4, 1, 1><<<g2, 256, gemm2_lds_bytes<Q, 2, TM, 2, 1>(), s>>>(a);
