@@ -496,6 +496,7 @@ struct LayerScratch {
   uint32_t* stage_xm;
   uint32_t* stage_xr;
   float* shared_gu;
+  void* blas;  // the Q8_0 shared expert on library GEMMs (large batches), or null
 };
 LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   LayerScratch s;
@@ -515,6 +516,13 @@ LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   s.shared_gu = c.take<float>(L->shared_intermediate
                                   ? decode_shared_partial_floats(L->hidden, L->shared_intermediate)
                                   : 1);
+  const int sq = L->shared_quant ? L->shared_quant : INFERNO_Q8_0;
+  const int sdq = L->shared_down_quant ? L->shared_down_quant : INFERNO_Q8_0;
+  const bool blas = L->shared_intermediate &&
+                    dense_blas_fits(sq, sdq, T, L->hidden, L->shared_intermediate);
+  s.blas = blas ? static_cast<void*>(c.take<unsigned char>(
+                      dense_blas_workspace_bytes(T, L->hidden, L->shared_intermediate)))
+                : nullptr;
   return s;
 }
 }  // namespace
@@ -697,7 +705,7 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
     if (Is && !shared_gemm) return shared_down_gemv();
     if (shared_gemm &&
         (st = launch_prefill_dense(s, sq, sdq, L->shared_gate, L->shared_up, L->shared_down, x16,
-                                   T, H, Is, reinterpret_cast<uint16_t*>(w.hs), w.ys)))
+                                   T, H, Is, reinterpret_cast<uint16_t*>(w.hs), w.ys, w.blas)))
       return st;
     return launch_prefill_combine(s, w.moe.y, Is ? w.ys : nullptr, residual, T, k, H, out);
   }

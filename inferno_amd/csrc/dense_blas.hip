@@ -1,0 +1,250 @@
+// The Q8_0 shared expert of a large prefill batch as library GEMMs.
+//
+// Reference: the shared expert of the prefill layer (crates/model/src/
+// laguna/gguf_model.rs:802-823; q8_0 gate/up SwiGLU and matvec-add kernels,
+// q2_kernels.metal:2066-2133): shared = W_d (silu(W_g x) * (W_u x)).
+//
+// Over many tokens it is a plain dense GEMM, so it runs as one: the Q8_0
+// blocks are expanded to f16 (round(d * q), the value the MFMA kernels'
+// in-register dequantisation forms), hipBLASLt multiplies with fp32
+// accumulation and fp32 output, a small kernel forms h = silu(g) * u in f16
+// (one rounding, as the grouped kernels' epilogue), and a second GEMM gives
+// the shared rows ys in fp32. The gate/up weights are expanded in the k
+// order of the f16 token copy (0 2 1 3 4 6 5 7 inside every eight, the
+// grouped kernels' operand order), the down weights and h in plain order.
+//
+// Work per call: the expansion reads the 34-byte blocks once and writes
+// 2 bytes per weight; the GEMMs are the library's (its algorithm picked by
+// its heuristic once per shape and kept).
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "gemv_common.hpp"
+#include "prefill.hpp"
+
+namespace inferno {
+namespace {
+
+// Tokens from which the shared expert takes the library GEMMs (below it the
+// grouped kernels' dense path).
+constexpr size_t kBlasMinTokens = 256;
+constexpr size_t kBlasWsBytes = size_t(32) << 20;  // the library's own workspace
+
+// Q8_0 [d f16 | 32 int8] blocks -> f16 rows. A 64-thread workgroup takes 64
+// consecutive 272-byte units (eight blocks, 256 values; 16-byte aligned)
+// of one matrix: the units are read into LDS with contiguous 16-byte loads,
+// then every output chunk of eight values (one uint4) is formed from LDS by
+// one thread, so that the stores are contiguous too. permute: k order
+// 0 2 1 3 4 6 5 7 inside every eight. The three matrices (gate, up:
+// permuted; down: plain) in one launch.
+struct ExpandArgs {
+  const uint8_t* src[3];
+  uint16_t* dst[3];
+  size_t groups[3];  // 64-unit groups of each matrix (the last may be partial)
+  size_t units[3];   // 256-value units of each matrix
+  int permute[3];
+};
+constexpr int kExpandThreads = 64;
+constexpr int kUnitBytes = 272;
+__global__ void __launch_bounds__(kExpandThreads) q8_0_to_f16_kernel(ExpandArgs a) {
+  __shared__ uint4 lds[kExpandThreads * kUnitBytes / 16];
+  size_t g = blockIdx.x;
+  int m = 0;
+  while (m < 3 && g >= a.groups[m]) g -= a.groups[m++];
+  if (m == 3) return;  // uniform
+  const size_t u0 = g * kExpandThreads;
+  const int nu = int(min(size_t(kExpandThreads), a.units[m] - u0));
+  const uint4* s4 = reinterpret_cast<const uint4*>(a.src[m] + u0 * kUnitBytes);
+  const int n16 = nu * kUnitBytes / 16;
+  for (int j = threadIdx.x; j < n16; j += kExpandThreads) lds[j] = s4[j];
+  __syncthreads();
+  const uint8_t* lb = reinterpret_cast<const uint8_t*>(lds);
+  const bool perm = a.permute[m] != 0;
+  uint4* o4 = reinterpret_cast<uint4*>(a.dst[m] + u0 * 256);
+  const int nchunks = nu * 32;  // uint4 chunks of eight values
+  for (int c = threadIdx.x; c < nchunks; c += kExpandThreads) {
+    const int u = c >> 5, w = c & 31, blk = w >> 2, q8 = w & 3;
+    const uint8_t* bp = lb + u * kUnitBytes + 34 * blk;
+    const float d = f16_bits_to_f32(uint16_t(bp[0] | (bp[1] << 8)));
+    uint32_t hv[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      hv[q] = __builtin_bit_cast(uint16_t, (_Float16)(d * float(int8_t(bp[2 + 8 * q8 + q]))));
+    const int p1 = perm ? 2 : 1, p2 = perm ? 1 : 2, p5 = perm ? 6 : 5, p6 = perm ? 5 : 6;
+    o4[c] = make_uint4(hv[0] | (hv[p1] << 16), hv[p2] | (hv[3] << 16), hv[4] | (hv[p5] << 16),
+                       hv[p6] | (hv[7] << 16));
+  }
+}
+
+// h[t][i] = silu(gu[t][i]) * gu[t][Is + i] in f16 (plain order), from the
+// gate/up GEMM's fp32 rows [T][2 Is].
+__global__ void __launch_bounds__(256)
+    swiglu_f16_kernel(const float* __restrict__ gu, size_t T, size_t Is,
+                      uint16_t* __restrict__ h) {
+  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= T * Is) return;
+  const size_t t = i / Is, c = i - t * Is;
+  const float g = gu[t * 2 * Is + c], u = gu[t * 2 * Is + Is + c];
+  h[i] = __builtin_bit_cast(uint16_t, (_Float16)(silu(g) * u));
+}
+
+constexpr int kMaxBlasDevices = 64;
+std::mutex g_blas_mu;
+hipblasLtHandle_t g_blas[kMaxBlasDevices] = {};
+std::map<std::tuple<int, int, int, int>, hipblasLtMatmulHeuristicResult_t> g_algo;
+
+int blas_error(const char* what, int status) {
+  set_error(std::string("hipBLASLt ") + what + " failed (status " + std::to_string(status) + ")");
+  return INFERNO_ERR_DEVICE;
+}
+
+// D[n][m] (row-major, fp32) = X[n][k] (row-major f16) . W[m][k]^T (row-major
+// f16): column-major D^T = op(W)^T-view x X-view with op(A) = T.
+int blas_gemm(hipStream_t s, const uint16_t* W, const uint16_t* X, float* D, int m, int n, int k,
+              void* ws) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxBlasDevices) {
+    set_error("hipBLASLt: cannot query the current device");
+    return INFERNO_ERR_DEVICE;
+  }
+  std::lock_guard<std::mutex> lock(g_blas_mu);
+  if (!g_blas[dev]) {
+    const hipblasStatus_t st = hipblasLtCreate(&g_blas[dev]);
+    if (st != HIPBLAS_STATUS_SUCCESS) return blas_error("create", int(st));
+  }
+  hipblasLtHandle_t h = g_blas[dev];
+  hipblasLtMatmulDesc_t op = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+  int rc = INFERNO_OK;
+  hipblasStatus_t st;
+  const hipblasOperation_t tA = HIPBLAS_OP_T, tB = HIPBLAS_OP_N;
+  const float alpha = 1.0f, beta = 0.0f;
+  auto fail = [&](const char* what) {
+    rc = blas_error(what, int(st));
+    return rc;
+  };
+  do {
+    if ((st = hipblasLtMatmulDescCreate(&op, HIPBLAS_COMPUTE_32F, HIP_R_32F)) != HIPBLAS_STATUS_SUCCESS) {
+      fail("matmul descriptor");
+      break;
+    }
+    hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSA, &tA, sizeof(tA));
+    hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSB, &tB, sizeof(tB));
+    if ((st = hipblasLtMatrixLayoutCreate(&la, HIP_R_16F, k, m, k)) != HIPBLAS_STATUS_SUCCESS ||
+        (st = hipblasLtMatrixLayoutCreate(&lb, HIP_R_16F, k, n, k)) != HIPBLAS_STATUS_SUCCESS ||
+        (st = hipblasLtMatrixLayoutCreate(&lc, HIP_R_32F, m, n, m)) != HIPBLAS_STATUS_SUCCESS) {
+      fail("matrix layout");
+      break;
+    }
+    const auto key = std::make_tuple(dev, m, n, k);
+    auto it = g_algo.find(key);
+    if (it == g_algo.end()) {
+      hipblasLtMatmulPreference_t pref = nullptr;
+      if ((st = hipblasLtMatmulPreferenceCreate(&pref)) != HIPBLAS_STATUS_SUCCESS) {
+        fail("preference");
+        break;
+      }
+      const uint64_t wsb = kBlasWsBytes;
+      hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
+                                            sizeof(wsb));
+      hipblasLtMatmulHeuristicResult_t res{};
+      int found = 0;
+      st = hipblasLtMatmulAlgoGetHeuristic(h, op, la, lb, lc, lc, pref, 1, &res, &found);
+      hipblasLtMatmulPreferenceDestroy(pref);
+      if (st != HIPBLAS_STATUS_SUCCESS || found < 1) {
+        if (st == HIPBLAS_STATUS_SUCCESS) st = HIPBLAS_STATUS_NOT_SUPPORTED;
+        fail("heuristic");
+        break;
+      }
+      it = g_algo.emplace(key, res).first;
+    }
+    if ((st = hipblasLtMatmul(h, op, &alpha, W, la, X, lb, &beta, D, lc, D, lc, &it->second.algo,
+                              ws, kBlasWsBytes, s)) != HIPBLAS_STATUS_SUCCESS) {
+      fail("matmul");
+      break;
+    }
+  } while (false);
+  if (lc) hipblasLtMatrixLayoutDestroy(lc);
+  if (lb) hipblasLtMatrixLayoutDestroy(lb);
+  if (la) hipblasLtMatrixLayoutDestroy(la);
+  if (op) hipblasLtMatmulDescDestroy(op);
+  return rc;
+}
+
+// Carved regions of the workspace, 256-byte aligned.
+struct BlasWs {
+  uint16_t* wgu;  // [2 Is][H] f16 (gate rows, then up rows), k order permuted
+  uint16_t* wd;   // [H][Is] f16
+  float* gu;      // [T][2 Is] fp32
+  uint16_t* h;    // [T][Is] f16
+  void* lib;      // the library's workspace
+  size_t end;
+};
+BlasWs carve(void* base, size_t T, size_t H, size_t Is) {
+  auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+  BlasWs w{};
+  char* p = static_cast<char*>(base);
+  size_t o = 0;
+  w.wgu = reinterpret_cast<uint16_t*>(p + o); o += al(2 * Is * H * 2);
+  w.wd = reinterpret_cast<uint16_t*>(p + o);  o += al(H * Is * 2);
+  w.gu = reinterpret_cast<float*>(p + o);     o += al(T * 2 * Is * 4);
+  w.h = reinterpret_cast<uint16_t*>(p + o);   o += al(T * Is * 2);
+  w.lib = p + o;                              o += kBlasWsBytes;
+  w.end = o;
+  return w;
+}
+
+int launch_expand(hipStream_t s, const void* gate, const void* up, const void* down, size_t H,
+                  size_t Is, uint16_t* wgu, uint16_t* wd) {
+  ExpandArgs a{};
+  a.src[0] = static_cast<const uint8_t*>(gate);
+  a.src[1] = static_cast<const uint8_t*>(up);
+  a.src[2] = static_cast<const uint8_t*>(down);
+  a.dst[0] = wgu;
+  a.dst[1] = wgu + Is * H;
+  a.dst[2] = wd;
+  const size_t units = Is * H / 256;  // H, Is multiples of 256
+  for (int m = 0; m < 3; ++m) {
+    a.units[m] = units;
+    a.groups[m] = (units + kExpandThreads - 1) / kExpandThreads;
+    a.permute[m] = m < 2 ? 1 : 0;
+  }
+  q8_0_to_f16_kernel<<<unsigned(3 * a.groups[0]), kExpandThreads, 0, s>>>(a);
+  INF_LAUNCHED();
+  return INFERNO_OK;
+}
+
+}  // namespace
+
+bool dense_blas_fits(int quant, int down_quant, size_t T, size_t H, size_t Is) {
+  return quant == INFERNO_Q8_0 && down_quant == INFERNO_Q8_0 && T >= kBlasMinTokens &&
+         H % 256 == 0 && Is % 256 == 0 && T < (size_t(1) << 30) && 2 * Is < (size_t(1) << 30) &&
+         H < (size_t(1) << 30);
+}
+
+// INFERNO_SHARED_BLAS=0: the grouped kernels' dense path at every T.
+bool dense_blas_takes(int quant, int down_quant, size_t T, size_t H, size_t Is) {
+  return dense_blas_fits(quant, down_quant, T, H, Is) && !switch_off("INFERNO_SHARED_BLAS");
+}
+
+size_t dense_blas_workspace_bytes(size_t T, size_t H, size_t Is) {
+  return carve(nullptr, T, H, Is).end + 256;
+}
+
+int launch_dense_blas(hipStream_t s, const void* gate, const void* up, const void* down,
+                      const uint16_t* x16, size_t T, size_t H, size_t Is, float* ys, void* ws) {
+  const BlasWs w = carve(reinterpret_cast<void*>((reinterpret_cast<uintptr_t>(ws) + 255) /
+                                                 256 * 256), T, H, Is);
+  int st;
+  if ((st = launch_expand(s, gate, up, down, H, Is, w.wgu, w.wd))) return st;
+  if ((st = blas_gemm(s, w.wgu, x16, w.gu, int(2 * Is), int(T), int(H), w.lib))) return st;
+  const size_t n = T * Is;
+  swiglu_f16_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(w.gu, T, Is, w.h);
+  INF_LAUNCHED();
+  return blas_gemm(s, w.wd, w.h, ys, int(H), int(T), int(Is), w.lib);
+}
+
+}  // namespace inferno

@@ -50,9 +50,21 @@ int launch_prefill_down(hipStream_t s, const PrefillRouted& p);
 bool prefill_dense_supported(int quant, int down_quant, size_t H, size_t Is);
 // Dense expert over all T rows (gate/up format quant, down down_quant):
 // h16 = silu(x G^T) * (x U^T); ys = h16 D^T.
+// The Q8_0 shared expert of a batch of T tokens on library GEMMs (f16
+// weights expanded per call, fp32 accumulation): taken by
+// launch_prefill_dense when it is given a workspace of
+// dense_blas_workspace_bytes and dense_blas_takes holds.
+// dense_blas_fits: the shapes the path covers (the workspace is sized by it);
+// dense_blas_takes: those, unless switched off.
+bool dense_blas_fits(int quant, int down_quant, size_t T, size_t H, size_t Is);
+bool dense_blas_takes(int quant, int down_quant, size_t T, size_t H, size_t Is);
+size_t dense_blas_workspace_bytes(size_t T, size_t H, size_t Is);
+int launch_dense_blas(hipStream_t s, const void* gate, const void* up, const void* down,
+                      const uint16_t* x16, size_t T, size_t H, size_t Is, float* ys, void* ws);
 int launch_prefill_dense(hipStream_t s, int quant, int down_quant, const void* gate,
                          const void* up, const void* down, const uint16_t* x16, size_t T,
-                         size_t H, size_t Is, uint16_t* h16, float* ys);
+                         size_t H, size_t Is, uint16_t* h16, float* ys,
+                         void* blas_ws = nullptr);
 
 // out = (residual + ys) + sum over ranks of y[t*k + r] (rank order); residual,
 // ys may be null.

@@ -954,6 +954,20 @@ def test_layer_decode_shared_expert_alone(cuda, switches, sel):
     _layer_parity(cuda, cfg, 1, variants=4, tol=1e-3)
 
 
+@pytest.mark.parametrize("blas", ["1", "0"])
+@pytest.mark.parametrize("key,T", [("c3", 512), ("c4", 300)])
+def test_layer_prefill_shared_expert_alone(cuda, switches, blas, key, T):
+    """The Q8_0 shared expert of a grouped-GEMM batch alone (routing scale
+    0): on the library GEMMs (default from 256 tokens: the blocks expanded
+    to f16, fp32 accumulation, h in f16) or on the grouped kernels' dense
+    path (INFERNO_SHARED_BLAS=0); every 4th token against the oracle. Both
+    round x and h to f16 as the reference prefill does: bound 2e-3."""
+    switches(INFERNO_SHARED_BLAS=blas)
+    cfg = dataclasses.replace(cf.CONFIGS[key], name=f"{key}_shared_alone", scale=0.0,
+                              balanced=False, zipf=0.0)
+    _layer_parity(cuda, cfg, T, tokens=np.arange(0, T, 4))
+
+
 @pytest.mark.parametrize("key", ["c2", "c4", "small", "small_noshared"])
 def test_layer_decode_warm_down_has_no_effect_on_results(cuda, switches, key):
     """The selecting gate/up launch warms L2 with the down launch's first
