@@ -496,7 +496,9 @@ struct LayerScratch {
   uint32_t* stage_xm;
   uint32_t* stage_xr;
   float* shared_gu;
-  void* blas;  // the Q8_0 shared expert on library GEMMs (large batches), or null
+  void* blas;     // the Q8_0 shared expert on library GEMMs (large batches), or null
+  void* rblas;    // the router's bf16 terms for the library GEMMs (large batches), or null
+  void* blas_lib; // the library's workspace when either runs, or null
 };
 LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   LayerScratch s;
@@ -523,6 +525,13 @@ LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
   s.blas = blas ? static_cast<void*>(c.take<unsigned char>(
                       dense_blas_workspace_bytes(T, L->hidden, L->shared_intermediate)))
                 : nullptr;
+  const bool rblas = router_blas_fits(T, L->hidden, L->experts);
+  s.rblas = rblas ? static_cast<void*>(c.take<unsigned char>(
+                        router_blas_workspace_bytes(L->hidden, L->experts)))
+                  : nullptr;
+  s.blas_lib = (blas || rblas) ? static_cast<void*>(c.take<unsigned char>(
+                                     blas_lib_workspace_bytes()))
+                               : nullptr;
   return s;
 }
 }  // namespace
@@ -660,7 +669,10 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
     d.h_quant = L->down_quant;
     return launch_decode_layer(s, d, L->quant);
   }
-  const int parts = router_logit_parts(T, H, E, x_dtype);
+  // bf16 tokens of a large batch: the logits as three library GEMMs
+  const bool router_blas = w.rblas != nullptr && w.blas_lib != nullptr &&
+                           router_blas_takes(T, H, E, x_dtype);
+  const int parts = router_blas ? 1 : router_logit_parts(T, H, E, x_dtype);
   const bool mfma_path = use_mfma(L->quant, L->down_quant, T, k, E, H, I);
   // the shared expert on the dense MFMA GEMMs when its formats have them
   // (Q8_0; the Laguna XS Q4_K gate/up with Q4_K or Q6_K down), else on the
@@ -673,9 +685,14 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
   const bool x16_by_router = mfma_path && !(Is && !shared_gemm) &&
                              router_writes_x16(T, H, E, x_dtype, parts) &&
                              !switch_off("INFERNO_ROUTER_X16");
-  if ((st = launch_router_logit_parts(s, x, x_dtype, L->router, T, H, E, w.logits, parts,
-                                      x16_by_router ? x16 : nullptr)))
+  if (router_blas) {
+    if ((st = launch_router_blas(s, static_cast<const uint16_t*>(x), L->router, T, H, E,
+                                 w.logits, w.rblas, w.blas_lib)))
+      return st;
+  } else if ((st = launch_router_logit_parts(s, x, x_dtype, L->router, T, H, E, w.logits, parts,
+                                             x16_by_router ? x16 : nullptr))) {
     return st;
+  }
   if ((st = launch_router_topk(s, w.logits, L->router_bias, T, E, k, L->score_fn,
                                L->norm_topk_prob, L->routed_scaling_factor, ids, wts, nullptr,
                                parts)))
@@ -705,7 +722,8 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
     if (Is && !shared_gemm) return shared_down_gemv();
     if (shared_gemm &&
         (st = launch_prefill_dense(s, sq, sdq, L->shared_gate, L->shared_up, L->shared_down, x16,
-                                   T, H, Is, reinterpret_cast<uint16_t*>(w.hs), w.ys, w.blas)))
+                                   T, H, Is, reinterpret_cast<uint16_t*>(w.hs), w.ys, w.blas,
+                                   w.blas_lib)))
       return st;
     return launch_prefill_combine(s, w.moe.y, Is ? w.ys : nullptr, residual, T, k, H, out);
   }

@@ -32,6 +32,8 @@ namespace {
 // grouped kernels' dense path).
 constexpr size_t kBlasMinTokens = 256;
 constexpr size_t kBlasWsBytes = size_t(32) << 20;  // the library's own workspace
+// Tokens from which bf16 router logits take three library GEMMs.
+constexpr size_t kRouterBlasMinTokens = 2048;
 
 // Q8_0 [d f16 | 32 int8] blocks -> f16 rows. A 64-thread workgroup takes 64
 // consecutive 272-byte units (eight blocks, 256 values; 16-byte aligned)
@@ -79,6 +81,42 @@ __global__ void __launch_bounds__(kExpandThreads) q8_0_to_f16_kernel(ExpandArgs 
   }
 }
 
+// The router's fp32 weights as three bf16 terms (terms + m E H, m = 0, 1,
+// 2): truncate, subtract, truncate, subtract, truncate; the last remainder
+// has at most eight significant bits, so w = t0 + t1 + t2 exactly, and a
+// bf16 x bf16 product is exact in fp32: three bf16 GEMMs accumulated in
+// fp32 give fp32-accurate logits (the split of the router logits kernel's
+// bf16x3 path, done once per call here).
+__global__ void __launch_bounds__(256)
+    split3_kernel(const float* __restrict__ w, size_t n8, size_t n, uint16_t* __restrict__ terms) {
+  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const float4 a = reinterpret_cast<const float4*>(w)[2 * i];
+  const float4 b = reinterpret_cast<const float4*>(w)[2 * i + 1];
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t h[3][4];
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    uint32_t t[3][2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t u = __builtin_bit_cast(uint32_t, v[j + q]);
+      const uint32_t u1 = u & 0xffff0000u;
+      const float r1 = v[j + q] - __builtin_bit_cast(float, u1);
+      const uint32_t u2 = __builtin_bit_cast(uint32_t, r1) & 0xffff0000u;
+      const float r2 = r1 - __builtin_bit_cast(float, u2);
+      t[0][q] = u1 >> 16;
+      t[1][q] = u2 >> 16;
+      t[2][q] = __builtin_bit_cast(uint32_t, r2) >> 16;
+    }
+#pragma unroll
+    for (int m = 0; m < 3; ++m) h[m][j / 2] = t[m][0] | (t[m][1] << 16);
+  }
+#pragma unroll
+  for (int m = 0; m < 3; ++m)
+    reinterpret_cast<uint4*>(terms + size_t(m) * n)[i] = make_uint4(h[m][0], h[m][1], h[m][2], h[m][3]);
+}
+
 // h[t][i] = silu(gu[t][i]) * gu[t][Is + i] in f16 (plain order), from the
 // gate/up GEMM's fp32 rows [T][2 Is].
 __global__ void __launch_bounds__(256)
@@ -94,7 +132,7 @@ __global__ void __launch_bounds__(256)
 constexpr int kMaxBlasDevices = 64;
 std::mutex g_blas_mu;
 hipblasLtHandle_t g_blas[kMaxBlasDevices] = {};
-std::map<std::tuple<int, int, int, int>, hipblasLtMatmulHeuristicResult_t> g_algo;
+std::map<std::tuple<int, int, int, int, int, int>, hipblasLtMatmulHeuristicResult_t> g_algo;
 
 int blas_error(const char* what, int status) {
   set_error(std::string("hipBLASLt ") + what + " failed (status " + std::to_string(status) + ")");
@@ -104,7 +142,7 @@ int blas_error(const char* what, int status) {
 // D[n][m] (row-major, fp32) = X[n][k] (row-major f16) . W[m][k]^T (row-major
 // f16): column-major D^T = op(W)^T-view x X-view with op(A) = T.
 int blas_gemm(hipStream_t s, const uint16_t* W, const uint16_t* X, float* D, int m, int n, int k,
-              void* ws) {
+              void* ws, hipDataType in_type = HIP_R_16F, float beta = 0.0f) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxBlasDevices) {
     set_error("hipBLASLt: cannot query the current device");
@@ -121,7 +159,7 @@ int blas_gemm(hipStream_t s, const uint16_t* W, const uint16_t* X, float* D, int
   int rc = INFERNO_OK;
   hipblasStatus_t st;
   const hipblasOperation_t tA = HIPBLAS_OP_T, tB = HIPBLAS_OP_N;
-  const float alpha = 1.0f, beta = 0.0f;
+  const float alpha = 1.0f;
   auto fail = [&](const char* what) {
     rc = blas_error(what, int(st));
     return rc;
@@ -133,13 +171,13 @@ int blas_gemm(hipStream_t s, const uint16_t* W, const uint16_t* X, float* D, int
     }
     hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSA, &tA, sizeof(tA));
     hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSB, &tB, sizeof(tB));
-    if ((st = hipblasLtMatrixLayoutCreate(&la, HIP_R_16F, k, m, k)) != HIPBLAS_STATUS_SUCCESS ||
-        (st = hipblasLtMatrixLayoutCreate(&lb, HIP_R_16F, k, n, k)) != HIPBLAS_STATUS_SUCCESS ||
+    if ((st = hipblasLtMatrixLayoutCreate(&la, in_type, k, m, k)) != HIPBLAS_STATUS_SUCCESS ||
+        (st = hipblasLtMatrixLayoutCreate(&lb, in_type, k, n, k)) != HIPBLAS_STATUS_SUCCESS ||
         (st = hipblasLtMatrixLayoutCreate(&lc, HIP_R_32F, m, n, m)) != HIPBLAS_STATUS_SUCCESS) {
       fail("matrix layout");
       break;
     }
-    const auto key = std::make_tuple(dev, m, n, k);
+    const auto key = std::make_tuple(dev, m, n, k, int(in_type), beta != 0.0f ? 1 : 0);
     auto it = g_algo.find(key);
     if (it == g_algo.end()) {
       hipblasLtMatmulPreference_t pref = nullptr;
@@ -180,7 +218,6 @@ struct BlasWs {
   uint16_t* wd;   // [H][Is] f16
   float* gu;      // [T][2 Is] fp32
   uint16_t* h;    // [T][Is] f16
-  void* lib;      // the library's workspace
   size_t end;
 };
 BlasWs carve(void* base, size_t T, size_t H, size_t Is) {
@@ -192,7 +229,6 @@ BlasWs carve(void* base, size_t T, size_t H, size_t Is) {
   w.wd = reinterpret_cast<uint16_t*>(p + o);  o += al(H * Is * 2);
   w.gu = reinterpret_cast<float*>(p + o);     o += al(T * 2 * Is * 4);
   w.h = reinterpret_cast<uint16_t*>(p + o);   o += al(T * Is * 2);
-  w.lib = p + o;                              o += kBlasWsBytes;
   w.end = o;
   return w;
 }
@@ -235,16 +271,50 @@ size_t dense_blas_workspace_bytes(size_t T, size_t H, size_t Is) {
 }
 
 int launch_dense_blas(hipStream_t s, const void* gate, const void* up, const void* down,
-                      const uint16_t* x16, size_t T, size_t H, size_t Is, float* ys, void* ws) {
+                      const uint16_t* x16, size_t T, size_t H, size_t Is, float* ys, void* ws,
+                      void* lib_ws) {
   const BlasWs w = carve(reinterpret_cast<void*>((reinterpret_cast<uintptr_t>(ws) + 255) /
                                                  256 * 256), T, H, Is);
   int st;
   if ((st = launch_expand(s, gate, up, down, H, Is, w.wgu, w.wd))) return st;
-  if ((st = blas_gemm(s, w.wgu, x16, w.gu, int(2 * Is), int(T), int(H), w.lib))) return st;
+  if ((st = blas_gemm(s, w.wgu, x16, w.gu, int(2 * Is), int(T), int(H), lib_ws))) return st;
   const size_t n = T * Is;
   swiglu_f16_kernel<<<unsigned((n + 255) / 256), 256, 0, s>>>(w.gu, T, Is, w.h);
   INF_LAUNCHED();
-  return blas_gemm(s, w.wd, w.h, ys, int(H), int(T), int(Is), w.lib);
+  return blas_gemm(s, w.wd, w.h, ys, int(H), int(T), int(Is), lib_ws);
+}
+
+size_t blas_lib_workspace_bytes() { return kBlasWsBytes; }
+
+// ------------------------------------------------------------ router
+
+bool router_blas_fits(size_t T, size_t H, size_t E) {
+  return T >= kRouterBlasMinTokens && H % 8 == 0 && H < (size_t(1) << 30) && E >= 1 &&
+         E <= 256 && T < (size_t(1) << 30);
+}
+
+bool router_blas_takes(size_t T, size_t H, size_t E, int x_dtype) {
+  return x_dtype == INFERNO_BF16 && router_blas_fits(T, H, E) &&
+         !switch_off("INFERNO_ROUTER_BLAS") && !switch_off("INFERNO_ROUTER_BF16X3");
+}
+
+size_t router_blas_workspace_bytes(size_t H, size_t E) {
+  return (3 * E * H * 2 + 255) / 256 * 256 + 256;
+}
+
+int launch_router_blas(hipStream_t s, const uint16_t* x, const float* w, size_t T, size_t H,
+                       size_t E, float* logits, void* terms_ws, void* lib_ws) {
+  uint16_t* terms = reinterpret_cast<uint16_t*>((reinterpret_cast<uintptr_t>(terms_ws) + 255) /
+                                                256 * 256);
+  const size_t n8 = E * H / 8;
+  split3_kernel<<<unsigned((n8 + 255) / 256), 256, 0, s>>>(w, n8, E * H, terms);
+  INF_LAUNCHED();
+  int st;
+  for (int m = 0; m < 3; ++m)
+    if ((st = blas_gemm(s, terms + size_t(m) * E * H, x, logits, int(E), int(T), int(H), lib_ws,
+                        HIP_R_16BF, m == 0 ? 0.0f : 1.0f)))
+      return st;
+  return INFERNO_OK;
 }
 
 }  // namespace inferno

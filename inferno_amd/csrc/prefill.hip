@@ -1247,14 +1247,15 @@ int launch_prefill_down(hipStream_t s, const PrefillRouted& p) {
 
 int launch_prefill_dense(hipStream_t s, int quant, int down_quant, const void* gate,
                          const void* up, const void* down, const uint16_t* x16, size_t T,
-                         size_t H, size_t Is, uint16_t* h16, float* ys, void* blas_ws) {
+                         size_t H, size_t Is, uint16_t* h16, float* ys, void* blas_ws,
+                         void* lib_ws) {
   if (T == 0) return INFERNO_OK;
   if (H % kUnit || Is % kUnit) {
     set_error("MFMA prefill path needs 256-multiple dimensions");
     return INFERNO_ERR_INVALID;
   }
-  if (blas_ws != nullptr && dense_blas_takes(quant, down_quant, T, H, Is))
-    return launch_dense_blas(s, gate, up, down, x16, T, H, Is, ys, blas_ws);
+  if (blas_ws != nullptr && lib_ws != nullptr && dense_blas_takes(quant, down_quant, T, H, Is))
+    return launch_dense_blas(s, gate, up, down, x16, T, H, Is, ys, blas_ws, lib_ws);
   GemmArgs g{};
   g.w0 = static_cast<const uint8_t*>(gate);
   g.w1 = static_cast<const uint8_t*>(up);

@@ -60,11 +60,21 @@ bool dense_blas_fits(int quant, int down_quant, size_t T, size_t H, size_t Is);
 bool dense_blas_takes(int quant, int down_quant, size_t T, size_t H, size_t Is);
 size_t dense_blas_workspace_bytes(size_t T, size_t H, size_t Is);
 int launch_dense_blas(hipStream_t s, const void* gate, const void* up, const void* down,
-                      const uint16_t* x16, size_t T, size_t H, size_t Is, float* ys, void* ws);
+                      const uint16_t* x16, size_t T, size_t H, size_t Is, float* ys, void* ws,
+                      void* lib_ws);
+// The library's own workspace, shared by the calls of one stream.
+size_t blas_lib_workspace_bytes();
+// Router logits of T bf16 tokens as three bf16 library GEMMs over the exact
+// three-term split of the fp32 router (fp32 accumulation): logits [T][E].
+bool router_blas_fits(size_t T, size_t H, size_t E);
+bool router_blas_takes(size_t T, size_t H, size_t E, int x_dtype);
+size_t router_blas_workspace_bytes(size_t H, size_t E);
+int launch_router_blas(hipStream_t s, const uint16_t* x, const float* w, size_t T, size_t H,
+                       size_t E, float* logits, void* terms_ws, void* lib_ws);
 int launch_prefill_dense(hipStream_t s, int quant, int down_quant, const void* gate,
                          const void* up, const void* down, const uint16_t* x16, size_t T,
                          size_t H, size_t Is, uint16_t* h16, float* ys,
-                         void* blas_ws = nullptr);
+                         void* blas_ws = nullptr, void* lib_ws = nullptr);
 
 // out = (residual + ys) + sum over ranks of y[t*k + r] (rank order); residual,
 // ys may be null.

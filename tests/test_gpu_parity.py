@@ -954,6 +954,40 @@ def test_layer_decode_shared_expert_alone(cuda, switches, sel):
     _layer_parity(cuda, cfg, 1, variants=4, tol=1e-3)
 
 
+@pytest.mark.parametrize("key,T", [("c3", 2048), ("c5", 4096)])
+def test_layer_prefill_router_blas(cuda, switches, key, T):
+    """bf16 tokens of a large batch: router logits as three bf16 library
+    GEMMs over the exact three-term split of the fp32 router (fp32
+    accumulation), against the matrix-core logits kernel
+    (INFERNO_ROUTER_BLAS=0): the selected ids agree except on near-ties of
+    the fp64 scores (gap below 1e-5 of the k-th score), the routing weights
+    within 1e-5, and the layer agrees with the oracle."""
+    cfg = cf.CONFIGS[key]
+    _layer_parity(cuda, cfg, T, tokens=np.arange(0, T, 32))
+    lt = cf.build_layer(cfg, 0, cuda, max_tokens=T)
+    x = cf.make_input(cfg, T, variant=1, device=cuda)
+    k = cfg.top_k
+    res = []
+    for flag in ("1", "0"):
+        switches(INFERNO_ROUTER_BLAS=flag)
+        ids = torch.empty(T * k, dtype=torch.int32, device=cuda)
+        w = torch.empty(T * k, dtype=torch.float32, device=cuda)
+        lt.layer.forward(x, None, ids=ids, weights=w)
+        torch.cuda.synchronize()
+        res.append((ph.to_np(ids).reshape(T, k), ph.to_np(w).reshape(T, k)))
+    (ia, wa), (ib, wb) = res
+    bad = np.nonzero((ia != ib).any(axis=1))[0]
+    if len(bad):
+        lg = ph.x_f32(x)[bad].astype(np.float64) @ ph.to_np(lt.router).astype(np.float64).T
+        sc = 1.0 / (1.0 + np.exp(-lg)) + ph.to_np(lt.bias).astype(np.float64)[None, :]
+        srt = np.sort(sc, axis=1)
+        gaps = srt[:, -k] - srt[:, -k - 1]
+        assert np.all(gaps < 1e-5 * np.abs(srt[:, -k])), gaps
+    good = np.setdiff1d(np.arange(T), bad)
+    np.testing.assert_allclose(wa[good], wb[good], rtol=1e-5, atol=1e-7)
+    print(f"{key} T={T}: tokens with other ids {len(bad)}")
+
+
 @pytest.mark.parametrize("blas", ["1", "0"])
 @pytest.mark.parametrize("key,T", [("c3", 512), ("c4", 300)])
 def test_layer_prefill_shared_expert_alone(cuda, switches, blas, key, T):
