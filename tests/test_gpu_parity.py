@@ -989,7 +989,7 @@ def test_layer_prefill_router_blas(cuda, switches, key, T):
 
 
 @pytest.mark.parametrize("blas", ["1", "0"])
-@pytest.mark.parametrize("key,T", [("c3", 512), ("c4", 300)])
+@pytest.mark.parametrize("key,T", [("c3", 512), ("c4", 300), ("e128_fp32", 300)])
 def test_layer_prefill_shared_expert_alone(cuda, switches, blas, key, T):
     """The Q8_0 shared expert of a grouped-GEMM batch alone (routing scale
     0): on the library GEMMs (default from 256 tokens: the blocks expanded
@@ -997,8 +997,8 @@ def test_layer_prefill_shared_expert_alone(cuda, switches, blas, key, T):
     path (INFERNO_SHARED_BLAS=0); every 4th token against the oracle. Both
     round x and h to f16 as the reference prefill does: bound 2e-3."""
     switches(INFERNO_SHARED_BLAS=blas)
-    cfg = dataclasses.replace(cf.CONFIGS[key], name=f"{key}_shared_alone", scale=0.0,
-                              balanced=False, zipf=0.0)
+    base = _E128_FP32 if key == "e128_fp32" else cf.CONFIGS[key]  # fp32 tokens: x16 from the router
+    cfg = dataclasses.replace(base, name=f"{key}_shared_alone", scale=0.0, balanced=False, zipf=0.0)
     _layer_parity(cuda, cfg, T, tokens=np.arange(0, T, 4))
 
 
