@@ -1,4 +1,5 @@
-// The Q8_0 shared expert of a large prefill batch as library GEMMs.
+// The Q8_0 shared expert of a large prefill batch, and the router logits of
+// a large bf16 batch, as library GEMMs (hipBLASLt).
 //
 // Reference: the shared expert of the prefill layer (crates/model/src/
 // laguna/gguf_model.rs:802-823; q8_0 gate/up SwiGLU and matvec-add kernels,
@@ -15,7 +16,9 @@
 //
 // Work per call: the expansion reads the 34-byte blocks once and writes
 // 2 bytes per weight; the GEMMs are the library's (its algorithm picked by
-// its heuristic once per shape and kept).
+// its heuristic once per shape and kept). The router logits (reference:
+// the router linear, gguf_model.rs:742-748) take the fp32 router split
+// exactly into three bf16 terms and three bf16 GEMMs accumulated in fp32.
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
