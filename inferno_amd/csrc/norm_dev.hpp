@@ -15,6 +15,19 @@ namespace inferno {
 constexpr int kNormThreads = 1024;
 constexpr int kNormVec = 8;  // float4s per thread held in registers
 
+// Sum of squares of one float4 added to s, in a fixed order with explicit
+// fused multiply-adds (every kernel that forms an RMSNorm scale uses it, so
+// they agree bit for bit).
+__device__ __forceinline__ float norm_sq4(float s, float4 v) {
+  s = fmaf(v.x, v.x, s);
+  s = fmaf(v.y, v.y, s);
+  s = fmaf(v.z, v.z, s);
+  return fmaf(v.w, v.w, s);
+}
+
+// One normalised value: x / scale * w (the division rounded first).
+__device__ __forceinline__ float norm_apply(float x, float scale, float w) { return x / scale * w; }
+
 // emit(i, v) receives every normalised value v of position i (each once, by
 // one thread). `part` is LDS of kNormThreads / 64 + 1 floats. Every thread
 // of the workgroup must call it; it contains two barriers.
@@ -24,24 +37,25 @@ __device__ __forceinline__ void rms_norm_row(const float* __restrict__ row,
                                              float* part, Emit emit) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool vec = H % 4 == 0 && H <= size_t(4 * kNormThreads * kNormVec);
-  float4 v[kNormVec];
+  float4 v[kNormVec], g[kNormVec];
   float s = 0.f;
   if (vec) {
+    // the row and the weights in one round trip (clamped addresses, so the
+    // loads are not held behind the bound checks)
     const float4* r4 = reinterpret_cast<const float4*>(row);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    const size_t n4 = H / 4;
 #pragma unroll
     for (int j = 0; j < kNormVec; ++j) {
       const size_t i = size_t(j) * kNormThreads + tid;
-      v[j] = i < H / 4 ? r4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 a = r4[i < n4 ? i : n4 - 1], b = w4[i < n4 ? i : n4 - 1];
+      v[j] = i < n4 ? a : make_float4(0.f, 0.f, 0.f, 0.f);
+      g[j] = b;
     }
 #pragma unroll
-    for (int j = 0; j < kNormVec; ++j) {
-      s += v[j].x * v[j].x;
-      s += v[j].y * v[j].y;
-      s += v[j].z * v[j].z;
-      s += v[j].w * v[j].w;
-    }
+    for (int j = 0; j < kNormVec; ++j) s = norm_sq4(s, v[j]);
   } else {
-    for (size_t i = tid; i < H; i += kNormThreads) s += row[i] * row[i];
+    for (size_t i = tid; i < H; i += kNormThreads) s = fmaf(row[i], row[i], s);
   }
 #pragma unroll
   for (int m = 1; m < 64; m <<= 1) s += __shfl_xor(s, m, 64);
@@ -55,20 +69,18 @@ __device__ __forceinline__ void rms_norm_row(const float* __restrict__ row,
   __syncthreads();
   const float scale = part[kNormThreads / 64];
   if (vec) {
-    const float4* w4 = reinterpret_cast<const float4*>(w);
 #pragma unroll
     for (int j = 0; j < kNormVec; ++j) {
       const size_t i = size_t(j) * kNormThreads + tid;
       if (i < H / 4) {
-        const float4 g = w4[i];
-        emit(4 * i, v[j].x / scale * g.x);
-        emit(4 * i + 1, v[j].y / scale * g.y);
-        emit(4 * i + 2, v[j].z / scale * g.z);
-        emit(4 * i + 3, v[j].w / scale * g.w);
+        emit(4 * i, norm_apply(v[j].x, scale, g[j].x));
+        emit(4 * i + 1, norm_apply(v[j].y, scale, g[j].y));
+        emit(4 * i + 2, norm_apply(v[j].z, scale, g[j].z));
+        emit(4 * i + 3, norm_apply(v[j].w, scale, g[j].w));
       }
     }
   } else {
-    for (size_t i = tid; i < H; i += kNormThreads) emit(i, row[i] / scale * w[i]);
+    for (size_t i = tid; i < H; i += kNormThreads) emit(i, norm_apply(row[i], scale, w[i]));
   }
 }
 
