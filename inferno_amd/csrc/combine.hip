@@ -26,6 +26,40 @@ __global__ void __launch_bounds__(256)
   out[i] = v;
 }
 
+// The same sum, four columns per thread (H a multiple of 4, 16-byte aligned
+// rows), the k rank rows (and weights) loaded at once: KMAX slots, indices
+// clamped to k - 1, the extra slots not added.
+__device__ __forceinline__ void add_scaled(float4& v, const float4& u, float s) {
+  v.x += u.x * s; v.y += u.y * s; v.z += u.z * s; v.w += u.w * s;
+}
+
+template <int KMAX>
+__global__ void __launch_bounds__(256)
+    topk_combine4_kernel(const float* __restrict__ shared, const float* __restrict__ residual,
+                         const float* __restrict__ y, const float* __restrict__ w, uint32_t H4,
+                         uint32_t n4, int k, float* __restrict__ out) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= n4) return;
+  const uint32_t t = i / H4, c4 = i - t * H4;
+  const float4* y4 = reinterpret_cast<const float4*>(y);
+  float4 u[KMAX];
+  float ws[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) {
+    const size_t a = size_t(t) * k + min(r, k - 1);
+    u[r] = y4[a * H4 + c4];
+    ws[r] = w ? w[a] : 1.0f;
+  }
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float4 sh = shared ? reinterpret_cast<const float4*>(shared)[i] : z;
+  const float4 rs = residual ? reinterpret_cast<const float4*>(residual)[i] : z;
+  float4 v = make_float4(sh.x + rs.x, sh.y + rs.y, sh.z + rs.z, sh.w + rs.w);
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r)
+    if (r < k) add_scaled(v, u[r], ws[r]);
+  reinterpret_cast<float4*>(out)[i] = v;
+}
+
 // acc + contributions of every assignment of token t, in assignment order
 // (crates/backend/src/backend.rs:10298-10352; moe_kernels.metal:53-81).
 __global__ void __launch_bounds__(256)
@@ -81,6 +115,20 @@ int launch_topk_combine(hipStream_t s, const float* shared, const float* residua
                         const float* y, const float* w, size_t T, size_t H, size_t k,
                         float* out) {
   if (T * H == 0) return INFERNO_OK;
+  auto a16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+  const size_t n4 = T * H / 4;
+  if (H % 4 == 0 && n4 <= 0xffffffffu && k >= 1 && k <= size_t(kMaxTopK) && a16(y) && a16(out) &&
+      a16(shared) && a16(residual)) {
+    const unsigned grid = unsigned((n4 + 255) / 256);
+    if (k <= 8)
+      topk_combine4_kernel<8><<<grid, 256, 0, s>>>(shared, residual, y, w, uint32_t(H / 4),
+                                                   uint32_t(n4), int(k), out);
+    else
+      topk_combine4_kernel<16><<<grid, 256, 0, s>>>(shared, residual, y, w, uint32_t(H / 4),
+                                                    uint32_t(n4), int(k), out);
+    INF_LAUNCHED();
+    return INFERNO_OK;
+  }
   topk_combine_kernel<<<blocks_for(T * H), 256, 0, s>>>(shared, residual, y, w, T, H, int(k),
                                                         out);
   INF_LAUNCHED();

@@ -929,22 +929,34 @@ __global__ void __launch_bounds__(256)
   out[i] = make_uint4(as_u32(a), as_u32(b), as_u32(c), as_u32(d));
 }
 
+// out = (residual + ys) + y ranks 0..k-1 of the token, in that order; one
+// float4 per thread. The k rank rows are loaded at once (KMAX slots, the
+// indices clamped to k - 1 and the extra slots not added), so a wavefront
+// has all of its loads in flight instead of one rank at a time.
+template <int KMAX>
 __global__ void __launch_bounds__(256)
     combine_kernel(const float* __restrict__ y, const float* __restrict__ ys,
-                   const float* __restrict__ residual, int k, size_t H, size_t n4,
+                   const float* __restrict__ residual, int k, uint32_t H4, uint32_t n4,
                    float4* __restrict__ out) {
-  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
   if (i >= n4) return;
-  const size_t t = (4 * i) / H, col = (4 * i) % H;
+  const uint32_t t = i / H4, c4 = i - t * H4;
+  const float4* y4 = reinterpret_cast<const float4*>(y);
+  float4 u[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r)
+    u[r] = y4[(size_t(t) * k + min(r, k - 1)) * H4 + c4];
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (residual) v = *reinterpret_cast<const float4*>(residual + 4 * i);
+  if (residual) v = reinterpret_cast<const float4*>(residual)[i];
   if (ys) {
-    const float4 s = *reinterpret_cast<const float4*>(ys + 4 * i);
+    const float4 s = reinterpret_cast<const float4*>(ys)[i];
     v.x += s.x; v.y += s.y; v.z += s.z; v.w += s.w;
   }
-  for (int r = 0; r < k; ++r) {
-    const float4 u = *reinterpret_cast<const float4*>(y + (t * k + r) * H + col);
-    v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) {
+    if (r < k) {
+      v.x += u[r].x; v.y += u[r].y; v.z += u[r].z; v.w += u[r].w;
+    }
   }
   out[i] = v;
 }
@@ -1282,8 +1294,16 @@ int launch_prefill_combine(hipStream_t s, const float* y, const float* ys, const
                            size_t T, size_t k, size_t H, float* out) {
   const size_t n4 = T * H / 4;
   if (n4 == 0) return INFERNO_OK;
-  combine_kernel<<<unsigned((n4 + 255) / 256), 256, 0, s>>>(y, ys, residual, int(k), H, n4,
-                                                             reinterpret_cast<float4*>(out));
+  if (H % 4 || n4 > 0xffffffffu || k == 0 || k > size_t(kMaxTopK)) {
+    set_error("prefill combine: H must be a multiple of 4, T * H / 4 < 2^32, 1 <= k <= 16");
+    return INFERNO_ERR_INVALID;
+  }
+  const unsigned grid = unsigned((n4 + 255) / 256);
+  float4* o = reinterpret_cast<float4*>(out);
+  if (k <= 8)
+    combine_kernel<8><<<grid, 256, 0, s>>>(y, ys, residual, int(k), uint32_t(H / 4), uint32_t(n4), o);
+  else
+    combine_kernel<16><<<grid, 256, 0, s>>>(y, ys, residual, int(k), uint32_t(H / 4), uint32_t(n4), o);
   INF_LAUNCHED();
   return INFERNO_OK;
 }

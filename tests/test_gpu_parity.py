@@ -289,6 +289,16 @@ def test_combine_and_gather_kats(cuda):
     c = ph.to_np(ops.topk_combine_residual(sh, res, yk, wk, 2))
     ref = ph.to_np(sh + res + (yk * wk[:, None]).view(3, 2, 8).sum(1))
     assert np.allclose(c, ref, rtol=1e-6, atol=1e-6)
+    # the four-column kernel (k up to 8 and up to 16) and the scalar one
+    # (H not a multiple of 4): rank order, against fp64 sums
+    for T, k, H in ((5, 10, 64), (4, 7, 256), (3, 3, 6)):
+        yk = torch.randn(T * k, H, device=cuda)
+        wk = torch.rand(T * k, device=cuda)
+        sh, res = torch.randn(T, H, device=cuda), torch.randn(T, H, device=cuda)
+        c = ph.to_np(ops.topk_combine_residual(sh, res, yk, wk, k))
+        y64 = ph.to_np(yk).astype(np.float64) * ph.to_np(wk).astype(np.float64)[:, None]
+        ref = ph.to_np(sh).astype(np.float64) + ph.to_np(res) + y64.reshape(T, k, H).sum(1)
+        assert np.allclose(c, ref, rtol=1e-5, atol=1e-5), (T, k, H)
 
 
 def test_rms_norm(cuda):
