@@ -33,6 +33,8 @@ __device__ __forceinline__ void add_scaled(float4& v, const float4& u, float s) 
   v.x += u.x * s; v.y += u.y * s; v.z += u.z * s; v.w += u.w * s;
 }
 
+typedef float fx4 __attribute__((ext_vector_type(4)));
+
 template <int KMAX>
 __global__ void __launch_bounds__(256)
     topk_combine4_kernel(const float* __restrict__ shared, const float* __restrict__ residual,
@@ -47,7 +49,8 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
   for (int r = 0; r < KMAX; ++r) {
     const size_t a = size_t(t) * k + min(r, k - 1);
-    u[r] = y4[a * H4 + c4];
+    const fx4 q = __builtin_nontemporal_load(reinterpret_cast<const fx4*>(y4 + a * H4 + c4));
+    u[r] = make_float4(q[0], q[1], q[2], q[3]);  // read once: nontemporal
     ws[r] = w ? w[a] : 1.0f;
   }
   const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);

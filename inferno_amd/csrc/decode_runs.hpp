@@ -442,7 +442,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_runs_kernel(DecodeArgs p, in
     for (int j = 0; j < PER; ++j) {
       int i = j * kThreads + tid;
       i = i < S::chunks ? i : S::chunks - 1;  // clamped; the extra chunks are not stored
-      v[j] = i < S::chunks / 2 ? g4[i] : u4[i - S::chunks / 2];
+      v[j] = mfma_decode::ld_tile(i < S::chunks / 2 ? g4 + i : u4 + (i - S::chunks / 2));
     }
   };
   int t = blockIdx.x;
@@ -564,7 +564,7 @@ __global__ void __launch_bounds__(kThreads) down_runs_kernel(DecodeArgs p, int n
       const uint32_t e = rank_e[r];
       const uint8_t* base = e == kSharedId ? p.sdown : p.down + size_t(e) * p.down_stride;
       const u32x4* src = reinterpret_cast<const u32x4*>(base + size_t(t) * TR * rb);
-      v[j] = src[w];
+      v[j] = mfma_decode::ld_tile(src + w);
     }
   };
   int t = blockIdx.x;
@@ -783,7 +783,7 @@ __global__ void __launch_bounds__(64 * WV) gate_up_runs_multi_kernel(DecodeArgs 
     for (int j = 0; j < PER; ++j) {
       int i = j * (64 * WV) + tid;
       i = i < S::chunks ? i : S::chunks - 1;  // clamped; the extra chunks are not stored
-      v[j] = i < S::chunks / 2 ? g4[i] : u4[i - S::chunks / 2];
+      v[j] = mfma_decode::ld_tile(i < S::chunks / 2 ? g4 + i : u4 + (i - S::chunks / 2));
     }
     xr.load(p, s2, min(NT, int(s2.z - s2.y)), row_of);
   };
@@ -913,7 +913,7 @@ __global__ void __launch_bounds__(kThreads) down_runs_multi_kernel(DecodeArgs p)
     for (int j = 0; j < PER; ++j) {
       int i = j * kThreads + tid;
       i = i < S::chunks ? i : S::chunks - 1;  // clamped; the extra chunks are not stored
-      v[j] = src[i];
+      v[j] = mfma_decode::ld_tile(src + i);
     }
     hr_pf.load(p, s2, min(NT, int(s2.z - s2.y)), row_of);
   };

@@ -932,7 +932,14 @@ __global__ void __launch_bounds__(256)
 // out = (residual + ys) + y ranks 0..k-1 of the token, in that order; one
 // float4 per thread. The k rank rows are loaded at once (KMAX slots, the
 // indices clamped to k - 1 and the extra slots not added), so a wavefront
-// has all of its loads in flight instead of one rank at a time.
+// has all of its loads in flight instead of one rank at a time; they are
+// read once, as nontemporal loads (c5: 216 -> 181 us for 905 MB).
+typedef float fx4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 load_nt(const float4* p) {
+  const fx4 q = __builtin_nontemporal_load(reinterpret_cast<const fx4*>(p));
+  return make_float4(q[0], q[1], q[2], q[3]);
+}
+
 template <int KMAX>
 __global__ void __launch_bounds__(256)
     combine_kernel(const float* __restrict__ y, const float* __restrict__ ys,
@@ -944,8 +951,7 @@ __global__ void __launch_bounds__(256)
   const float4* y4 = reinterpret_cast<const float4*>(y);
   float4 u[KMAX];
 #pragma unroll
-  for (int r = 0; r < KMAX; ++r)
-    u[r] = y4[(size_t(t) * k + min(r, k - 1)) * H4 + c4];
+  for (int r = 0; r < KMAX; ++r) u[r] = load_nt(y4 + (size_t(t) * k + min(r, k - 1)) * H4 + c4);
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
   if (residual) v = reinterpret_cast<const float4*>(residual)[i];
   if (ys) {
@@ -1298,12 +1304,13 @@ int launch_prefill_combine(hipStream_t s, const float* y, const float* ys, const
     set_error("prefill combine: H must be a multiple of 4, T * H / 4 < 2^32, 1 <= k <= 16");
     return INFERNO_ERR_INVALID;
   }
-  const unsigned grid = unsigned((n4 + 255) / 256);
   float4* o = reinterpret_cast<float4*>(out);
-  if (k <= 8)
-    combine_kernel<8><<<grid, 256, 0, s>>>(y, ys, residual, int(k), uint32_t(H / 4), uint32_t(n4), o);
+  const unsigned grid = unsigned((n4 + 255) / 256);
+  const uint32_t H4 = uint32_t(H / 4), N4 = uint32_t(n4);
+  if (k > 8)
+    combine_kernel<16><<<grid, 256, 0, s>>>(y, ys, residual, int(k), H4, N4, o);
   else
-    combine_kernel<16><<<grid, 256, 0, s>>>(y, ys, residual, int(k), uint32_t(H / 4), uint32_t(n4), o);
+    combine_kernel<8><<<grid, 256, 0, s>>>(y, ys, residual, int(k), H4, N4, o);
   INF_LAUNCHED();
   return INFERNO_OK;
 }
