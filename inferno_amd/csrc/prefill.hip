@@ -471,12 +471,9 @@ template <>
 struct Stage<INFERNO_Q2_K> {
   static constexpr int kWords = 21, kPitch = 21;
   using Chunk = uint32_t;
-  __device__ static Chunk load(const uint8_t* b, int shift) { return ld_u1(b) >> shift; }
+  __device__ static Chunk load(const uint8_t* b) { return ld_u1(b); }
   __device__ static void put(uint32_t* row, int j, Chunk v) { row[j] = v; }
-  __device__ static int offset(int j, int& shift) {
-    shift = 0;
-    return 4 * j;
-  }
+  __device__ static int offset(int j) { return 4 * j; }
   __device__ static void frag(const uint32_t* row, int qc, int kg, uint32_t r[6]) {
     const int h = qc >> 1;
     const uint32_t* a = row + 4 + 8 * h + 2 * kg;
@@ -485,18 +482,17 @@ struct Stage<INFERNO_Q2_K> {
     r[5] = row[20];
   }
 };
-// Q3_K: 110 bytes per row; word 27 holds bytes 108..109 (d), read as the
-// dword at byte 106 shifted down 16 so no load passes the super-block.
+// Q3_K: 110 bytes per row; word 27 is the dword at byte 106 (d in its high
+// half), so no load passes the super-block. The staged words are the loaded
+// ones as they are: nothing uses a loaded value before its LDS store, so the
+// loads stay in flight through the step's MFMAs.
 template <>
 struct Stage<INFERNO_Q3_K> {
   static constexpr int kWords = 28, kPitch = 28;
   using Chunk = uint32_t;
-  __device__ static Chunk load(const uint8_t* b, int shift) { return ld_u1(b) >> shift; }
+  __device__ static Chunk load(const uint8_t* b) { return ld_u1(b); }
   __device__ static void put(uint32_t* row, int j, Chunk v) { row[j] = v; }
-  __device__ static int offset(int j, int& shift) {
-    shift = j == 27 ? 16 : 0;
-    return j == 27 ? 106 : 4 * j;
-  }
+  __device__ static int offset(int j) { return j == 27 ? 106 : 4 * j; }
   __device__ static void frag(const uint32_t* row, int qc, int kg, uint32_t r[11]) {
     const int n = qc >> 1;
     const u32x2a qa = *reinterpret_cast<const u32x2a*>(row + 8 + 8 * n + 2 * kg);
@@ -507,7 +503,7 @@ struct Stage<INFERNO_Q3_K> {
     r[4] = ha.x; r[5] = ha.y; r[6] = hb.x; r[7] = hb.y;
     r[8] = row[24 + (qc & 1)];
     r[9] = row[26];
-    r[10] = row[27] & 0xffffu;
+    r[10] = row[27] >> 16;
   }
 };
 // Q4_K: 144 bytes per row, fetched as nine 16-byte chunks (seven rows per
@@ -517,11 +513,8 @@ template <>
 struct Stage<INFERNO_Q4_K> {
   static constexpr int kWords = 9, kPitch = 37;
   using Chunk = uint4;
-  __device__ static int offset(int j, int& shift) {
-    shift = 0;
-    return 16 * j;
-  }
-  __device__ static Chunk load(const uint8_t* b, int) { return ld_u4(b); }
+  __device__ static int offset(int j) { return 16 * j; }
+  __device__ static Chunk load(const uint8_t* b) { return ld_u4(b); }
   __device__ static void put(uint32_t* row, int j, Chunk v) {
     row[4 * j] = v.x; row[4 * j + 1] = v.y; row[4 * j + 2] = v.z; row[4 * j + 3] = v.w;
   }
@@ -534,24 +527,18 @@ struct Stage<INFERNO_Q4_K> {
 };
 
 // Q6_K: 210 bytes per row, fetched as thirteen 16-byte chunks (bytes
-// 0..207) and a fourteenth holding only the dword at byte 206 shifted down
-// 16 (d), so no load passes the super-block; stored as 53 dwords per row
-// (an odd pitch); Frag<Q6_K>'s words read back from LDS.
+// 0..207) and a fourteenth, bytes 194..209, of which only the last dword
+// (d in its high half) is kept, so no load passes the super-block; stored as
+// 53 dwords per row (an odd pitch); Frag<Q6_K>'s words read back from LDS.
 template <>
 struct Stage<INFERNO_Q6_K> {
   static constexpr int kWords = 14, kPitch = 53;
   using Chunk = uint4;
-  __device__ static int offset(int j, int& shift) {
-    shift = j == 13 ? 16 : 0;
-    return j == 13 ? 206 : 16 * j;
-  }
-  __device__ static Chunk load(const uint8_t* b, int shift) {
-    if (shift) return make_uint4(ld_u1(b) >> shift, 0u, 0u, 0u);
-    return ld_u4(b);
-  }
+  __device__ static int offset(int j) { return j == 13 ? 194 : 16 * j; }
+  __device__ static Chunk load(const uint8_t* b) { return ld_u4(b); }
   __device__ static void put(uint32_t* row, int j, Chunk v) {
     if (j == 13) {
-      row[52] = v.x;
+      row[52] = v.w;
       return;
     }
     row[4 * j] = v.x; row[4 * j + 1] = v.y; row[4 * j + 2] = v.z; row[4 * j + 3] = v.w;
@@ -568,7 +555,7 @@ struct Stage<INFERNO_Q6_K> {
     r[10] = row[36 + 8 * h + 2 * kg];  // qh bytes 144 + 32 h + 8 kg
     r[11] = row[37 + 8 * h + 2 * kg];
     r[12] = row[48 + 2 * h + (qc & 1)];  // scales 8 h + 4 (qc & 1) ..
-    r[13] = row[52] & 0xffffu;           // d
+    r[13] = row[52] >> 16;               // d
   }
 };
 
@@ -581,11 +568,8 @@ template <>
 struct Stage<INFERNO_Q8_0> {
   static constexpr int kWords = 17, kPitch = 69;
   using Chunk = uint4;
-  __device__ static int offset(int j, int& shift) {
-    shift = 0;
-    return 16 * j;
-  }
-  __device__ static Chunk load(const uint8_t* b, int) { return ld_u4(b); }
+  __device__ static int offset(int j) { return 16 * j; }
+  __device__ static Chunk load(const uint8_t* b) { return ld_u4(b); }
   __device__ static void put(uint32_t* row, int j, Chunk v) {
     row[4 * j] = v.x; row[4 * j + 1] = v.y; row[4 * j + 2] = v.z; row[4 * j + 3] = v.w;
   }
@@ -692,8 +676,7 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
   // instruction's RPI rows; wavefront rows [wave RW, wave RW + RW) of the
   // R staged rows (matrix (wave RW) / 256)
   const int lrow = lane / S::kWords, j = lane - lrow * S::kWords;
-  int wshift;
-  const int woff = S::offset(j, wshift);
+  const int woff = S::offset(j);
   const bool wlane = lrow < RPI;
   const int rr0 = wave * RW;
   const uint8_t* wm = (NMAT == 2 && rr0 >= TN) ? p.w1 : p.w0;
@@ -710,7 +693,7 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
 #pragma unroll
     for (int u = 0; u < NQ; ++u) {
       const int q = part * NQ + u;
-      if (q < NI && wlane && q * RPI + lrow < RW) wv[slot][u] = S::load(b + size_t(q * RPI) * row_bytes, wshift);
+      if (q < NI && wlane && q * RPI + lrow < RW) wv[slot][u] = S::load(b + size_t(q * RPI) * row_bytes);
     }
   };
   auto store_w = [&](int buf, int part, int slot) {
