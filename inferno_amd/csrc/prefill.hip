@@ -668,6 +668,7 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
     c0 = blockIdx.y * TM;
     c1 = min(c0 + uint32_t(TM), p.rows);
   }
+  if (c1 <= c0) return;  // uniform: no rows (the epilogue's clamped reads need one)
   const int n0 = blockIdx.x * TN;
   const int K = p.K;
   const size_t row_bytes = size_t(K / kUnit) * F::kBytes;
@@ -840,7 +841,17 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
   }
 
   // accumulator element v of lane (i, kg): weight row 8 (v / 4) + 4 kg + v % 4
-  // of this wavefront's 32, token column i of the 32-token block
+  // of this wavefront's 32, token column i of the 32-token block. The
+  // assignment of each of the lane's token columns is loaded here, for every
+  // token block at once and from a clamped index (a load under the bound
+  // check would be waited for at the check's join), so it is in flight
+  // through the exchange below; the routing weights follow in one round trip.
+  uint32_t asg[NBW];
+#pragma unroll
+  for (int tb = 0; tb < NBW; ++tb) {
+    const uint32_t c = min(c0 + uint32_t((wt * NBW + tb) * 32 + i), c1 - 1);
+    asg[tb] = p.sorted ? p.sorted[c] : c;
+  }
   if constexpr (SPL) {
     // the up wavefronts' sums to the gate wavefronts, through the LDS of
     // the token and weight buffers (no wavefront reads them after this
@@ -860,16 +871,19 @@ __global__ void __launch_bounds__(64 * (SPL ? 2 * WR : WR * WT))
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc1[tb][v] = xch[((wr * NBW + tb) * 16 + v) * 64 + lane];
   }
+  float wts[NBW];
+#pragma unroll
+  for (int tb = 0; tb < NBW; ++tb) wts[tb] = (NMAT == 2 && p.route_w) ? p.route_w[asg[tb]] : 1.0f;
 #pragma unroll
   for (int tb = 0; tb < NBW; ++tb) {
     const uint32_t c = c0 + uint32_t((wt * NBW + tb) * 32 + i);
     if (c >= c1) continue;
-    const uint32_t a = p.sorted ? p.sorted[c] : c;
+    const uint32_t a = asg[tb];
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const int r0 = n0 + 32 * wr + 8 * g4 + 4 * kg;
       if constexpr (NMAT == 2) {
-        const float wa = p.route_w ? p.route_w[a] : 1.0f;
+        const float wa = wts[tb];
         float h[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
