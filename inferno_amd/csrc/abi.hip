@@ -527,7 +527,7 @@ LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
                 : nullptr;
   const bool rblas = router_blas_fits(T, L->hidden, L->experts);
   s.rblas = rblas ? static_cast<void*>(c.take<unsigned char>(
-                        router_blas_workspace_bytes(L->hidden, L->experts)))
+                        router_blas_workspace_bytes(T, L->hidden, L->experts)))
                   : nullptr;
   s.blas_lib = (blas || rblas) ? static_cast<void*>(c.take<unsigned char>(
                                      blas_lib_workspace_bytes()))
@@ -669,7 +669,8 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
     d.h_quant = L->down_quant;
     return launch_decode_layer(s, d, L->quant);
   }
-  // bf16 tokens of a large batch: the logits as three library GEMMs
+  // bf16 tokens of a large batch: the logits as one library GEMM over the
+  // router's three bf16 terms
   const bool router_blas = w.rblas != nullptr && w.blas_lib != nullptr &&
                            router_blas_takes(T, H, E, x_dtype);
   const int parts = router_blas ? 1 : router_logit_parts(T, H, E, x_dtype);

@@ -18,7 +18,8 @@
 // 2 bytes per weight; the GEMMs are the library's (its algorithm picked by
 // its heuristic once per shape and kept). The router logits (reference:
 // the router linear, gguf_model.rs:742-748) take the fp32 router split
-// exactly into three bf16 terms and three bf16 GEMMs accumulated in fp32.
+// exactly into three bf16 terms, one bf16 GEMM over the three terms' rows
+// (fp32 accumulation) and an ordered sum of the three per expert.
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
@@ -35,7 +36,7 @@ namespace {
 // grouped kernels' dense path).
 constexpr size_t kBlasMinTokens = 256;
 constexpr size_t kBlasWsBytes = size_t(32) << 20;  // the library's own workspace
-// Tokens from which bf16 router logits take three library GEMMs.
+// Tokens from which bf16 router logits take the library GEMM.
 constexpr size_t kRouterBlasMinTokens = 2048;
 
 // Q8_0 [d f16 | 32 int8] blocks -> f16 rows. A 64-thread workgroup takes 64
@@ -87,8 +88,8 @@ __global__ void __launch_bounds__(kExpandThreads) q8_0_to_f16_kernel(ExpandArgs 
 // The router's fp32 weights as three bf16 terms (terms + m E H, m = 0, 1,
 // 2): truncate, subtract, truncate, subtract, truncate; the last remainder
 // has at most eight significant bits, so w = t0 + t1 + t2 exactly, and a
-// bf16 x bf16 product is exact in fp32: three bf16 GEMMs accumulated in
-// fp32 give fp32-accurate logits (the split of the router logits kernel's
+// bf16 x bf16 product is exact in fp32: the three terms' bf16 products
+// accumulated in fp32 give fp32-accurate logits (the split of the router logits kernel's
 // bf16x3 path, done once per call here).
 __global__ void __launch_bounds__(256)
     split3_kernel(const float* __restrict__ w, size_t n8, size_t n, uint16_t* __restrict__ terms) {
@@ -301,22 +302,39 @@ bool router_blas_takes(size_t T, size_t H, size_t E, int x_dtype) {
          !switch_off("INFERNO_ROUTER_BLAS") && !switch_off("INFERNO_ROUTER_BF16X3");
 }
 
-size_t router_blas_workspace_bytes(size_t H, size_t E) {
-  return (3 * E * H * 2 + 255) / 256 * 256 + 256;
+namespace {
+// The three terms' logits of T tokens [T][3E] (term-major within a token)
+// are added as (t0 + t1) + t2 per expert: the order of the three
+// accumulating GEMMs (beta 1) this single GEMM replaces.
+__global__ void __launch_bounds__(256)
+    sum3_kernel(const float* __restrict__ d3, size_t T, uint32_t E, float* __restrict__ logits) {
+  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= T * E) return;
+  const size_t t = i / E, e = i - t * E;
+  const float* r = d3 + t * 3 * E + e;
+  logits[i] = (r[0] + r[E]) + r[2 * E];
+}
+}  // namespace
+
+size_t router_blas_workspace_bytes(size_t T, size_t H, size_t E) {
+  return (3 * E * H * 2 + 255) / 256 * 256 + (T * 3 * E * 4 + 255) / 256 * 256 + 256;
 }
 
 int launch_router_blas(hipStream_t s, const uint16_t* x, const float* w, size_t T, size_t H,
                        size_t E, float* logits, void* terms_ws, void* lib_ws) {
   uint16_t* terms = reinterpret_cast<uint16_t*>((reinterpret_cast<uintptr_t>(terms_ws) + 255) /
                                                 256 * 256);
+  float* d3 = reinterpret_cast<float*>(terms + (3 * E * H + 127) / 128 * 128);
   const size_t n8 = E * H / 8;
   split3_kernel<<<unsigned((n8 + 255) / 256), 256, 0, s>>>(w, n8, E * H, terms);
   INF_LAUNCHED();
-  int st;
-  for (int m = 0; m < 3; ++m)
-    if ((st = blas_gemm(s, terms + size_t(m) * E * H, x, logits, int(E), int(T), int(H), lib_ws,
-                        HIP_R_16BF, m == 0 ? 0.0f : 1.0f)))
-      return st;
+  // the three terms [3][E][H] are one [3E][H] operand: one GEMM of 3E
+  // columns fills the chip better than three of E (c5: 256 columns made
+  // 256 tiles of 64 x 64, one workgroup per CU)
+  if (int st = blas_gemm(s, terms, x, d3, int(3 * E), int(T), int(H), lib_ws, HIP_R_16BF, 0.0f))
+    return st;
+  sum3_kernel<<<unsigned((T * E + 255) / 256), 256, 0, s>>>(d3, T, uint32_t(E), logits);
+  INF_LAUNCHED();
   return INFERNO_OK;
 }
 

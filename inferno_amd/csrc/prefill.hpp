@@ -68,7 +68,7 @@ size_t blas_lib_workspace_bytes();
 // three-term split of the fp32 router (fp32 accumulation): logits [T][E].
 bool router_blas_fits(size_t T, size_t H, size_t E);
 bool router_blas_takes(size_t T, size_t H, size_t E, int x_dtype);
-size_t router_blas_workspace_bytes(size_t H, size_t E);
+size_t router_blas_workspace_bytes(size_t T, size_t H, size_t E);
 int launch_router_blas(hipStream_t s, const uint16_t* x, const float* w, size_t T, size_t H,
                        size_t E, float* logits, void* terms_ws, void* lib_ws);
 int launch_prefill_dense(hipStream_t s, int quant, int down_quant, const void* gate,
