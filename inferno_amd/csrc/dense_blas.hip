@@ -36,8 +36,9 @@ namespace {
 // grouped kernels' dense path).
 constexpr size_t kBlasMinTokens = 256;
 constexpr size_t kBlasWsBytes = size_t(32) << 20;  // the library's own workspace
-// Tokens from which bf16 router logits take the library GEMM.
-constexpr size_t kRouterBlasMinTokens = 2048;
+// Tokens from which bf16 router logits take the library GEMM (c3's 512:
+// 1.777-1.779 against 1.785-1.795 ms on the K-chunk kernel).
+constexpr size_t kRouterBlasMinTokens = 512;
 
 // Q8_0 [d f16 | 32 int8] blocks -> f16 rows. A 64-thread workgroup takes 64
 // consecutive 272-byte units (eight blocks, 256 values; 16-byte aligned)

@@ -964,11 +964,12 @@ def test_layer_decode_shared_expert_alone(cuda, switches, sel):
     _layer_parity(cuda, cfg, 1, variants=4, tol=1e-3)
 
 
-@pytest.mark.parametrize("key,T", [("c3", 2048), ("c5", 4096)])
+@pytest.mark.parametrize("key,T", [("c3", 512), ("c3", 2048), ("c5", 4096)])
 def test_layer_prefill_router_blas(cuda, switches, key, T):
-    """bf16 tokens of a large batch: router logits as three bf16 library
-    GEMMs over the exact three-term split of the fp32 router (fp32
-    accumulation), against the matrix-core logits kernel
+    """bf16 tokens of a large batch (512 and up): router logits as one bf16
+    library GEMM over the exact three-term split of the fp32 router (fp32
+    accumulation; the three terms' results added in order), against the
+    matrix-core logits kernel
     (INFERNO_ROUTER_BLAS=0): the selected ids agree except on near-ties of
     the fp64 scores (gap below 1e-5 of the k-th score), the routing weights
     within 1e-5, and the layer agrees with the oracle."""
