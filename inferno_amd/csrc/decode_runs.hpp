@@ -731,7 +731,7 @@ __global__ void __launch_bounds__(64 * WV) gate_up_runs_multi_kernel(DecodeArgs 
       __builtin_amdgcn_s_setprio(3);
       float lg[4], bs[4];
       load_logits1(p, lg, bs);
-      topk1_wave(lg, bs, p.E, k, p.score_fn, p.norm, p.scale, tk);
+      topk1_wave_narrow(lg, bs, p.E, k, p.score_fn, p.norm, p.scale, tk);
       if (lane < k) {  // slot j = j-th smallest id, assignment = its rank
         const uint32_t rank = tk->rank[lane];
         sel_e[lane] = tk->id[lane];

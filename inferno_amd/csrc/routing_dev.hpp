@@ -195,10 +195,12 @@ struct Top1Lds {
 // pairs. On return (after a wave barrier) s holds the winners in id order
 // with their ranks, and ids and weights in rank order; weights are
 // renormalised by the rank-order sum of the scores (as topk_row_wave).
-__device__ __forceinline__ void topk1_wave(const float (&lgin)[4], const float (&bs)[4], int E,
-                                           int k, int score_fn, int norm, float scale,
-                                           Top1Lds* __restrict__ s) {
-  constexpr int PER = kMaxExperts / kWave;
+// PER: the slots lg[j], j < PER, that can hold an expert (E <= 64 PER).
+template <int PER>
+__device__ __forceinline__ void topk1_wave_p(const float (&lgin)[4], const float (&bs)[4], int E,
+                                             int k, int score_fn, int norm, float scale,
+                                             Top1Lds* __restrict__ s) {
+  static_assert(PER >= 1 && PER * kWave <= kMaxExperts, "slots per lane");
   const int lane = threadIdx.x & 63;
   float score[PER];
   uint32_t key[PER];
@@ -307,6 +309,25 @@ __device__ __forceinline__ void topk1_wave(const float (&lgin)[4], const float (
     s->w[lane] = wv * scale;
   }
   __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ void topk1_wave(const float (&lgin)[4], const float (&bs)[4], int E,
+                                           int k, int score_fn, int norm, float scale,
+                                           Top1Lds* __restrict__ s) {
+  topk1_wave_p<kMaxExperts / kWave>(lgin, bs, E, k, score_fn, norm, scale, s);
+}
+
+// The same with one slot per lane when the router has at most 64 experts
+// (one ballot per search step instead of four: c1 20.0 -> 19.0 us per
+// token). Only the run kernels' prologue takes it: in the fp8 x fp4
+// gate/up kernel the second instantiation cost c2 +1.2 us.
+__device__ __forceinline__ void topk1_wave_narrow(const float (&lgin)[4], const float (&bs)[4],
+                                                  int E, int k, int score_fn, int norm,
+                                                  float scale, Top1Lds* __restrict__ s) {
+  if (E <= kWave)
+    topk1_wave_p<1>(lgin, bs, E, k, score_fn, norm, scale, s);
+  else
+    topk1_wave_p<kMaxExperts / kWave>(lgin, bs, E, k, score_fn, norm, scale, s);
 }
 
 constexpr int kDispatchThreads = 1024;
