@@ -44,13 +44,15 @@ __device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
 // and the selected k are ranked against each other. Lanes 0..k-1 store the
 // results at their ranks; every lane also gets the selected ids in rank
 // order in `sel_id` (wave-uniform).
-__device__ __forceinline__ void topk_row_wave(const float* row, const float* __restrict__ bias,
-                                              int E, int k, int score_fn, int norm, float scale,
-                                              int t, uint32_t* __restrict__ ids,
-                                              float* __restrict__ weights,
-                                              uint32_t* __restrict__ token_idx,
-                                              uint32_t (&sel_id)[kMaxTopK]) {
-  constexpr int PER = kMaxExperts / kWave;  // 4 candidates per lane
+// PER: candidates per lane (E <= 64 PER).
+template <int PER>
+__device__ __forceinline__ void topk_row_wave_p(const float* row, const float* __restrict__ bias,
+                                                int E, int k, int score_fn, int norm, float scale,
+                                                int t, uint32_t* __restrict__ ids,
+                                                float* __restrict__ weights,
+                                                uint32_t* __restrict__ token_idx,
+                                                uint32_t (&sel_id)[kMaxTopK]) {
+  static_assert(PER >= 1 && PER * kWave <= kMaxExperts, "candidates per lane");
   const int lane = threadIdx.x & 63;
   float lg[PER], score[PER];
   uint32_t key[PER];
@@ -171,6 +173,21 @@ __device__ __forceinline__ void topk_row_wave(const float* row, const float* __r
     weights[a] = wv * scale;
     if (token_idx) token_idx[a] = uint32_t(t);
   }
+}
+
+// One candidate per lane for routers of at most 64 experts (one ballot per
+// search step instead of four), else four.
+__device__ __forceinline__ void topk_row_wave(const float* row, const float* __restrict__ bias,
+                                              int E, int k, int score_fn, int norm, float scale,
+                                              int t, uint32_t* __restrict__ ids,
+                                              float* __restrict__ weights,
+                                              uint32_t* __restrict__ token_idx,
+                                              uint32_t (&sel_id)[kMaxTopK]) {
+  if (E <= kWave)
+    topk_row_wave_p<1>(row, bias, E, k, score_fn, norm, scale, t, ids, weights, token_idx, sel_id);
+  else
+    topk_row_wave_p<kMaxExperts / kWave>(row, bias, E, k, score_fn, norm, scale, t, ids, weights,
+                                         token_idx, sel_id);
 }
 
 
