@@ -621,10 +621,11 @@ bool mfma_gate_up_covers(const DecodeArgs& a, int quant) {
          device_cus() > 0;
 }
 
-template <int Q, int NB, bool SEL>
-int launch_gate_up_mfma_nb(hipStream_t s, const DecodeArgs& a, int ntiles) {
+template <int Q, int NB, int SP>
+int launch_gate_up_mfma_sp(hipStream_t s, const DecodeArgs& a, int ntiles) {
+  constexpr bool SEL = SP > 0;
   static bool attr = false;
-  auto* kern = mfma_decode::gate_up_fp4_kernel<Q, NB, SEL>;
+  auto* kern = mfma_decode::gate_up_fp4_kernel<Q, NB, SEL, SEL ? SP : 4>;
   if (!attr) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                             160 * 1024) != hipSuccess) {
@@ -637,6 +638,16 @@ int launch_gate_up_mfma_nb(hipStream_t s, const DecodeArgs& a, int ntiles) {
   kern<<<grid, mfma_decode::kThreads, mfma_decode::lds_bytes(a.H, Q, SEL, (a.Is && a.ys) ? a.Is : 0), s>>>(a, ntiles);
   INF_LAUNCHED();
   return INFERNO_OK;
+}
+
+template <int Q, int NB, bool SEL>
+int launch_gate_up_mfma_nb(hipStream_t s, const DecodeArgs& a, int ntiles) {
+  // H = 4096 (the Laguna-S width) also has an instance whose selection
+  // takes routers of at most 128 experts with two slots per lane
+  if constexpr (SEL && NB == 16) {
+    if (a.E <= 2 * kWave) return launch_gate_up_mfma_sp<Q, NB, 2>(s, a, ntiles);
+  }
+  return launch_gate_up_mfma_sp<Q, NB, SEL ? 4 : 0>(s, a, ntiles);
 }
 
 template <int Q, bool SEL>

@@ -275,7 +275,9 @@ __host__ __device__ constexpr Fp4Lds fp4_lds_layout(int H, int quant, bool sel, 
 // w), whose dot products run while the first routed tile's loads are in
 // flight. The selection is the select launch's (same function), so the
 // result does not depend on which launch ran it.
-template <int Q, int NB, bool SEL>
+// SP: the selection's router slots per lane (SEL; 4 covers 256 experts, 2
+// covers 128 with half the ballots per search step).
+template <int Q, int NB, bool SEL, int SP = 4>
 __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int ntiles) {
   extern __shared__ uint32_t smem[];
   constexpr int kB = fp4_block_bytes(Q);
@@ -322,7 +324,7 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
       __builtin_amdgcn_s_setprio(3);
       float lg[4], bs[4];
       load_logits1(p, lg, bs);
-      topk1_wave(lg, bs, p.E, p.k, p.score_fn, p.norm, p.scale, tk);
+      topk1_wave_p<SP>(lg, bs, p.E, p.k, p.score_fn, p.norm, p.scale, tk);
       if (lane < p.k) {  // slot j = j-th smallest id, assignment = its rank
         const uint32_t rank = tk->rank[lane];
         slot_e[lane] = tk->id[lane];
