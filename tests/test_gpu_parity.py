@@ -106,6 +106,26 @@ def test_router_tie_kat(cuda):
     assert np.allclose(ph.to_np(w), [1.25, 1.25], atol=1e-6)
 
 
+@pytest.mark.parametrize("E", [8, 64, 65, 128, 256])
+def test_router_topk_tiers(cuda, E):
+    """Router top-k over widths on both sides of the one-candidate-per-lane
+    selection (E <= 64) with tied logits in three tiers and a tie-breaking
+    bias on some experts: ids (rank order) and weights as the oracle's."""
+    T, k = 6, min(8, E)
+    rng = np.random.default_rng(E)
+    tiers = np.array([-1.0, 0.0, 0.75], np.float32)
+    logits = tiers[rng.integers(0, 3, size=(T, E))].astype(np.float32)
+    bias = np.zeros(E, np.float32)
+    bias[rng.choice(E, size=max(1, E // 8), replace=False)] = 0.125
+    for score_fn in (SCORE_SIGMOID, SCORE_SOFTMAX):
+        b = bias if score_fn == SCORE_SIGMOID else None
+        ids, w, _ = ops.router_topk(dev(logits, cuda), None if b is None else dev(b, cuda), k,
+                                    score_fn, True, 1.5)
+        oid, ow = orc.router_topk(logits, b, k, score_fn, True, 1.5)
+        assert np.array_equal(ph.to_np(ids).view(np.uint32), oid), (E, score_fn)
+        np.testing.assert_allclose(ph.to_np(w), ow, rtol=2e-6, atol=0)
+
+
 def test_router_specialised_decode_case(cuda):
     # laguna_xs.rs:2269-2316 inputs; expected ids from the oracle
     E = 256
@@ -421,12 +441,15 @@ def test_layer_c2_glm_q2k_decode_full_size(cuda):
 # Exact ties in the one-token decode selection: a zero router makes every
 # logit 0, so the selection keys are the bias tiers (sigmoid) or all equal
 # (softmax, no bias); the k winners must be the oracle's (key desc, id asc),
-# in rank order, with the oracle's weights. E = 64 and 256 (four candidates
-# per lane), Q2_K (fp8 x fp4 gate/up) and Q4_K (run gate/up).
+# in rank order, with the oracle's weights. Q2_K / Q3_K take the fp8 x fp4
+# gate/up (four router slots per lane; two at H = 4096 for E <= 128), Q4_K
+# the run gate/up (one slot per lane for E <= 64, else four).
 @pytest.mark.parametrize("score_fn", [SCORE_SIGMOID, SCORE_SOFTMAX])
-@pytest.mark.parametrize("E,k,quant", [(64, 8, Q2_K), (256, 8, Q2_K), (256, 16, Q4_K)])
-def test_layer_decode_selection_ties(cuda, score_fn, E, k, quant):
-    cfg = cf.Config(f"ties_e{E}_k{k}", 90 + E // 64, 1024, E, 512, k, (quant,), score_fn, True,
+@pytest.mark.parametrize("E,k,quant,H", [(64, 8, Q2_K, 1024), (256, 8, Q2_K, 1024),
+                                         (256, 16, Q4_K, 1024), (64, 8, Q4_K, 1024),
+                                         (128, 10, Q2_K, 4096), (128, 10, Q3_K, 4096)])
+def test_layer_decode_selection_ties(cuda, score_fn, E, k, quant, H):
+    cfg = cf.Config(f"ties_e{E}_k{k}_h{H}", 90 + E // 64, H, E, 512, k, (quant,), score_fn, True,
                     2.5, 0.0, 256, torch.bfloat16, (1,))
     bias = None
     if score_fn == SCORE_SIGMOID:
