@@ -283,8 +283,12 @@ int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* layer, cons
  * cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Its scratch is a fixed device array of
  * inferno_moe_layer_noalloc_max_bytes() bytes (32 MiB) per GPU, held until
- * the process ends; shapes whose inferno_moe_layer_workspace_bytes exceeds it
- * return INFERNO_ERR_SIZE (decode up to T = 32 fits the c2 and c4 shapes).
+ * the process ends; shapes whose workspace exceeds it return INFERNO_ERR_SIZE
+ * (decode up to T = 32 fits the c2 and c4 shapes). It runs no library GEMM
+ * (hipBLASLt allocates): the shared expert and the router logits stay on the
+ * grouped kernels, so its outputs can differ in the last bits from
+ * inferno_moe_layer_forward's on batches where that call takes them (bitwise
+ * equal with INFERNO_SHARED_BLAS=0 up to 511 tokens).
  * Every call on one GPU uses that GPU's one array: calls that overlap on a GPU
  * (several streams or threads) race and must be serialised by the caller.
  * Nothing in the scratch needs to start at zero; it keeps the last call's

@@ -500,7 +500,9 @@ struct LayerScratch {
   void* rblas;    // the router's bf16 terms for the library GEMMs (large batches), or null
   void* blas_lib; // the library's workspace when either runs, or null
 };
-LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
+// lib: the library GEMMs (hipBLASLt) may run (their regions are carved);
+// the no-alloc entry point passes false: the library allocates on its own.
+LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T, bool lib = true) {
   LayerScratch s;
   // router logits, or their K-chunk partials for a small bf16 batch
   s.logits = c.take<float>(T * L->experts *
@@ -520,12 +522,12 @@ LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
                                   : 1);
   const int sq = L->shared_quant ? L->shared_quant : INFERNO_Q8_0;
   const int sdq = L->shared_down_quant ? L->shared_down_quant : INFERNO_Q8_0;
-  const bool blas = L->shared_intermediate &&
+  const bool blas = lib && L->shared_intermediate &&
                     dense_blas_fits(sq, sdq, T, L->hidden, L->shared_intermediate);
   s.blas = blas ? static_cast<void*>(c.take<unsigned char>(
                       dense_blas_workspace_bytes(T, L->hidden, L->shared_intermediate)))
                 : nullptr;
-  const bool rblas = router_blas_fits(T, L->hidden, L->experts);
+  const bool rblas = lib && router_blas_fits(T, L->hidden, L->experts);
   s.rblas = rblas ? static_cast<void*>(c.take<unsigned char>(
                         router_blas_workspace_bytes(T, L->hidden, L->experts)))
                   : nullptr;
@@ -536,18 +538,24 @@ LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T) {
 }
 }  // namespace
 
-size_t inferno_moe_layer_workspace_bytes(const inferno_moe_layer* layer, size_t T) {
+namespace {
+size_t layer_workspace_bytes(const inferno_moe_layer* layer, size_t T, bool lib) {
   if (!layer) return 0;
   Carver c{nullptr};
-  carve_layer(c, layer, T);
+  carve_layer(c, layer, T, lib);
   return c.used;
+}
+}  // namespace
+
+size_t inferno_moe_layer_workspace_bytes(const inferno_moe_layer* layer, size_t T) {
+  return layer_workspace_bytes(layer, T, true);
 }
 
 namespace {
 int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x_dtype,
                   const float* residual, size_t T, float* out, uint32_t* expert_ids_out,
                   float* expert_weights_out, void* workspace, size_t workspace_bytes,
-                  const float* logits_ready);
+                  const float* logits_ready, bool lib = true);
 }  // namespace
 
 int inferno_moe_layer_forward(void* stream, const inferno_moe_layer* L, const void* x,
@@ -590,7 +598,7 @@ bool layer_takes_decode(const inferno_moe_layer* L, size_t T, int x_dtype) {
 int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x_dtype,
                   const float* residual, size_t T, float* out, uint32_t* expert_ids_out,
                   float* expert_weights_out, void* workspace, size_t workspace_bytes,
-                  const float* logits_ready) {
+                  const float* logits_ready, bool lib) {
   clear_error();
   INF_CHECK_ARG(L != nullptr, "null layer");
   const size_t H = L->hidden, E = L->experts, I = L->intermediate, k = L->top_k;
@@ -623,14 +631,14 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
   // shared expert (the GLM and Laguna S layers); other formats (Laguna XS:
   // Q4_K gate/up, Q4_K or Q6_K down) run the shared expert on the GEMV kernels
   const bool shared_q8 = Is == 0 || (sq == INFERNO_Q8_0 && sdq == INFERNO_Q8_0);
-  size_t need = inferno_moe_layer_workspace_bytes(L, T);
+  size_t need = layer_workspace_bytes(L, T, lib);
   if (workspace_bytes < need) {
     set_error("workspace too small: need " + std::to_string(need) + " bytes");
     return INFERNO_ERR_SIZE;
   }
   if (int st_ = require_device()) return st_;
   Carver c{static_cast<char*>(workspace)};
-  LayerScratch w = carve_layer(c, L, T);
+  LayerScratch w = carve_layer(c, L, T, lib);
   hipStream_t s = as_stream(stream);
   uint32_t* ids = expert_ids_out ? expert_ids_out : w.ids;
   float* wts = expert_weights_out ? expert_weights_out : w.weights;
@@ -784,7 +792,9 @@ int inferno_moe_layer_forward_noalloc(void* stream, const inferno_moe_layer* L, 
                                       uint32_t* expert_ids_out, float* expert_weights_out) {
   clear_error();
   INF_CHECK_ARG(L != nullptr, "null layer");
-  const size_t need = inferno_moe_layer_workspace_bytes(L, T);
+  // no library GEMMs here (hipBLASLt allocates): the shared expert and the
+  // router stay on the grouped kernels
+  const size_t need = layer_workspace_bytes(L, T, false);
   if (need > kNoAllocScratchBytes) {
     set_error("no-alloc layer: these shapes need " + std::to_string(need) +
               " bytes of scratch, above the fixed maximum of " +
@@ -796,8 +806,8 @@ int inferno_moe_layer_forward_noalloc(void* stream, const inferno_moe_layer* L, 
   void* ws = nullptr;
   int st = scratch_ptr(&ws);
   if (st) return st;
-  return inferno_moe_layer_forward(stream, L, x, x_dtype, residual, T, out, expert_ids_out,
-                                   expert_weights_out, ws, kNoAllocScratchBytes);
+  return layer_forward(stream, L, x, x_dtype, residual, T, out, expert_ids_out,
+                       expert_weights_out, ws, kNoAllocScratchBytes, nullptr, false);
 }
 
 // ------------------------------------------------------------- stack

@@ -1023,11 +1023,12 @@ def test_layer_prefill_router_blas(cuda, switches, key, T):
 
 
 @pytest.mark.parametrize("blas", ["1", "0"])
-@pytest.mark.parametrize("key,T", [("c3", 512), ("c4", 300), ("e128_fp32", 300)])
+@pytest.mark.parametrize("key,T", [("c3", 512), ("c4", 300), ("e128_fp32", 300), ("c4", 32),
+                                   ("c2", 12)])
 def test_layer_prefill_shared_expert_alone(cuda, switches, blas, key, T):
     """The Q8_0 shared expert of a grouped-GEMM batch alone (routing scale
-    0): on the library GEMMs (default from 256 tokens: the blocks expanded
-    to f16, fp32 accumulation, h in f16) or on the grouped kernels' dense
+    0): on the library GEMMs (default: the blocks expanded to f16, fp32
+    accumulation, h in f16) or on the grouped kernels' dense
     path (INFERNO_SHARED_BLAS=0); every 4th token against the oracle. Both
     round x and h to f16 as the reference prefill does: bound 2e-3."""
     switches(INFERNO_SHARED_BLAS=blas)

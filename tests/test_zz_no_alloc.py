@@ -1,7 +1,10 @@
 """The no-allocation layer entry point (inferno_moe_layer_forward_noalloc,
 fixed device scratch) against inferno_moe_layer_forward with a caller
 workspace: bit-identical outputs and routing, on two calls in a row, the
-second with fewer tokens (the scratch keeps the first call's contents)."""
+second with fewer tokens (the scratch keeps the first call's contents).
+The no-alloc entry point keeps the shared expert and the router on the
+grouped kernels (the library GEMMs allocate), so the workspace entry point
+is run with INFERNO_SHARED_BLAS=0 for the bitwise comparison."""
 import pytest
 import torch
 
@@ -13,7 +16,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("name,T1,T2", [("c2", 16, 1), ("c4", 32, 1), ("c1", 16, 3)])
-def test_noalloc_matches_workspace_entry_point(cuda, name, T1, T2):
+def test_noalloc_matches_workspace_entry_point(cuda, monkeypatch, name, T1, T2):
+    monkeypatch.setenv("INFERNO_SHARED_BLAS", "0")
     cfg = cf.CONFIGS[name]
     lt = cf.build_layer(cfg, 0, cuda, max_tokens=T1)
     k = cfg.top_k
