@@ -166,7 +166,8 @@ def main():
     finally:
         ops.kernel_timing(False)
     launches = reps * n_sub
-    # the library takes the grouped-GEMM path from 96 assignments on (several
+    # the library takes the grouped-GEMM path from 66 assignments on (48 without
+    # a shared expert; several
     # tokens per expert), the fused decode launches below; the label says which
     prefill = labels[ops.TIMER_GATE_UP].startswith("prefill")
     if prefill:

@@ -113,8 +113,12 @@ int validate_moe(int quant, int down_quant, size_t gate_bytes, size_t up_bytes,
 // Routed part shared by inferno_gguf_moe and the layer: dispatch, gate/up,
 // down. Leaves per-assignment down rows (already routing-weighted) in m.y.
 // Many assignments take the MFMA grouped GEMM; few take the packed-f16 GEMV.
-bool use_mfma(int quant, int down_quant, size_t T, size_t k, size_t E, size_t H, size_t I) {
-  return T * k >= env_size("INFERNO_PREFILL_MIN_ASSIGNMENTS", kPrefillMinAssignments) &&
+// Is: the layer's shared expert width (0: none); with one, the decode
+// launches keep more assignments (they run the shared expert inside them).
+bool use_mfma(int quant, int down_quant, size_t T, size_t k, size_t E, size_t H, size_t I,
+              size_t Is = 0) {
+  const size_t from = Is ? kPrefillMinAssignmentsShared : kPrefillMinAssignments;
+  return T * k >= env_size("INFERNO_PREFILL_MIN_ASSIGNMENTS", from) &&
          prefill_routed_supported(quant, down_quant, H, I, E);
 }
 
@@ -124,10 +128,9 @@ bool use_mfma(int quant, int down_quant, size_t T, size_t k, size_t E, size_t H,
 int run_routed(hipStream_t s, int quant, int down_quant, const void* gate, const void* up,
                const void* down, const void* x, int x_dtype, const uint32_t* ids,
                const float* w, size_t T, size_t k, size_t E, size_t H, size_t I,
-               const MoeScratch& m, bool x_staged, const uint16_t* x16 = nullptr,
+               const MoeScratch& m, bool x_staged, bool mfma, const uint16_t* x16 = nullptr,
                bool distinct_ids = false) {
   int st;
-  const bool mfma = use_mfma(quant, down_quant, T, k, E, H, I);
   // on the MFMA path the dispatch also writes the GEMM's tile lists
   const PlanOut plan = mfma ? prefill_plan_out(m.plan, T * k, E) : PlanOut{};
   if ((st = launch_dispatch(s, ids, T, k, E, m.offsets, m.sorted, m.active, mfma ? &plan : nullptr)))
@@ -315,7 +318,8 @@ int inferno_gguf_moe(void* stream, int quant, int down_quant, const void* gate,
   MoeScratch m = carve_moe(c, T, k, E, H, I);
   hipStream_t s = as_stream(stream);
   if ((st = run_routed(s, quant, down_quant, gate, up, down, x, x_dtype, expert_ids,
-                       expert_weights, T, k, E, H, I, m, false)))
+                       expert_weights, T, k, E, H, I, m, false,
+                       use_mfma(quant, down_quant, T, k, E, H, I))))
     return st;
   return launch_topk_combine(s, nullptr, nullptr, m.y, nullptr, T, H, k, out);
 }
@@ -590,7 +594,7 @@ bool layer_takes_decode(const inferno_moe_layer* L, size_t T, int x_dtype) {
                           L->quant, L->down_quant) &&
          shared_q8 &&
          (T == 1 || !use_mfma(L->quant, L->down_quant, T, L->top_k, L->experts, L->hidden,
-                              L->intermediate));
+                              L->intermediate, Is));
 }
 
 // logits_ready: the tokens' router logits [T, E], already formed (the
@@ -642,10 +646,9 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
   hipStream_t s = as_stream(stream);
   uint32_t* ids = expert_ids_out ? expert_ids_out : w.ids;
   float* wts = expert_weights_out ? expert_weights_out : w.weights;
-  // the fused decode path below kPrefillMinAssignments assignments (and for
-  // one token); from there the grouped MFMA GEMM reads each expert's weights
-  // once for all its tokens (c2 at T = 16: 0.55 ms against 0.62 ms; c4 at
-  // T = 32: 2.0 ms against 3.9 ms)
+  // the fused decode path below the grouped GEMM's assignment threshold
+  // (use_mfma; and for one token); from there the grouped MFMA GEMM reads
+  // each expert's weights once for all its tokens
   const bool decode = layer_takes_decode(L, T, x_dtype);
   if (logits_ready && !decode) {
     set_error("precomputed logits need the decode path");
@@ -682,7 +685,7 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
   const bool router_blas = w.rblas != nullptr && w.blas_lib != nullptr &&
                            router_blas_takes(T, H, E, x_dtype);
   const int parts = router_blas ? 1 : router_logit_parts(T, H, E, x_dtype);
-  const bool mfma_path = use_mfma(L->quant, L->down_quant, T, k, E, H, I);
+  const bool mfma_path = use_mfma(L->quant, L->down_quant, T, k, E, H, I, Is);
   // the shared expert on the dense MFMA GEMMs when its formats have them
   // (Q8_0; the Laguna XS Q4_K gate/up with Q4_K or Q6_K down), else on the
   // GEMV kernels
@@ -726,7 +729,7 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
     // x in f16 once for the routed and the shared expert GEMMs
     if (!x16_by_router && (st = launch_to_f16(s, x, x_dtype, T, H, x16))) return st;
     if ((st = run_routed(s, L->quant, L->down_quant, L->gate, L->up, L->down, x, x_dtype, ids,
-                         wts, T, k, E, H, I, w.moe, false, x16, true)))
+                         wts, T, k, E, H, I, w.moe, false, true, x16, true)))
       return st;
     if (Is && !shared_gemm) return shared_down_gemv();
     if (shared_gemm &&
@@ -739,7 +742,7 @@ int layer_forward(void* stream, const inferno_moe_layer* L, const void* x, int x
   // x is staged once for the routed and the shared gate/up
   if ((st = launch_stage(s, x, x_dtype, T, H, w.moe.stage_x))) return st;
   if ((st = run_routed(s, L->quant, L->down_quant, L->gate, L->up, L->down, x, x_dtype, ids, wts,
-                       T, k, E, H, I, w.moe, true)))
+                       T, k, E, H, I, w.moe, true, mfma_path)))
     return st;
   if (Is) {
     if ((st = shared_gate_up_gemv(true))) return st;

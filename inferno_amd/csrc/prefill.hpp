@@ -9,9 +9,15 @@ bool prefill_supported(int quant);
 // True when the routed layer (gate/up kind, down kind, shapes) has the MFMA path.
 bool prefill_routed_supported(int quant, int down_quant, size_t H, size_t I, size_t E);
 // Assignments from which the routed layer takes the MFMA path (measured
-// crossover against the several-token decode kernels: 96 to 128 assignments
-// for the c1, c2 and c4 layers; INFERNO_PREFILL_MIN_ASSIGNMENTS overrides).
-constexpr size_t kPrefillMinAssignments = 96;
+// crossovers against the several-token decode kernels, with the shared
+// expert of the MFMA path on the library GEMMs; INFERNO_PREFILL_MIN_ASSIGNMENTS
+// overrides both). Without a shared expert (c1): 32 assignments 55.7 against
+// 63.2 us on the decode kernels, 48 70.9 against 67.2, 64 82.5 against
+// 71.5. With one (c2, c4): 48-56 decode (c2 T = 6 0.262 against 0.313 ms),
+// 64 even (c2 T = 8 0.335 against 0.338), 70 and up MFMA (c4 T = 7 1.030
+// against 1.015, T = 8 1.151 against 1.050, c2 T = 10 0.408 against 0.378).
+constexpr size_t kPrefillMinAssignments = 48;
+constexpr size_t kPrefillMinAssignmentsShared = 66;
 
 // 32-bit words of the routed planner's scratch (tile lists and counts).
 size_t prefill_plan_words(size_t A, size_t E);

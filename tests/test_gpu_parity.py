@@ -204,7 +204,7 @@ def _skewed_ids(T, E, k, hot=(0, 1), share=(1.0, 0.8)):
                                                  (96, 768, 512, 8, 4, False, True),
                                                  (40, 512, 256, 8, 4, True, "dup")])
 def test_gguf_moe_mfma_prefill(cuda, quant, down, T, H, I, E, k, bf16, skew):
-    # T * k >= 96 assignments: the MFMA grouped GEMM (f16 operands, fp32
+    # T * k >= 48 assignments: the MFMA grouped GEMM (f16 operands, fp32
     # accumulation). The skewed case gives two experts >= 64 rows (128-row
     # tiles) next to small experts (32-row tiles). "dup": caller ids that
     # name expert 0 twice in every token (the entry point takes any ids),
@@ -425,6 +425,13 @@ def test_layer_prefill_shared_ragged_tiles(cuda, T):
     cfg = cf.Config("shared_ragged", 9, 1024, 16, 512, 2, (Q2_K,), SCORE_SIGMOID, True, 1.0, 0.1,
                     512, torch.bfloat16, (T,))
     _layer_parity(cuda, cfg, T, tokens=np.r_[0:24, T - 48:T])
+
+
+@pytest.mark.parametrize("key,T", [("c2", 4), ("c2", 8), ("c4", 6)])
+def test_layer_decode_several_tokens_shared(cuda, key, T):
+    # below the grouped GEMM's 66 assignments with a Q8_0 shared expert: the
+    # several-token decode launches (select, packed-f16 tiles), full size
+    _layer_parity(cuda, key, T)
 
 
 @pytest.mark.parametrize("T", [1, 16])
@@ -915,7 +922,7 @@ def test_layer_prefill_router_x16_variant(cuda, switches, key, T):
 # grouped GEMM, ~4 rows per expert), Q2_K with a Q8_0 shared expert, bf16
 # and fp32 tokens, against the oracle.
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("T", [1, 5, 64])
+@pytest.mark.parametrize("T", [1, 4, 64])
 def test_layer_router_caps(cuda, T, dt):
     cfg = cf.Config(f"caps_e256_k16_t{T}", 95, 512, 256, 256, 16, (Q2_K,), cf.SCORE_SIGMOID, True,
                     2.5, 0.1, 256, dt, (T,))
