@@ -526,7 +526,9 @@ LayerScratch carve_layer(Carver& c, const inferno_moe_layer* L, size_t T, bool l
                                   : 1);
   const int sq = L->shared_quant ? L->shared_quant : INFERNO_Q8_0;
   const int sdq = L->shared_down_quant ? L->shared_down_quant : INFERNO_Q8_0;
-  const bool blas = lib && L->shared_intermediate &&
+  // (only batches that can take the grouped GEMMs: a decode call carries no
+  // f16 copy of the shared expert)
+  const bool blas = lib && L->shared_intermediate && T * L->top_k >= kPrefillMinAssignments &&
                     dense_blas_fits(sq, sdq, T, L->hidden, L->shared_intermediate);
   s.blas = blas ? static_cast<void*>(c.take<unsigned char>(
                       dense_blas_workspace_bytes(T, L->hidden, L->shared_intermediate)))
