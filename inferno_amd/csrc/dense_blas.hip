@@ -43,39 +43,48 @@ constexpr size_t kBlasWsBytes = size_t(32) << 20;  // the library's own workspac
 // 1.777-1.779 against 1.785-1.795 ms on the K-chunk kernel).
 constexpr size_t kRouterBlasMinTokens = 512;
 
-// Q8_0 [d f16 | 32 int8] blocks -> f16 rows. A 64-thread workgroup takes 64
-// consecutive 272-byte units (eight blocks, 256 values; 16-byte aligned)
+// Q8_0 [d f16 | 32 int8] blocks -> f16 rows. A 256-thread workgroup takes
+// 64 consecutive 272-byte units (eight blocks, 256 values; 16-byte aligned)
 // of one matrix: the units are read into LDS with contiguous 16-byte loads,
-// then every output chunk of eight values (one uint4) is formed from LDS by
-// one thread, so that the stores are contiguous too. permute: k order
-// 0 2 1 3 4 6 5 7 inside every eight. The three matrices (gate, up:
-// permuted; down: plain) in one launch.
+// all issued before the first LDS store (a load-store loop waited for each
+// load in turn: c4 T = 32 29 us per layer), then every output chunk of eight
+// values (one uint4) is formed from LDS by one thread, so that the stores are
+// contiguous too. permute: k order 0 2 1 3 4 6 5 7 inside every eight. The
+// three matrices (gate, up: permuted; down: plain) in one launch.
 struct ExpandArgs {
   const uint8_t* src[3];
   uint16_t* dst[3];
-  size_t groups[3];  // 64-unit groups of each matrix (the last may be partial)
+  size_t groups[3];  // kExpandUnits-unit groups of each matrix (the last may be partial)
   size_t units[3];   // 256-value units of each matrix
   int permute[3];
 };
-constexpr int kExpandThreads = 64;
+constexpr int kExpandThreads = 256;
+constexpr int kExpandUnits = 64;
 constexpr int kUnitBytes = 272;
+constexpr int kExpandLoads = (kExpandUnits * kUnitBytes / 16 + kExpandThreads - 1) / kExpandThreads;
 __global__ void __launch_bounds__(kExpandThreads) q8_0_to_f16_kernel(ExpandArgs a) {
-  __shared__ uint4 lds[kExpandThreads * kUnitBytes / 16];
+  __shared__ uint4 lds[kExpandUnits * kUnitBytes / 16];
   size_t g = blockIdx.x;
   int m = 0;
   while (m < 3 && g >= a.groups[m]) g -= a.groups[m++];
   if (m == 3) return;  // uniform
-  const size_t u0 = g * kExpandThreads;
-  const int nu = int(min(size_t(kExpandThreads), a.units[m] - u0));
+  const int tid = threadIdx.x;
+  const size_t u0 = g * kExpandUnits;
+  const int nu = int(min(size_t(kExpandUnits), a.units[m] - u0));
   const uint4* s4 = reinterpret_cast<const uint4*>(a.src[m] + u0 * kUnitBytes);
   const int n16 = nu * kUnitBytes / 16;
-  for (int j = threadIdx.x; j < n16; j += kExpandThreads) lds[j] = s4[j];
+  uint4 v[kExpandLoads];
+#pragma unroll
+  for (int i = 0; i < kExpandLoads; ++i) v[i] = s4[min(i * kExpandThreads + tid, n16 - 1)];
+#pragma unroll
+  for (int i = 0; i < kExpandLoads; ++i)
+    if (i * kExpandThreads + tid < n16) lds[i * kExpandThreads + tid] = v[i];
   __syncthreads();
   const uint8_t* lb = reinterpret_cast<const uint8_t*>(lds);
   const bool perm = a.permute[m] != 0;
   uint4* o4 = reinterpret_cast<uint4*>(a.dst[m] + u0 * 256);
   const int nchunks = nu * 32;  // uint4 chunks of eight values
-  for (int c = threadIdx.x; c < nchunks; c += kExpandThreads) {
+  for (int c = tid; c < nchunks; c += kExpandThreads) {
     const int u = c >> 5, w = c & 31, blk = w >> 2, q8 = w & 3;
     const uint8_t* bp = lb + u * kUnitBytes + 34 * blk;
     const float d = f16_bits_to_f32(uint16_t(bp[0] | (bp[1] << 8)));
@@ -253,7 +262,7 @@ int launch_expand(hipStream_t s, const void* gate, const void* up, const void* d
   const size_t units = Is * H / 256;  // H, Is multiples of 256
   for (int m = 0; m < 3; ++m) {
     a.units[m] = units;
-    a.groups[m] = (units + kExpandThreads - 1) / kExpandThreads;
+    a.groups[m] = (units + kExpandUnits - 1) / kExpandUnits;
     a.permute[m] = m < 2 ? 1 : 0;
   }
   q8_0_to_f16_kernel<<<unsigned(3 * a.groups[0]), kExpandThreads, 0, s>>>(a);
