@@ -59,6 +59,28 @@ typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
 // same hint on the packed-f16 GEMV loads, whose 16-byte reads straddle
 // blocks and lines, cost c2 +4 and c4 +11 us)
 __device__ __forceinline__ u32x4 ld_tile(const u32x4* p) { return __builtin_nontemporal_load(p); }
+
+// Global -> LDS copy of n 16-byte words by NT threads in two steps, so that
+// a kernel can issue other loads between them: load() puts every word of
+// this thread (at most MAXIT) in flight at once (a load-store loop waits for
+// each load in turn), store() writes them; words past MAXIT * NT are copied
+// by a plain loop in store().
+template <int NT, int MAXIT>
+struct LdsCopy {
+  uint4 t[MAXIT];
+  __device__ __forceinline__ void load(const uint4* src, int n) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < MAXIT; ++i) t[i] = src[min(i * NT + tid, n - 1)];
+  }
+  __device__ __forceinline__ void store(uint4* dst, const uint4* src, int n) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < MAXIT; ++i)
+      if (i * NT + tid < n) dst[i * NT + tid] = t[i];
+    for (int j = MAXIT * NT + tid; j < n; j += NT) dst[j] = src[j];
+  }
+};
 typedef uint32_t u32_a2 __attribute__((aligned(2)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 
@@ -644,9 +666,12 @@ __global__ void __launch_bounds__(kThreads) down_q2k_kernel(DecodeArgs p, int nt
   u32x4 v[PER];
   int t = blockIdx.x;
   __syncthreads();
+  // the staged h rows and the first tile in flight together
+  LdsCopy<kThreads, (kMaxDownRanks * Sh / 4 + kThreads - 1) / kThreads> hcp;
+  const uint4* hsrc = reinterpret_cast<const uint4*>(p.stage_h);
+  hcp.load(hsrc, k * Sh / 4);
   if (t < ntiles) fetch_down_tile<NB, TR, PER>(v, p, k, rank_e, t);
-  for (int i = tid; i < k * Sh / 4; i += kThreads)
-    reinterpret_cast<uint4*>(hs)[i] = reinterpret_cast<const uint4*>(p.stage_h)[i];
+  hcp.store(reinterpret_cast<uint4*>(hs), hsrc, k * Sh / 4);
   if (tid < 4) zero[tid] = 0;
   const bool act = q == 2 * (n >> 3) + (n & 1);
   const int pm = (n >> 1) & 3;
