@@ -245,10 +245,14 @@ __device__ __forceinline__ void split3(const float4& a, const float4& b, u32x4v 
 // chunk a multiple of 2 KS of them): chunk z writes its partial logits to
 // logits + z T E, summed in chunk order by the top-k kernel; a small batch
 // then spreads over enough workgroups to draw on every CU.
+// x16 (non-null only for KS = 1): the f16 copy of x for the grouped GEMMs
+// (to_f16_kernel's values and k order 0 2 1 3 4 6 5 7), written by the first
+// expert group's first wavefront from the token rows it loads over its chunk.
 template <int NTB, int KS>
 __global__ void __launch_bounds__(256 * KS)
     logits_bf16x3_kernel(const uint16_t* __restrict__ x, const float* __restrict__ w, int T,
-                         int H, int E, float* __restrict__ logits) {
+                         int H, int E, float* __restrict__ logits,
+                         uint16_t* __restrict__ x16 = nullptr) {
   __shared__ float4v part[KS > 1 ? KS - 1 : 1][4][NTB][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = wave & 3, s = wave >> 2;
@@ -291,14 +295,36 @@ __global__ void __launch_bounds__(256 * KS)
                                                          __builtin_bit_cast(bf16x8, u.xv[b]),
                                                          acc[b], 0, 0, 0);
   };
+  const bool w16 = KS == 1 && x16 != nullptr && blockIdx.x == 0 && wave == 0;  // uniform
+  auto store16 = [&](const Buf& u, int kb) {
+#pragma unroll
+    for (int b = 0; b < NTB; ++b) {
+      const int t = t0 + 16 * b + r;
+      if (t >= T) continue;
+      auto f16 = [](uint32_t bf) {  // bf16 bits -> fp32 -> f16 (round to nearest even)
+        return uint32_t(__builtin_bit_cast(uint16_t, (_Float16)__builtin_bit_cast(float, bf)));
+      };
+      uint32_t h[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        h[2 * i] = f16(u.xv[b][i] << 16);
+        h[2 * i + 1] = f16(u.xv[b][i] & 0xffff0000u);
+      }
+      *reinterpret_cast<uint4*>(x16 + size_t(t) * H + kb * 32 + 8 * g) =
+          make_uint4(h[0] | (h[2] << 16), h[1] | (h[3] << 16), h[4] | (h[6] << 16),
+                     h[5] | (h[7] << 16));
+    }
+  };
   // the host launches this kernel only when 2 * KS divides the chunk's blocks
   Buf u0, u1;
   load(kz0 + s, u0);
   load(kz0 + s + KS, u1);
   for (int kb = kz0 + s; kb < nkb; kb += 2 * KS) {
     compute(u0);
+    if (w16) store16(u0, kb);
     load(kb + 2 * KS, u0);
     compute(u1);
+    if (w16) store16(u1, kb + KS);
     load(kb + 3 * KS, u1);
   }
   if constexpr (KS > 1) {
@@ -389,7 +415,7 @@ int router_logit_parts_max(size_t T, size_t H, size_t E) {
 }
 bool router_writes_x16(size_t T, size_t H, size_t E, int x_dtype, int parts) {
   (void)T; (void)E;
-  return x_dtype == INFERNO_F32 && parts > 1 && H % 32 == 0;
+  return parts > 1 && H % 32 == 0;
 }
 
 int router_logit_parts(size_t T, size_t H, size_t E, int x_dtype) {
@@ -408,7 +434,7 @@ int launch_router_logit_parts(hipStream_t s, const void* x, int x_dtype, const f
   const dim3 grid(unsigned((E + 63) / 64), unsigned((T + 15) / 16), unsigned(parts));
   if (x_dtype == INFERNO_BF16)
     logits_bf16x3_kernel<1, 1><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(x), w, int(T),
-                                                    int(H), int(E), parts_out);
+                                                    int(H), int(E), parts_out, x16);
   else  // fp32 tokens on the fp32 matrix cores, K split the same way
     logits_mfma_kernel<float, 1><<<grid, 256, 0, s>>>(static_cast<const float*>(x), w, int(T),
                                                       int(H), int(E), parts_out, x16);

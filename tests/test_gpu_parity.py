@@ -896,9 +896,10 @@ _E128_FP32 = cf.Config("q4k_h2048_e128_fp32_q8shared", 91, 2048, 128, 768, 8, (Q
                        cf.SCORE_SIGMOID, True, 2.5, 0.1, 1024, torch.float32, (24,))
 
 
-@pytest.mark.parametrize("key,T", [("c1", 16), ("xs", 64), ("c1", 300), (_E128_FP32, 24)])
+@pytest.mark.parametrize("key,T", [("c1", 16), ("xs", 64), ("c1", 300), (_E128_FP32, 24),
+                                   ("c2", 16), ("c4", 32)])
 def test_layer_prefill_router_x16_variant(cuda, switches, key, T):
-    """fp32 tokens on the grouped GEMMs with the router logits over K chunks:
+    """fp32 and bf16 tokens on the grouped GEMMs with the router logits over K chunks:
     the logits launch also writes x in f16 for the GEMMs (no conversion
     launch); INFERNO_ROUTER_X16=0 keeps the conversion launch. Same f16
     rounding of the same values: outputs bit-identical; the default agrees
