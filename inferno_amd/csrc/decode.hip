@@ -780,7 +780,13 @@ int launch_decode_shared_slot(hipStream_t s, DecodeArgs a, int quant) {
   a.xr_quant = quant;
   a.h_mfma = 1;
   a.ys = nullptr;
+  // the down launch's first tiles (k + 1 ranks), warmed in L2 by the
+  // selecting gate/up launch under its last tile (INFERNO_DECODE_WARM_DOWN=0: off)
   a.dpf_rows = a.dpf_row_bytes = 0;
+  if (!switch_off("INFERNO_DECODE_WARM_DOWN")) {
+    a.dpf_rows = runs_down_tile_rows(a.h_quant, a.H, a.I, a.k + 1);
+    a.dpf_row_bytes = runs_down_row_bytes(a.h_quant, a.I);
+  }
   a.max_slots = a.k;
   if (int st = launch_route(s, a, 0)) return st;
   int st = timed(s, kTimerGateUp,

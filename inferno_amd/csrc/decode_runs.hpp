@@ -789,6 +789,25 @@ __global__ void __launch_bounds__(64 * WV) gate_up_runs_multi_kernel(DecodeArgs 
   };
   fetch(t);
   if (tid < 4) zero[tid] = 0;
+  // SEL: the down launch's workgroup of this index (on the same XCD) starts
+  // with its tile blockIdx.x. Under this workgroup's last tile, its tile
+  // registers v (free from then on) load the k (+ shared) ranks' rows of
+  // that down tile, as far as kWarmPer chunks per thread reach; the data is
+  // not used, the loads leave the rows in this XCD's L2. Ordinary loads the
+  // compiler counts: nothing waits for them until the sink at the end.
+  constexpr int kWarmPer = SEL ? (PER < 4 ? PER : 4) : 0;
+  auto warm_down = [&]() {
+    if (!p.dpf_rows || int(blockIdx.x) >= p.H / p.dpf_rows) return;  // uniform
+    const size_t tb = size_t(p.dpf_rows) * size_t(p.dpf_row_bytes);
+    const int cr = int(tb / 16), nc = (k + p.shared_slot) * cr;
+#pragma unroll
+    for (int j = 0; j < kWarmPer; ++j) {
+      const int i = min(j * (64 * WV) + tid, nc - 1), r = i / cr, w = i - r * cr;
+      const uint32_t e = sel_e[r];
+      const uint8_t* base = e == kSharedId ? p.sdown : p.down + size_t(e) * p.down_stride;
+      v[j] = reinterpret_cast<const u32x4*>(base + size_t(blockIdx.x) * tb)[w];
+    }
+  };
   const int mat = wave & 1;  // units (mat, c) = wave + 16 j: the matrix is the wave's parity
   for (int it = 0; t < ntiles; t += gridDim.x, ++it) {
     const int slot = t / tiles_i, tile = t - slot * tiles_i;
@@ -804,6 +823,7 @@ __global__ void __launch_bounds__(64 * WV) gate_up_runs_multi_kernel(DecodeArgs 
     xr.store(xs, tok_a, min(NT, int(sl.z - sl.y)));
     __syncthreads();
     if (t + int(gridDim.x) < ntiles) fetch(t + gridDim.x);
+    else if constexpr (kWarmPer > 0) warm_down();  // the last tile of this workgroup
     for (int c0 = int(sl.y); c0 < int(sl.z); c0 += NT) {
       const int nt = min(NT, int(sl.z) - c0);
       if (c0 != int(sl.y)) {  // a later chunk of a slot with more than NT tokens
@@ -859,6 +879,10 @@ __global__ void __launch_bounds__(64 * WV) gate_up_runs_multi_kernel(DecodeArgs 
       }
       // the next writes of part and xs come after a barrier these lanes reach
     }
+  }
+  if constexpr (kWarmPer > 0) {  // sink of the warm-up loads: the kernel ends after them
+#pragma unroll
+    for (int j = 0; j < kWarmPer; ++j) asm volatile("" : : "v"(v[j]));
   }
 }
 

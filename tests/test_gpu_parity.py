@@ -1045,14 +1045,15 @@ def test_layer_prefill_shared_expert_alone(cuda, switches, blas, key, T):
     _layer_parity(cuda, cfg, T, tokens=np.arange(0, T, 4))
 
 
-@pytest.mark.parametrize("key", ["c2", "c4", "small", "small_noshared"])
+@pytest.mark.parametrize("key", ["c2", "c4", "c1", "xs", "small", "small_noshared"])
 def test_layer_decode_warm_down_has_no_effect_on_results(cuda, switches, key):
     """The selecting gate/up launch warms L2 with the down launch's first
-    tiles through the LDS DMA into a KB of LDS nothing reads afterwards (the
-    shared down's area, or a KB of its own without a shared expert), under
-    its last routed tile: the outputs must be bitwise those of
+    tiles under its last routed tile (loads into its free tile registers,
+    never used): the outputs must be bitwise those of
     INFERNO_DECODE_WARM_DOWN=0, on c2 (Q2_K MFMA down), c4 layer 2 (Q3_K run
-    down) and a 1024-wide layer with and without a shared expert."""
+    down), c1 (Q4_K run gate/up and down), XS (the shared expert as rank k
+    of the Q6_K run down) and a 1024-wide layer with and without a shared
+    expert."""
     if key.startswith("small"):
         cfg = cf.Config("warm_" + key, 27, 1024, 16, 2048, 4, (cf.Q2_K,), cf.SCORE_SIGMOID,
                         True, 2.5, 0.1, 0 if key.endswith("noshared") else 256, torch.bfloat16, (1,))
@@ -1072,7 +1073,7 @@ def test_layer_decode_warm_down_has_no_effect_on_results(cuda, switches, key):
     for a, b in zip(got["1"], got["0"]):
         assert np.isfinite(a).all()
         assert np.array_equal(a, b)
-    if key != "c4":  # layer 0's launches; c4's layer 2 is checked by the c4 label tests
+    if key not in ("c4", "c1", "xs"):  # the fp8 x fp4 kernels (c4's layer 2: its label tests)
         labels, _ = _labels_of_one_step(cfg, cuda)
         assert labels[ops.TIMER_GATE_UP].startswith("mfma+select:")
 
