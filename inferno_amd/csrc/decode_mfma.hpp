@@ -84,6 +84,23 @@ struct LdsCopy {
 typedef uint32_t u32_a2 __attribute__((aligned(2)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 
+// N words at an LDS address that is only 2-byte aligned (Q3_K and Q6_K
+// blocks, 110 and 210 bytes, start at 2 mod 4 every other block): N + 1
+// aligned word reads and N byte-aligns. The word at p - (p & 3) + 4 N may lie
+// past the block (never past the LDS allocation: a later block, row or
+// region follows); its bytes are shifted out.
+template <int N>
+__device__ __forceinline__ void lds_words_a2(const uint8_t* p, uint32_t (&out)[N]) {
+  const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p)) & 3u;
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(p - sh);
+  uint32_t d[N + 1];
+#pragma unroll
+  for (int i = 0; i <= N; ++i) d[i] = w[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
+}
+
+
 constexpr int kWaves = 16;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kQ2Bytes = 84;
@@ -483,8 +500,10 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
         const uint32_t F = 0x33333333u;
         floatx4 C0 = {0.f, 0.f, 0.f, 0.f}, C1 = C0;
         if constexpr (Q == INFERNO_Q3_K) {
-          const u32x4_a2 qs = *reinterpret_cast<const u32x4_a2*>(blk + 32 + 16 * q);
-          const u32x4_a2 hm = *reinterpret_cast<const u32x4_a2*>(blk + 16 * (q & 1));
+          uint32_t qw[4], hw[4];
+          lds_words_a2(blk + 32 + 16 * q, qw);
+          lds_words_a2(blk + 16 * (q & 1), hw);
+          const u32x4 qs = {qw[0], qw[1], qw[2], qw[3]}, hm = {hw[0], hw[1], hw[2], hw[3]};
           const v8i B0 = v8i{int(qs.x & F), int(qs.y & F), int(qs.z & F), int(qs.w & F), 0, 0, 0, 0};
           const v8i B1 = v8i{int((qs.x >> 2) & F), int((qs.y >> 2) & F), int((qs.z >> 2) & F),
                              int((qs.w >> 2) & F), 0, 0, 0, 0};
@@ -506,9 +525,9 @@ __global__ void __launch_bounds__(kThreads) gate_up_fp4_kernel(DecodeArgs p, int
           C1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A[1], H1, C1, 0, 4, 0, sa + 2, 0, 127);
           // group 8 hq + k: 6-bit scale = nibble hq of scales[k] | bits
           // 2 (2 hq + k / 4) .. + 1 of scales[8 + k % 4] at bit 4
-          const uint32_t l0 = *reinterpret_cast<const u32_a2*>(blk + 96);
-          const uint32_t l1 = *reinterpret_cast<const u32_a2*>(blk + 100);
-          const uint32_t hb = *reinterpret_cast<const u32_a2*>(blk + 104);
+          uint32_t sc[3];
+          lds_words_a2(blk + 96, sc);
+          const uint32_t l0 = sc[0], l1 = sc[1], hb = sc[2];
           const uint32_t s6a = ((l0 >> (4 * hq)) & 0x0f0f0f0fu) | (((hb >> (4 * hq)) & 0x03030303u) << 4);
           const uint32_t s6b = ((l1 >> (4 * hq)) & 0x0f0f0f0fu) | (((hb >> (4 * hq + 2)) & 0x03030303u) << 4);
           const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 108));

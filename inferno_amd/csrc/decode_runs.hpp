@@ -39,6 +39,7 @@ using mfma_decode::as_h2;
 using mfma_decode::floatx4;
 using mfma_decode::half8;
 using mfma_decode::u32x4;
+using mfma_decode::lds_words_a2;
 typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
 typedef uint32_t u32_a2 __attribute__((aligned(2)));
 
@@ -129,15 +130,16 @@ struct RF<INFERNO_Q3_K> {
                              const uint32_t* zero, int n, int q, floatx4 (&C)[NA]) {
     const bool act = q == 2 * (n >> 3) + (n & 1);
     const int pm = (n >> 1) & 3;
-    const u32x4_a2 qs = *reinterpret_cast<const u32x4_a2*>(blk + 32 + 16 * q);
-    const u32x4_a2 hm = *reinterpret_cast<const u32x4_a2*>(blk + 16 * (q & 1));
+    uint32_t qs[4], hm[4];
+    lds_words_a2(blk + 32 + 16 * q, qs);
+    lds_words_a2(blk + 16 * (q & 1), hm);
     // lane group q = 2 h + s needs bit 4 h + pp of each hmask byte: shifted
     // down by 4 h once, bit pp of every byte is that bit
     const int hsh = 4 * (q >> 1);
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      const uint32_t w0 = hf ? qs.z : qs.x, w1 = hf ? qs.w : qs.y;
-      const uint32_t x0 = (hf ? hm.z : hm.x) >> hsh, x1 = (hf ? hm.w : hm.y) >> hsh;
+      const uint32_t w0 = qs[2 * hf], w1 = qs[2 * hf + 1];
+      const uint32_t x0 = hm[2 * hf] >> hsh, x1 = hm[2 * hf + 1] >> hsh;
       const uint32_t o0 = w0 >> 8, o1 = w1 >> 8;
 #pragma unroll
       for (int pp = 0; pp < 4; ++pp) {
@@ -160,8 +162,10 @@ struct RF<INFERNO_Q3_K> {
                                    int q) {
     // groups 4 q + j: low nibble of scales[(4 q + j) % 8] (high nibble for
     // q >= 2), high two bits of scales[8 + j] at bit 2 q
-    const uint32_t lo = *reinterpret_cast<const u32_a2*>(blk + 96 + 4 * (q & 1));
-    const uint32_t hi = *reinterpret_cast<const u32_a2*>(blk + 104);
+    uint32_t lw[1], hw[1];
+    lds_words_a2(blk + 96 + 4 * (q & 1), lw);
+    lds_words_a2(blk + 104, hw);
+    const uint32_t lo = lw[0], hi = hw[0];
     const uint32_t s6 = ((lo >> (4 * (q >> 1))) & 0x0f0f0f0fu) | (((hi >> (2 * q)) & 0x03030303u) << 4);
     const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 108));
     const float c[4] = {C[0], C[1], C[2], C[3]};
@@ -266,17 +270,18 @@ struct RF<INFERNO_Q6_K> {
   template <int NA>
   __device__ static void dot(const uint8_t* blk, const uint32_t* const (&cols)[NA],
                              const uint32_t* zero, int n, int q, floatx4 (&C)[NA]) {
-    typedef uint32_t u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
     const bool act_q = (q >> 1) == (n & 1);
     const int mh = n >> 3, mu = (n >> 1) & 3;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const u32x2_a2 l0 = *reinterpret_cast<const u32x2_a2*>(blk + 64 * h + 8 * q);
-      const u32x2_a2 l1 = *reinterpret_cast<const u32x2_a2*>(blk + 64 * h + 32 + 8 * q);
-      const u32x2_a2 hq = *reinterpret_cast<const u32x2_a2*>(blk + 128 + 32 * h + 8 * q);
+      uint32_t l0[2], l1[2], hw[2];
+      lds_words_a2(blk + 64 * h + 8 * q, l0);
+      lds_words_a2(blk + 64 * h + 32 + 8 * q, l1);
+      lds_words_a2(blk + 128 + 32 * h + 8 * q, hw);
+      const uint2 hq = make_uint2(hw[0], hw[1]);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const uint32_t w0 = (u & 1) ? l1.x : l0.x, w1 = (u & 1) ? l1.y : l0.y;
+        const uint32_t w0 = (u & 1) ? l1[0] : l0[0], w1 = (u & 1) ? l1[1] : l0[1];
         const int nb = 4 * (u >> 1);  // the field's bit offset
         const uint32_t M = 0x000f000fu << nb, MH = 0x00300030u << nb;
         // qh bits 2 u, 2 u + 1 of each byte moved to bits nb + 4, nb + 5
@@ -297,7 +302,9 @@ struct RF<INFERNO_Q6_K> {
   __device__ static float epilogue(const uint8_t* blk, floatx4 C, float4 sums, float4 kk,
                                    int q) {
     // runs 4 q + j: int8 scales at bytes 192 + 4 q + j
-    const uint32_t sw = *reinterpret_cast<const u32_a2*>(blk + 192 + 4 * q);
+    uint32_t sws[1];
+    lds_words_a2(blk + 192 + 4 * q, sws);
+    const uint32_t sw = sws[0];
     const float d = f16_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 208));
     const float c[4] = {C[0], C[1], C[2], C[3]};
     const float s[4] = {sums.x, sums.y, sums.z, sums.w};
